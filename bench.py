@@ -1,0 +1,382 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X Gated DeltaNet hot path (one GPU).
+
+A "step" is one batched decode update of one GDN layer at B=64, T=1
+(Hk=16, Hv=32, Dk=Dv=128): the state of every row is read, advanced by one
+token and written back in place, and the next step reads it again (state
+carried across back-to-back steps, inputs redrawn per step).  ``value`` is
+the algorithmic state+I/O bytes per step over the measured step time (GB/s);
+the JSON line also carries the other workloads of the path measured in the
+same run (decode B=1, MTP verify+commit, chunked prefill T=4096 with the
+fused conv prologue, and a mixed continuous-batching launch set), the
+roofline of the dominant kernel and a CPU baseline.
+
+Usage: python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--no-cpu]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import platform
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
+MFMA_BF16_PEAK_TFLOPS = 2516.6  # MI355X dense bf16 MFMA, TFLOP/s
+Hk, Hv, Dk, Dv, KT = 16, 32, 128, 128, 4
+C_DIM = 2 * Hk * Dk + Hv * Dv
+CHUNK = 64
+METRIC = "GDN decode state GB/s (% HBM peak) at B=64; chunked-prefill tokens/s"
+
+
+# ------------------------------------------------------------ work models
+
+def state_bytes(B):
+    return B * Hv * Dv * Dk * 4
+
+
+def io_bytes(B, T):
+    # q, k read; v read, y written (bf16); a, b read (bf16)
+    return B * T * (2 * Hk * Dk * 2 + 2 * Hv * Dv * 2 + 2 * Hv * 2)
+
+
+def decode_bytes(B, T=1):
+    """State read + written once, plus the per-token I/O."""
+    return 2 * state_bytes(B) + io_bytes(B, T)
+
+
+def chunk_flops(C=CHUNK):
+    """Algorithmic FLOPs per (chunk, head): KK^T, solve, W, U, 3 state products, QK^T, attn V."""
+    return 2 * C * C * Dk + (2.0 / 3.0) * C ** 3 + 2 * C * C * Dk + 2 * C * C * Dv + 6 * C * Dk * Dv \
+        + 2 * C * C * Dk + 2 * C * C * Dv
+
+
+def prefill_flops(lengths):
+    return sum(math.ceil(n / CHUNK) for n in lengths) * Hv * chunk_flops()
+
+
+# ----------------------------------------------------------------- inputs
+
+def draw(gen, B, T, torch, dev, state=True, dtype=None):
+    """Seeded inputs: q,k ~ N(0,1) L2-normalised per head (q also / sqrt(Dk)),
+    v ~ N(0,1), a, b ~ N(0,1), A_log ~ U(0, ln 16), dt_bias ~ U(-1, 1),
+    S0 ~ N(0, 0.02); drawn on the CPU, then copied to ``dev``."""
+    dtype = dtype or torch.bfloat16
+    q = torch.randn(B, T, Hk, Dk, generator=gen)
+    k = torch.randn(B, T, Hk, Dk, generator=gen)
+    q = q / q.norm(dim=-1, keepdim=True) / math.sqrt(Dk)
+    k = k / k.norm(dim=-1, keepdim=True)
+    d = dict(
+        q=q.to(dtype), k=k.to(dtype), v=torch.randn(B, T, Hv, Dv, generator=gen).to(dtype),
+        a=torch.randn(B, T, Hv, generator=gen).to(dtype), b=torch.randn(B, T, Hv, generator=gen).to(dtype),
+        A_log=torch.rand(Hv, generator=gen) * math.log(16.0), dt_bias=torch.rand(Hv, generator=gen) * 2 - 1,
+        state=(torch.randn(B, Hv, Dv, Dk, generator=gen) * 0.02) if state else None,
+    )
+    return {kk: (None if vv is None else vv.to(dev)) for kk, vv in d.items()}
+
+
+# ---------------------------------------------------------------- timing
+
+class Timer:
+    """HIP-event timing on torch's current stream (where every launch goes)."""
+
+    def __init__(self, torch):
+        self.torch = torch
+
+    def total_ms(self, fn, iters):
+        t = self.torch
+        t.cuda.synchronize()
+        s, e = t.cuda.Event(enable_timing=True), t.cuda.Event(enable_timing=True)
+        s.record()
+        for i in range(iters):
+            fn(i)
+        e.record()
+        t.cuda.synchronize()
+        return s.elapsed_time(e)
+
+    def per_launch_ms(self, fn, iters):
+        """Mean of event pairs placed tightly around each launch."""
+        t = self.torch
+        evs = [(t.cuda.Event(enable_timing=True), t.cuda.Event(enable_timing=True)) for _ in range(iters)]
+        t.cuda.synchronize()
+        for i, (s, e) in enumerate(evs):
+            s.record()
+            fn(i)
+            e.record()
+        t.cuda.synchronize()
+        ds = sorted(s.elapsed_time(e) for s, e in evs)
+        return sum(ds) / len(ds), ds[len(ds) // 2]
+
+
+def read_traffic(name):
+    """HBM bytes per launch from a committed rocprofv3 PMC summary, or None."""
+    p = ROOT / "profiles" / name
+    if not p.exists():
+        return None
+    vals = {}
+    for line in p.read_text().splitlines():
+        if "=" in line and line.split("=", 1)[0].strip() in ("fetch_bytes_per_launch", "write_bytes_per_launch"):
+            k, v = line.split("=", 1)
+            vals[k.strip()] = float(v.split()[0])
+    if len(vals) != 2:
+        return None
+    return vals["fetch_bytes_per_launch"] + vals["write_bytes_per_launch"]
+
+
+# ------------------------------------------------------------- workloads
+
+def bench_decode_b64(torch, mx, dev, steps, warmup, timer):
+    gen = torch.Generator().manual_seed(1001)
+    B = 64
+    n = max(steps, warmup, 1)
+    d = draw(gen, B, n, torch, dev)
+    # one contiguous [B,1,...] slab per step
+    per = {k: [d[k][:, s:s + 1].contiguous() for s in range(n)] for k in ("q", "k", "v", "a", "b")}
+    state = d["state"]
+    plans = [mx.prepare_recurrent(per["q"][s], per["k"][s], per["v"][s], per["a"][s], per["b"][s], d["A_log"],
+                                  d["dt_bias"], state, state_out=state) for s in range(n)]
+    for i in range(warmup):
+        plans[i % n].launch()
+    total = timer.total_ms(lambda i: plans[i % n].launch(), steps)
+    per_launch, median = timer.per_launch_ms(lambda i: plans[i % n].launch(), steps)
+    ok = bool(torch.isfinite(state).all())
+    return dict(ms_per_step=total / steps, kernel_ms=per_launch, kernel_ms_median=median, finite=ok)
+
+
+def bench_decode_b1(torch, mx, dev, timer, iters=200):
+    gen = torch.Generator().manual_seed(1000)
+    d = draw(gen, 1, 1, torch, dev)
+    plan = mx.prepare_recurrent(d["q"], d["k"], d["v"], d["a"], d["b"], d["A_log"], d["dt_bias"], d["state"],
+                                state_out=d["state"])
+    for _ in range(20):
+        plan.launch()
+    total = timer.total_ms(lambda i: plan.launch(), iters)
+    per, med = timer.per_launch_ms(lambda i: plan.launch(), iters)
+    return dict(us_per_step=1e3 * total / iters, kernel_us=1e3 * per, bytes=decode_bytes(1))
+
+
+def bench_verify(torch, mx, dev, timer, iters=50):
+    gen = torch.Generator().manual_seed(1002)
+    B, T = 32, 4
+    d = draw(gen, B, T, torch, dev)
+    n_b = torch.randint(1, T + 1, (B,), generator=gen, dtype=torch.int32).to(dev)
+    verify = mx.prepare_recurrent(d["q"], d["k"], d["v"], d["a"], d["b"], d["A_log"], d["dt_bias"], d["state"],
+                                  write_state=False)
+    commit = mx.prepare_recurrent(None, d["k"], d["v"], d["a"], d["b"], d["A_log"], d["dt_bias"], d["state"],
+                                  y=False, commit_len=n_b, state_out=torch.empty_like(d["state"]))
+    snap = mx.prepare_recurrent(d["q"], d["k"], d["v"], d["a"], d["b"], d["A_log"], d["dt_bias"], d["state"],
+                                write_state=False, snapshots=True)
+
+    def round_commit(i):
+        verify.launch()
+        commit.launch()
+
+    for _ in range(5):
+        round_commit(0)
+        snap.launch()
+    t_commit = timer.total_ms(round_commit, iters) / iters
+    t_verify, _ = timer.per_launch_ms(lambda i: verify.launch(), iters)
+    t_snap = timer.total_ms(lambda i: snap.launch(), iters) / iters
+    credited = 2 * state_bytes(B) + io_bytes(B, T)
+    return dict(ms_verify_plus_commit=t_commit, ms_verify=t_verify, ms_snapshot_verify=t_snap,
+                credited_bytes=credited, gbs=credited / (t_commit * 1e-3) / 1e9,
+                frac=credited / (t_commit * 1e-3) / 1e9 / HBM_PEAK_GBS)
+
+
+def bench_prefill(torch, mx, dev, timer, iters=10):
+    gen = torch.Generator().manual_seed(1003)
+    T = 4096
+    qkv = torch.randn(1, T, C_DIM, generator=gen).to(torch.bfloat16).to(dev)
+    w = (torch.randn(C_DIM, KT, generator=gen) * 0.1).to(torch.bfloat16).to(dev)
+    cs = torch.zeros(1, KT - 1, C_DIM, dtype=torch.bfloat16, device=dev)
+    a = torch.randn(1, T, Hv, generator=gen).to(torch.bfloat16).to(dev)
+    b = torch.randn(1, T, Hv, generator=gen).to(torch.bfloat16).to(dev)
+    A_log = (torch.rand(Hv, generator=gen) * math.log(16.0)).to(dev)
+    dt_bias = (torch.rand(Hv, generator=gen) * 2 - 1).to(dev)
+    ws = torch.empty(mx.chunk_workspace_bytes(1, T, Hv, Dk, Dv), dtype=torch.uint8, device=dev)
+    out = {}
+
+    def step(i):
+        q, k, v, _ = mx.gdn_conv_prologue(qkv, w, Hk, Hv, Dk, Dv, cs)
+        out["y"], out["S"] = mx.gated_delta_update(q, k, v, a, b, A_log, dt_bias, None, chunked=True, workspace=ws)
+
+    q, k, v, _ = mx.gdn_conv_prologue(qkv, w, Hk, Hv, Dk, Dv, cs)
+
+    def gdn_only(i):
+        mx.gated_delta_update(q, k, v, a, b, A_log, dt_bias, None, chunked=True, workspace=ws)
+
+    def pro_only(i):
+        mx.gdn_conv_prologue(qkv, w, Hk, Hv, Dk, Dv, cs)
+
+    for _ in range(3):
+        step(0)
+    t_all = timer.total_ms(step, iters) / iters
+    t_gdn = timer.total_ms(gdn_only, iters) / iters
+    t_pro = timer.total_ms(pro_only, iters) / iters
+    flops = prefill_flops([T])
+    return dict(ms_total=t_all, ms_gdn=t_gdn, ms_prologue=t_pro, tokens_per_s=T / (t_all * 1e-3),
+                gdn_tflops=flops / (t_gdn * 1e-3) / 1e12, mfma_frac=flops / (t_gdn * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS,
+                flops=flops, finite=bool(torch.isfinite(out["S"]).all()))
+
+
+def bench_mixed(torch, mx, dev, timer, iters=10):
+    gen = torch.Generator().manual_seed(1004)
+    lens = [1024, 2560, 7168]
+    n_tok = sum(lens)
+    cu = torch.tensor([0] + [sum(lens[:i + 1]) for i in range(3)], dtype=torch.int32)
+    pf = draw(gen, 1, n_tok, torch, dev, state=False)
+    pf_state = (torch.randn(3, Hv, Dv, Dk, generator=gen) * 0.02).to(dev)
+    dec = draw(gen, 48, 1, torch, dev)
+    ver = draw(gen, 16, 4, torch, dev)
+    n_b = torch.randint(1, 5, (16,), generator=gen, dtype=torch.int32).to(dev)
+    ws = torch.empty(mx.chunk_workspace_bytes(3, n_tok, Hv, Dk, Dv), dtype=torch.uint8, device=dev)
+    dplan = mx.prepare_recurrent(dec["q"], dec["k"], dec["v"], dec["a"], dec["b"], dec["A_log"], dec["dt_bias"],
+                                 dec["state"], state_out=dec["state"])
+    vplan = mx.prepare_recurrent(ver["q"], ver["k"], ver["v"], ver["a"], ver["b"], ver["A_log"], ver["dt_bias"],
+                                 ver["state"], write_state=False)
+    cplan = mx.prepare_recurrent(None, ver["k"], ver["v"], ver["a"], ver["b"], ver["A_log"], ver["dt_bias"],
+                                 ver["state"], y=False, commit_len=n_b, state_out=torch.empty_like(ver["state"]))
+    st_out = torch.empty_like(pf_state)
+
+    def step(i):
+        mx.gated_delta_update(pf["q"], pf["k"], pf["v"], pf["a"], pf["b"], pf["A_log"], pf["dt_bias"], pf_state,
+                              cu_seqlens=cu, chunked=True, workspace=ws, state_out=st_out)
+        dplan.launch()
+        vplan.launch()
+        cplan.launch()
+
+    for _ in range(3):
+        step(0)
+    t = timer.total_ms(step, iters) / iters
+    flops = prefill_flops(lens)
+    hbm = decode_bytes(48) + 2 * state_bytes(16) + io_bytes(16, 4)
+    toks = n_tok + 48 + 64
+    return dict(ms=t, tokens_per_s=toks / (t * 1e-3), prefill_gflop=flops / 1e9, decode_verify_bytes=hbm)
+
+
+# ------------------------------------------------------------ CPU baseline
+
+def cpu_baseline(torch, budget_s=12.0):
+    """The reference's ops path (fp32 port, oracle/ops_path.py) on host cores.
+
+    Bounded sample: decode steps at B=64 until ``budget_s`` seconds have
+    passed (at least 2), reported as algorithmic GB/s like ``value``; plus one
+    512-token prefill chunk (the reference's chunk size) for tokens/s.
+    """
+    sys.path.insert(0, str(ROOT))
+    from oracle import ops_path
+
+    threads = max(1, min(16, os.cpu_count() or 1))
+    torch.set_num_threads(threads)
+    gen = torch.Generator().manual_seed(1001)
+    d = draw(gen, 64, 1, torch, "cpu")
+    S = d["state"].float()
+    done, t0 = 0, time.perf_counter()
+    while done < 2 or (time.perf_counter() - t0 < budget_s and done < 50):
+        _, S = ops_path.gated_delta_update(d["q"], d["k"], d["v"], d["a"], d["b"], d["A_log"], d["dt_bias"], S)
+        done += 1
+    dt = (time.perf_counter() - t0) / done
+    gen = torch.Generator().manual_seed(1003)
+    T = 512
+    qkv = torch.randn(1, T, C_DIM, generator=gen).to(torch.bfloat16)
+    w = (torch.randn(C_DIM, KT, generator=gen) * 0.1).to(torch.bfloat16)
+    a = torch.randn(1, T, Hv, generator=gen).to(torch.bfloat16)
+    b = torch.randn(1, T, Hv, generator=gen).to(torch.bfloat16)
+    A_log = torch.rand(Hv, generator=gen) * math.log(16.0)
+    dt_bias = torch.rand(Hv, generator=gen) * 2 - 1
+    t1 = time.perf_counter()
+    q, k, v, _ = ops_path.conv_prologue(qkv, w, Hk, Hv, Dk, Dv, torch.zeros(1, KT - 1, C_DIM))
+    ops_path.gated_delta_update(q, k, v, a, b, A_log, dt_bias, torch.zeros(1, Hv, Dv, Dk))
+    tp = time.perf_counter() - t1
+    return dict(value=decode_bytes(64) / dt / 1e9, unit="GB/s", cores=threads, kind="port",
+                sample=f"{done} decode steps at B=64 (ops-path port, fp32, torch CPU), "
+                       f"{dt * 1e3:.1f} ms/step; prefill 512 tokens with conv prologue: {T / tp:.0f} tokens/s",
+                ms_per_step=dt * 1e3, prefill_tokens_per_s=T / tp,
+                cpu=platform.processor() or platform.machine())
+
+
+# ------------------------------------------------------------------- main
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--decode-only", action="store_true", help="only the B=64 decode workload")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures one GPU: this build's path runs on a single MI355X "
+              "(multi-GPU sharding is design-only); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+    if args.steps < 1:
+        print("--steps must be >= 1", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    sys.path.insert(0, str(ROOT))
+    import multiplex_amd as mx
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        sys.exit(1)
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    timer = Timer(torch)
+
+    dec = bench_decode_b64(torch, mx, dev, args.steps, args.warmup, timer)
+    step_bytes = decode_bytes(64)
+    value = step_bytes / (dec["ms_per_step"] * 1e-3) / 1e9
+    achieved = step_bytes / (dec["kernel_ms"] * 1e-3) / 1e9
+    configs = {}
+    if not args.decode_only:
+        configs["decode_b1"] = bench_decode_b1(torch, mx, dev, timer)
+        configs["verify_b32_t4"] = bench_verify(torch, mx, dev, timer)
+        configs["prefill_t4096"] = bench_prefill(torch, mx, dev, timer)
+        configs["mixed"] = bench_mixed(torch, mx, dev, timer)
+    base = None if args.no_cpu else cpu_baseline(torch)
+
+    line = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(dec["ms_per_step"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {
+            "workload": "GDN decode B=64 T=1 Hk=16 Hv=32 Dk=Dv=128, fp32 state carried in place over back-to-back steps",
+            "B": 64, "T": 1, "Hk": Hk, "Hv": Hv, "Dk": Dk, "Dv": Dv, "io_dtype": "bf16",
+            "bytes_per_step": step_bytes, "hbm_frac": round(value / HBM_PEAK_GBS, 4),
+        },
+        "roofline": {
+            "bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": read_traffic("decode_b64_traffic.txt"),
+            "kernel": "recurrent_kernel<128,bf16>", "kernel_ms": round(dec["kernel_ms"], 5),
+        },
+        "cpu_baseline": None if base is None else {k: base[k] for k in ("value", "unit", "cores", "kind", "sample")},
+        "prefill": None,
+        "configs": configs,
+    }
+    if "prefill_t4096" in configs:
+        p = configs["prefill_t4096"]
+        line["prefill"] = {"tokens_per_s": round(p["tokens_per_s"], 1), "ms": round(p["ms_total"], 4),
+                           "gdn_ms": round(p["ms_gdn"], 4), "mfma_frac": round(p["mfma_frac"], 4),
+                           "cpu_tokens_per_s": None if base is None else round(base["prefill_tokens_per_s"], 1)}
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,187 @@
+/*
+ * gdn.h -- C ABI of libgdn.so, the MI355X (gfx950) Gated DeltaNet hot path.
+ *
+ * Every entry point takes plain device pointers and sizes, enqueues work on
+ * the given HIP stream (a hipStream_t passed as void*, NULL = default
+ * stream) and returns immediately.  Nothing here allocates device memory or
+ * synchronises: the caller owns every buffer, including workspaces, and the
+ * pointers are borrowed only for the enqueue.
+ *
+ * Return value: GDN_OK (0) or a negative status.  Argument errors are
+ * detected before any HIP call, so they are reported identically with or
+ * without a GPU.  gdn_last_error() gives a message for the calling thread.
+ *
+ * Layouts (row-major, contiguous, batch-major with heads before head dim,
+ * as mlx-lm lays them out):
+ *   q, k   [B, T, Hk, Dk]          v, y   [B, T, Hv, Dv]
+ *   a, b, g, beta  [B, T, Hv]      A_log, dt_bias  [Hv]
+ *   state  [B, Hv, Dv, Dk] fp32 (Dk innermost)     mask  [B, T] uint8 (0/1)
+ * Packed ragged sequences (cu_seqlens != NULL): B is the number of
+ * sequences, tensors are [1, N_tok, ...] and sequence n owns tokens
+ * [cu_seqlens[n], cu_seqlens[n+1]); state rows are per sequence.
+ * GQA: v-head h reads q/k head h / (Hv / Hk).
+ *
+ * Recurrence per (sequence, v-head), S in R^{Dv x Dk}:
+ *   g = exp(-exp(A_log) * softplus(a + dt_bias)),  beta = sigmoid(b)
+ *   S <- g S;  kv = S k;  S <- S + beta (v - kv) k^T;  y = S q
+ * A token whose mask byte is 0 leaves S unchanged and gets y = 0.
+ */
+#ifndef GDN_H
+#define GDN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define GDN_ABI_VERSION 1
+
+/* dtype codes for the void* operands */
+#define GDN_DTYPE_F32 0
+#define GDN_DTYPE_BF16 1
+#define GDN_DTYPE_F16 2
+
+/* gate modes of gdn_recurrent_args.gate_mode / gdn_chunk_fwd */
+#define GDN_GATES_RAW 0 /* gx = a, gy = b, with A_log and dt_bias   */
+#define GDN_GATES_PRE 1 /* gx = g, gy = beta (already transformed)  */
+
+/* status codes */
+#define GDN_OK 0
+#define GDN_ERR_LAUNCH (-5)       /* a HIP call failed               */
+#define GDN_ERR_INVALID (-22)     /* bad pointer / shape / dtype      */
+#define GDN_ERR_UNSUPPORTED (-95) /* valid but not built (e.g. Dk)    */
+
+/* Version of this ABI (GDN_ABI_VERSION of the built library). */
+int gdn_abi_version(void);
+
+/* Message for the last failing call on this thread ("" if none). */
+const char* gdn_last_error(void);
+
+/*
+ * mlx-lm gated_delta_update(q, k, v, a, b, A_log, dt_bias, state, mask):
+ * replaces the fused entry point multiplex calls at
+ * multiplex/kernel/dflash.py:372-374 and :417-422 (reached from
+ * multiplex/kernel/engine.py:164-167).  The gate transforms are fused.
+ * state_in NULL = zero state; mask NULL = all tokens active.  y and
+ * state_out are written (state_out may alias state_in for in-place use).
+ */
+int gdn_gated_delta_update(const void* q, const void* k, const void* v, int qkv_dtype,
+                           const void* a, const void* b, int ab_dtype,
+                           const void* A_log, const void* dt_bias, int param_dtype,
+                           const float* state_in, const uint8_t* mask,
+                           void* y, float* state_out,
+                           int64_t B, int64_t T, int64_t Hk, int64_t Hv,
+                           int64_t Dk, int64_t Dv, void* stream);
+
+/*
+ * mlx-lm gated_delta_kernel(q, k, v, g, beta, state, mask): the same
+ * recurrence with the decay g and write strength beta precomputed
+ * (mlx-lm dispatches to it from gated_delta_update, dflash.py:373).
+ */
+int gdn_gated_delta_kernel(const void* q, const void* k, const void* v, int qkv_dtype,
+                           const void* g, const void* beta, int gb_dtype,
+                           const float* state_in, const uint8_t* mask,
+                           void* y, float* state_out,
+                           int64_t B, int64_t T, int64_t Hk, int64_t Hv,
+                           int64_t Dk, int64_t Dv, void* stream);
+
+/*
+ * General recurrent launch (decode, MTP verify, commit, ragged rows).
+ * Replaces the verify forward plus the replay rollback of
+ * multiplex/kernel/engine.py:337-359 and dflash.py:403-426.
+ *   state_out  NULL: the state is not written (verify without commit).
+ *   snapshots  [B,T,Hv,Dv,Dk] fp32 (or [N_tok,...] packed): the state after
+ *              every token (for rollback by index), NULL = none.
+ *   y          NULL: outputs not computed (commit-only launch).
+ *   commit_len [B] int32: row b writes the state after its first
+ *              commit_len[b] tokens (0 = initial state, < 0 = no write,
+ *              > length = clamped); NULL = after all tokens.
+ * Rows run independently; a launch never reads another row's state.
+ */
+typedef struct gdn_recurrent_args {
+  const void* q;
+  const void* k;
+  const void* v;
+  int32_t qkv_dtype;
+  int32_t gate_mode;   /* GDN_GATES_RAW / GDN_GATES_PRE */
+  const void* gx;      /* a or g      [B,T,Hv] */
+  const void* gy;      /* b or beta   [B,T,Hv] */
+  int32_t gate_dtype;
+  int32_t param_dtype; /* A_log / dt_bias (raw mode only) */
+  const void* A_log;
+  const void* dt_bias;
+  const float* state_in;
+  float* state_out;
+  float* snapshots;
+  void* y;
+  const uint8_t* mask;
+  const int32_t* cu_seqlens; /* [B+1] or NULL */
+  const int32_t* commit_len; /* [B] or NULL */
+  int64_t B, T;              /* T = tokens per row, or N_tok when packed */
+  int64_t Hk, Hv, Dk, Dv;
+  void* stream;
+} gdn_recurrent_args;
+
+int gdn_recurrent(const gdn_recurrent_args* args);
+
+/*
+ * Chunked (WY/UT) prefill of packed ragged sequences on bf16 MFMA; the
+ * long-T form of gdn_gated_delta_update (the reference runs prefill chunks
+ * of 512 tokens through the sequential kernel, multiplex/kernel/
+ * scheduler.py:331-333 -> engine.py:261-269).  q/k/v must be bf16.
+ * cu_seqlens [n_seqs+1] (NULL: n_seqs rows of n_tok/n_seqs tokens each,
+ * [B,T,...] layout).  state_in [n_seqs,Hv,Dv,Dk] fp32 or NULL (zeros),
+ * state_out may alias state_in.  No mask.  chunk must be 64.
+ * workspace must hold gdn_chunk_workspace_bytes(...) bytes (256-B aligned).
+ */
+size_t gdn_chunk_workspace_bytes(int64_t n_seqs, int64_t n_tok, int64_t Hv,
+                                 int64_t Dk, int64_t Dv, int64_t chunk);
+
+int gdn_chunk_fwd(const void* q, const void* k, const void* v, int qkv_dtype,
+                  int gate_mode, const void* gx, const void* gy, int gate_dtype,
+                  const void* A_log, const void* dt_bias, int param_dtype,
+                  const float* state_in, void* y, float* state_out,
+                  const int32_t* cu_seqlens, int64_t n_seqs, int64_t n_tok,
+                  int64_t Hk, int64_t Hv, int64_t Dk, int64_t Dv, int64_t chunk,
+                  void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Fused mixer prologue of GatedDeltaNet (dflash.py:351-370): mask zeroing,
+ * concat(conv_state, qkv), depthwise causal conv1d with Kt taps (no bias),
+ * SiLU, split into q | k | v, q = rms_norm(q)/Dk, k = rms_norm(k)/sqrt(Dk)
+ * (rms_norm(x) = x / sqrt(mean(x^2) + eps)), and the new conv state
+ * (last Kt-1 rows of the concat).
+ *   qkv            [B,S,C] with C = 2*Hk*Dk + Hv*Dv, io_dtype
+ *   conv_state_in  [B,Kt-1,C] io_dtype or NULL (zeros)
+ *   weight         [C,Kt] w_dtype (mlx-lm's [C,Kt,1] squeezed)
+ *   mask           [B,S] uint8 or NULL
+ *   q_out, k_out   [B,S,Hk,Dk];  v_out [B,S,Hv,Dv]   (io_dtype)
+ *   conv_state_out [B,Kt-1,C] or NULL; must not alias conv_state_in
+ * cu_seqlens: packed sequences as in gdn_chunk_fwd (B = n_seqs, S = n_tok).
+ * Requires Dk == Dv in {64, 128, 256}.
+ */
+int gdn_conv_prologue(const void* qkv, int io_dtype, const void* conv_state_in,
+                      const void* weight, int w_dtype, const uint8_t* mask,
+                      const int32_t* cu_seqlens,
+                      void* q_out, void* k_out, void* v_out, void* conv_state_out,
+                      int64_t B, int64_t S, int64_t Hk, int64_t Hv, int64_t Dk,
+                      int64_t Dv, int64_t Kt, float eps, void* stream);
+
+/*
+ * Conv-state commit of a partially accepted verify (dflash.py:424-425):
+ * conv_state_out[b] = concat(conv_state_in[b], masked qkv[b])[n : n+Kt-1]
+ * with n = n_commit[b] in [0, T].  conv_state_out must not alias
+ * conv_state_in.
+ */
+int gdn_conv_state_commit(const void* conv_state_in, const void* qkv, int io_dtype,
+                          const uint8_t* mask, const int32_t* n_commit,
+                          void* conv_state_out, int64_t B, int64_t T, int64_t C,
+                          int64_t Kt, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GDN_H */

@@ -1,0 +1,36 @@
+"""multiplex_amd: MI355X-native Gated DeltaNet hot path of wang1ang/multiplex.
+
+The public functions mirror mlx-lm's ``mlx_lm.models.gated_delta`` module
+(which multiplex calls from ``multiplex/kernel/dflash.py:372-374``) on
+PyTorch-ROCm tensors, backed by hand-written gfx950 HIP kernels in
+``libgdn.so`` (C ABI: ``include/gdn.h``).
+"""
+
+from .gated_delta import (
+    CHUNK_MIN_TOKENS,
+    chunk_workspace_bytes,
+    compute_beta,
+    compute_g,
+    gated_delta_commit,
+    gated_delta_kernel,
+    gated_delta_ops,
+    gated_delta_update,
+    gated_delta_verify,
+    prepare_recurrent,
+)
+from .conv import conv_state_commit, gdn_conv_prologue
+
+__all__ = [
+    "CHUNK_MIN_TOKENS",
+    "chunk_workspace_bytes",
+    "compute_beta",
+    "compute_g",
+    "conv_state_commit",
+    "gated_delta_commit",
+    "gated_delta_kernel",
+    "gated_delta_ops",
+    "gated_delta_update",
+    "gated_delta_verify",
+    "gdn_conv_prologue",
+    "prepare_recurrent",
+]

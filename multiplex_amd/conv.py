@@ -1,0 +1,107 @@
+"""Fused GatedDeltaNet prologue on MI355X (``libgdn.so`` ``gdn_conv_prologue``).
+
+Replaces the prologue of the mixer that multiplex restates at
+``multiplex/kernel/dflash.py:351-370``: mask zeroing of the mixed qkv
+projection, ``concat(conv_state, qkv)``, depthwise causal conv1d (4 taps, no
+bias) + SiLU, the q | k | v split, ``q = rms_norm(q) / Dk`` and
+``k = rms_norm(k) / sqrt(Dk)``, and the conv-state update -- in one launch
+that reads each input element once.
+"""
+
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+
+from . import _lib
+from .gated_delta import IntSeq, _contig, _cu_seqlens, _dtype_code, _int_rows, _mask_u8, _ptr, _require_device, _stream
+
+__all__ = ["gdn_conv_prologue", "conv_state_commit"]
+
+
+def _weight_2d(conv_weight: torch.Tensor, C: int) -> torch.Tensor:
+    """Accepts mlx-lm's ``[C, K, 1]``, torch's ``[C, 1, K]`` or plain ``[C, K]`` taps."""
+    w = conv_weight
+    if w.dim() == 3:
+        if w.shape[2] == 1:
+            w = w[:, :, 0]
+        elif w.shape[1] == 1:
+            w = w[:, 0, :]
+        else:
+            raise ValueError(f"conv weight of shape {tuple(conv_weight.shape)} is not depthwise")
+    if w.dim() != 2 or w.shape[0] != C:
+        raise ValueError(f"conv weight must be [C={C}, K] (got {tuple(conv_weight.shape)})")
+    return w.contiguous()
+
+
+def gdn_conv_prologue(qkv: torch.Tensor, conv_weight: torch.Tensor, num_k_heads: int,
+                      num_v_heads: int, head_k_dim: int, head_v_dim: int,
+                      conv_state: Optional[torch.Tensor] = None, mask: Optional[torch.Tensor] = None,
+                      *, cu_seqlens: Optional[IntSeq] = None, eps: float = 1e-6,
+                      write_conv_state: bool = True):
+    """Returns ``(q, k, v, new_conv_state)``.
+
+    qkv ``[B,S,C]`` (C = 2*Hk*Dk + Hv*Dv, channels q | k | v), conv_weight
+    ``[C,K]`` (or ``[C,K,1]`` / ``[C,1,K]``), conv_state ``[B,K-1,C]`` or None
+    (zeros), mask ``[B,S]`` or None.  q, k are ``[B,S,Hk,Dk]``, v is
+    ``[B,S,Hv,Dv]``, all in qkv's dtype; the new conv state is the last K-1
+    rows of ``concat(conv_state, masked qkv)`` (None if not requested).
+    With ``cu_seqlens`` the rows are packed ragged sequences (``B == 1``) and
+    conv_state has one row per sequence.
+    """
+    dev = _require_device([qkv, conv_weight, conv_state, mask], ["qkv", "conv_weight", "conv_state", "mask"])
+    if qkv.dim() != 3:
+        raise ValueError("qkv must be [B, S, C]")
+    B, S, C = qkv.shape
+    Hk, Hv, Dk, Dv = int(num_k_heads), int(num_v_heads), int(head_k_dim), int(head_v_dim)
+    if C != 2 * Hk * Dk + Hv * Dv:
+        raise ValueError(f"qkv has {C} channels, expected 2*{Hk}*{Dk} + {Hv}*{Dv}")
+    w = _weight_2d(conv_weight, C)
+    Kt = w.shape[1]
+    io = _dtype_code(qkv, "qkv")
+    wdt = _dtype_code(w, "conv_weight")
+    cu = _cu_seqlens(cu_seqlens, S, dev) if cu_seqlens is not None else None
+    if cu is not None and B != 1:
+        raise ValueError("packed sequences need qkv of shape [1, N_tok, C]")
+    n_rows = (cu.numel() - 1) if cu is not None else B
+    if conv_state is not None:
+        if tuple(conv_state.shape) != (n_rows, Kt - 1, C) or conv_state.dtype != qkv.dtype:
+            raise ValueError(f"conv_state must be {(n_rows, Kt - 1, C)} of dtype {qkv.dtype}")
+        conv_state = conv_state.contiguous()
+    m = _mask_u8(mask, (B, S))
+    qkv = _contig(qkv)
+    q = torch.empty(B, S, Hk, Dk, dtype=qkv.dtype, device=dev)
+    k = torch.empty(B, S, Hk, Dk, dtype=qkv.dtype, device=dev)
+    v = torch.empty(B, S, Hv, Dv, dtype=qkv.dtype, device=dev)
+    cs_out = torch.empty(n_rows, Kt - 1, C, dtype=qkv.dtype, device=dev) if write_conv_state else None
+    with torch.cuda.device(dev):
+        _lib.call("gdn_conv_prologue", _ptr(qkv), io, _ptr(conv_state), _ptr(w), wdt, _ptr(m), _ptr(cu),
+                  _ptr(q), _ptr(k), _ptr(v), _ptr(cs_out), n_rows, S, Hk, Hv, Dk, Dv, Kt, float(eps),
+                  _stream(dev))
+    return q, k, v, cs_out
+
+
+def conv_state_commit(conv_state: Optional[torch.Tensor], qkv: torch.Tensor, n_commit: IntSeq,
+                      mask: Optional[torch.Tensor] = None, kernel_size: int = 4) -> torch.Tensor:
+    """Conv state after the accepted prefix of a verify (``dflash.py:424-425``).
+
+    ``new[b] = concat(conv_state[b], masked qkv[b])[n : n + K - 1]`` with
+    ``n = n_commit[b]``.  qkv ``[B,T,C]`` is the verify's mixed projection.
+    """
+    dev = _require_device([conv_state, qkv, mask], ["conv_state", "qkv", "mask"])
+    B, T, C = qkv.shape
+    Kt = int(kernel_size)
+    if conv_state is not None:
+        if tuple(conv_state.shape) != (B, Kt - 1, C) or conv_state.dtype != qkv.dtype:
+            raise ValueError(f"conv_state must be {(B, Kt - 1, C)} of dtype {qkv.dtype}")
+        conv_state = conv_state.contiguous()
+    io = _dtype_code(qkv, "qkv")
+    n = _int_rows(n_commit, B, dev, "n_commit")
+    m = _mask_u8(mask, (B, T))
+    out = torch.empty(B, Kt - 1, C, dtype=qkv.dtype, device=dev)
+    qkv = _contig(qkv)
+    with torch.cuda.device(dev):
+        _lib.call("gdn_conv_state_commit", _ptr(conv_state), _ptr(qkv), io, _ptr(m), _ptr(n), _ptr(out),
+                  B, T, C, Kt, _stream(dev))
+    return out

@@ -1,0 +1,218 @@
+// Shared device helpers and host-side status handling for libgdn (gfx950).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstdio>
+#include <string>
+
+#include "../../include/gdn.h"
+
+namespace gdn {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
+typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
+
+// ---------------------------------------------------------------- dtypes
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) {
+  return __uint_as_float(static_cast<uint32_t>(h) << 16);
+}
+
+// Round-to-nearest-even fp32 -> bf16 (NaN stays NaN).
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+__device__ __forceinline__ float f16_to_f32(uint16_t h) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, h));
+}
+
+__device__ __forceinline__ uint16_t f32_to_f16(float f) {
+  return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
+}
+
+// Scalar load of a runtime-typed element (gates, per-head parameters).
+__device__ __forceinline__ float load_any(const void* p, int dt, int64_t i) {
+  if (dt == GDN_DTYPE_F32) return static_cast<const float*>(p)[i];
+  const uint16_t h = static_cast<const uint16_t*>(p)[i];
+  return dt == GDN_DTYPE_BF16 ? bf16_to_f32(h) : f16_to_f32(h);
+}
+
+// Compile-time typed I/O for q/k/v/y: DT is one of the GDN_DTYPE_* codes.
+template <int DT>
+struct IO;
+
+template <>
+struct IO<GDN_DTYPE_F32> {
+  using elem = float;
+  __device__ __forceinline__ static f32x4 load4(const void* p, int64_t i) {
+    return *reinterpret_cast<const f32x4*>(static_cast<const float*>(p) + i);
+  }
+  __device__ __forceinline__ static float load1(const void* p, int64_t i) {
+    return static_cast<const float*>(p)[i];
+  }
+  __device__ __forceinline__ static void store1(void* p, int64_t i, float x) {
+    static_cast<float*>(p)[i] = x;
+  }
+  __device__ __forceinline__ static void store2(void* p, int64_t i, float x0, float x1) {
+    f32x2 v = {x0, x1};
+    *reinterpret_cast<f32x2*>(static_cast<float*>(p) + i) = v;
+  }
+  __device__ __forceinline__ static f32x2 load2(const void* p, int64_t i) {
+    return *reinterpret_cast<const f32x2*>(static_cast<const float*>(p) + i);
+  }
+};
+
+template <>
+struct IO<GDN_DTYPE_BF16> {
+  using elem = uint16_t;
+  __device__ __forceinline__ static f32x4 load4(const void* p, int64_t i) {
+    u16x4 h = *reinterpret_cast<const u16x4*>(static_cast<const uint16_t*>(p) + i);
+    return f32x4{bf16_to_f32(h.x), bf16_to_f32(h.y), bf16_to_f32(h.z), bf16_to_f32(h.w)};
+  }
+  __device__ __forceinline__ static float load1(const void* p, int64_t i) {
+    return bf16_to_f32(static_cast<const uint16_t*>(p)[i]);
+  }
+  __device__ __forceinline__ static void store1(void* p, int64_t i, float x) {
+    static_cast<uint16_t*>(p)[i] = f32_to_bf16(x);
+  }
+  __device__ __forceinline__ static void store2(void* p, int64_t i, float x0, float x1) {
+    u16x2 h = {f32_to_bf16(x0), f32_to_bf16(x1)};
+    *reinterpret_cast<u16x2*>(static_cast<uint16_t*>(p) + i) = h;
+  }
+  __device__ __forceinline__ static f32x2 load2(const void* p, int64_t i) {
+    u16x2 h = *reinterpret_cast<const u16x2*>(static_cast<const uint16_t*>(p) + i);
+    return f32x2{bf16_to_f32(h.x), bf16_to_f32(h.y)};
+  }
+};
+
+template <>
+struct IO<GDN_DTYPE_F16> {
+  using elem = uint16_t;
+  __device__ __forceinline__ static f32x4 load4(const void* p, int64_t i) {
+    u16x4 h = *reinterpret_cast<const u16x4*>(static_cast<const uint16_t*>(p) + i);
+    return f32x4{f16_to_f32(h.x), f16_to_f32(h.y), f16_to_f32(h.z), f16_to_f32(h.w)};
+  }
+  __device__ __forceinline__ static float load1(const void* p, int64_t i) {
+    return f16_to_f32(static_cast<const uint16_t*>(p)[i]);
+  }
+  __device__ __forceinline__ static void store1(void* p, int64_t i, float x) {
+    static_cast<uint16_t*>(p)[i] = f32_to_f16(x);
+  }
+  __device__ __forceinline__ static void store2(void* p, int64_t i, float x0, float x1) {
+    u16x2 h = {f32_to_f16(x0), f32_to_f16(x1)};
+    *reinterpret_cast<u16x2*>(static_cast<uint16_t*>(p) + i) = h;
+  }
+  __device__ __forceinline__ static f32x2 load2(const void* p, int64_t i) {
+    u16x2 h = *reinterpret_cast<const u16x2*>(static_cast<const uint16_t*>(p) + i);
+    return f32x2{f16_to_f32(h.x), f16_to_f32(h.y)};
+  }
+};
+
+// ------------------------------------------------------------ gate math
+
+// softplus(x) = log(1 + e^x) = max(x, 0) + log1p(e^-|x|), stable for all x.
+__device__ __forceinline__ float softplus_f(float x) {
+  return fmaxf(x, 0.0f) + log1pf(expf(-fabsf(x)));
+}
+
+__device__ __forceinline__ float sigmoid_f(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+// Decay and write strength of token index gi (= token * Hv + hv).
+__device__ __forceinline__ void load_gates(int mode, const void* gx, const void* gy, int gdt,
+                                           const void* A_log, const void* dt_bias, int pdt,
+                                           int64_t gi, int hv, float& g, float& beta) {
+  if (mode == GDN_GATES_PRE) {
+    g = load_any(gx, gdt, gi);
+    beta = load_any(gy, gdt, gi);
+  } else {
+    const float a = load_any(gx, gdt, gi);
+    const float bb = load_any(gy, gdt, gi);
+    const float al = load_any(A_log, pdt, hv);
+    const float db = load_any(dt_bias, pdt, hv);
+    g = expf(-expf(al) * softplus_f(a + db));
+    beta = sigmoid_f(bb);
+  }
+}
+
+// Log of the decay (for chunked cumulative sums): -exp(A_log) softplus(a+dt_bias).
+__device__ __forceinline__ void load_log_gates(int mode, const void* gx, const void* gy, int gdt,
+                                               const void* A_log, const void* dt_bias, int pdt,
+                                               int64_t gi, int hv, float& logg, float& beta) {
+  if (mode == GDN_GATES_PRE) {
+    logg = logf(load_any(gx, gdt, gi));
+    beta = load_any(gy, gdt, gi);
+  } else {
+    const float a = load_any(gx, gdt, gi);
+    const float bb = load_any(gy, gdt, gi);
+    const float al = load_any(A_log, pdt, hv);
+    const float db = load_any(dt_bias, pdt, hv);
+    logg = -expf(al) * softplus_f(a + db);
+    beta = sigmoid_f(bb);
+  }
+}
+
+// ------------------------------------------------------- cross-lane sums
+
+// DPP lane permutations inside a 16-lane row (gfx9 encodings).
+#define GDN_DPP_QUAD_XOR1 0xB1  // quad_perm [1,0,3,2]
+#define GDN_DPP_QUAD_XOR2 0x4E  // quad_perm [2,3,0,1]
+#define GDN_DPP_HALF_MIRROR 0x141
+#define GDN_DPP_ROW_MIRROR 0x140
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float x) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over aligned groups of 8 lanes; every lane of the group gets the sum.
+__device__ __forceinline__ float sum8(float x) {
+  x += dpp_f<GDN_DPP_QUAD_XOR1>(x);
+  x += dpp_f<GDN_DPP_QUAD_XOR2>(x);
+  x += dpp_f<GDN_DPP_HALF_MIRROR>(x);
+  return x;
+}
+
+// Sum over aligned groups of 16 lanes.
+__device__ __forceinline__ float sum16(float x) {
+  x = sum8(x);
+  x += dpp_f<GDN_DPP_ROW_MIRROR>(x);
+  return x;
+}
+
+// Sum over the whole 64-lane wavefront; every lane gets the sum.
+__device__ __forceinline__ float wave_sum(float x) {
+  x = sum16(x);
+  x += __shfl_xor(x, 16, 64);
+  x += __shfl_xor(x, 32, 64);
+  return x;
+}
+
+}  // namespace gdn
+
+// ----------------------------------------------------- host-side status
+
+namespace gdn_host {
+
+// Records a message for gdn_last_error() and returns the status code.
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+
+// Checks hipGetLastError() after a launch.
+int check_launch(const char* what);
+
+inline bool dtype_ok(int dt) {
+  return dt == GDN_DTYPE_F32 || dt == GDN_DTYPE_BF16 || dt == GDN_DTYPE_F16;
+}
+
+inline bool aligned(const void* p, size_t a) {
+  return (reinterpret_cast<uintptr_t>(p) % a) == 0;
+}
+
+}  // namespace gdn_host

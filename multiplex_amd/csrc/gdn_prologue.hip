@@ -1,0 +1,318 @@
+// Fused GatedDeltaNet prologue: depthwise causal conv1d (4 taps) + SiLU +
+// q/k RMS-norm + scales + conv-state update, and the conv-state commit of a
+// partially accepted verify.  Bound by HBM: each mixed-qkv element is read
+// once and each q/k/v element written once.
+//
+// A wavefront owns one head-wide channel group (D = Dk = Dv channels; lane
+// holds D/64 adjacent channels) and walks a run of consecutive tokens with a
+// sliding window of the previous 3 inputs in registers, so the causal conv
+// needs no re-reads.  The per-token q/k norm is a wavefront reduction.
+#include "gdn_common.hpp"
+
+namespace {
+
+using namespace gdn;
+
+constexpr int kRun = 16;   // tokens per wavefront
+constexpr int kWaves = 4;  // wavefronts per workgroup (consecutive runs)
+constexpr int KT = 4;      // conv taps
+
+struct ProParams {
+  const void* qkv;
+  const void* cs_in;
+  const void* weight;
+  int w_dtype;
+  const uint8_t* mask;
+  const int32_t* cu_seqlens;
+  void* q_out;
+  void* k_out;
+  void* v_out;
+  void* cs_out;
+  int n_seqs, S, Hk, Hv, C;
+  float eps;
+};
+
+template <int CPL, int DT>
+__device__ __forceinline__ void load_vec(const void* p, int64_t i, float (&x)[CPL]) {
+  if constexpr (CPL == 1) {
+    x[0] = IO<DT>::load1(p, i);
+  } else if constexpr (CPL == 2) {
+    const f32x2 v = IO<DT>::load2(p, i);
+    x[0] = v.x;
+    x[1] = v.y;
+  } else {
+    const f32x4 v = IO<DT>::load4(p, i);
+    x[0] = v.x;
+    x[1] = v.y;
+    x[2] = v.z;
+    x[3] = v.w;
+  }
+}
+
+template <int CPL, int DT>
+__device__ __forceinline__ void store_vec(void* p, int64_t i, const float (&x)[CPL]) {
+  if constexpr (CPL == 1) {
+    IO<DT>::store1(p, i, x[0]);
+  } else {
+#pragma unroll
+    for (int j = 0; j < CPL; j += 2) IO<DT>::store2(p, i + j, x[j], x[j + 1]);
+  }
+}
+
+// Locates (sequence, first token, length, run) of this workgroup.  Packed
+// mode walks cu_seqlens: sequence n owns max(1, ceil(len/64)) run slots.
+__device__ __forceinline__ bool locate(const ProParams& p, int& seq, int64_t& start, int& len,
+                                       int& run) {
+  constexpr int RW = kRun * kWaves;
+  run = blockIdx.y;
+  if (p.cu_seqlens == nullptr) {
+    seq = blockIdx.z;
+    start = static_cast<int64_t>(seq) * p.S;
+    len = p.S;
+    return true;
+  }
+  for (int n = 0; n < p.n_seqs; ++n) {
+    const int l = p.cu_seqlens[n + 1] - p.cu_seqlens[n];
+    const int runs = l > 0 ? (l + RW - 1) / RW : 1;
+    if (run < runs) {
+      seq = n;
+      start = p.cu_seqlens[n];
+      len = l;
+      return true;
+    }
+    run -= runs;
+  }
+  return false;
+}
+
+template <int D, int DT>
+__global__ __launch_bounds__(256) void prologue_kernel(const ProParams p) {
+  constexpr int CPL = D / 64;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int grp = blockIdx.x;
+  int seq, len, run;
+  int64_t start;
+  if (!locate(p, seq, start, len, run)) return;
+  const int t_begin = run * (kRun * kWaves) + wave * kRun;
+  if (t_begin >= len && !(len == 0 && t_begin == 0)) return;
+  const int t_end = t_begin + kRun < len ? t_begin + kRun : len;
+
+  const int c0 = grp * D + lane * CPL;
+  const int64_t C = p.C;
+  float w[KT][CPL];
+#pragma unroll
+  for (int j = 0; j < CPL; ++j)
+#pragma unroll
+    for (int i = 0; i < KT; ++i) w[i][j] = load_any(p.weight, p.w_dtype, (c0 + j) * KT + i);
+
+  // window[i] = X[t + i], X = concat(conv_state (KT-1 rows), masked qkv)
+  float win[KT - 1][CPL];
+#pragma unroll
+  for (int i = 0; i < KT - 1; ++i) {
+    const int xi = t_begin + i;
+    if (xi < KT - 1) {
+      if (p.cs_in != nullptr) {
+        load_vec<CPL, DT>(p.cs_in, (static_cast<int64_t>(seq) * (KT - 1) + xi) * C + c0, win[i]);
+      } else {
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) win[i][j] = 0.0f;
+      }
+    } else {
+      const int64_t tok = start + xi - (KT - 1);
+      if (p.mask == nullptr || p.mask[tok] != 0) {
+        load_vec<CPL, DT>(p.qkv, tok * C + c0, win[i]);
+      } else {
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) win[i][j] = 0.0f;
+      }
+    }
+  }
+
+  // Head role of this channel group: 0 = q, 1 = k, 2 = v.
+  const int role = grp < p.Hk ? 0 : (grp < 2 * p.Hk ? 1 : 2);
+  const int head = role == 0 ? grp : (role == 1 ? grp - p.Hk : grp - 2 * p.Hk);
+  void* out = role == 0 ? p.q_out : (role == 1 ? p.k_out : p.v_out);
+  const int H = role == 2 ? p.Hv : p.Hk;
+  const float post = role == 0 ? 1.0f / static_cast<float>(D) : rsqrtf(static_cast<float>(D));
+
+  for (int t = t_begin; t < t_end; ++t) {
+    const int64_t tok = start + t;
+    float x[CPL];
+    if (p.mask == nullptr || p.mask[tok] != 0) {
+      load_vec<CPL, DT>(p.qkv, tok * C + c0, x);
+    } else {
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) x[j] = 0.0f;
+    }
+    float o[CPL];
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+      float acc = w[KT - 1][j] * x[j];
+#pragma unroll
+      for (int i = 0; i < KT - 1; ++i) acc = fmaf(w[i][j], win[i][j], acc);
+      o[j] = acc / (1.0f + expf(-acc));  // SiLU
+      ss = fmaf(o[j], o[j], ss);
+    }
+#pragma unroll
+    for (int i = 0; i < KT - 2; ++i)
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) win[i][j] = win[i + 1][j];
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) win[KT - 2][j] = x[j];
+    if (role != 2) {
+      ss = wave_sum(ss);
+      const float sc = rsqrtf(ss / static_cast<float>(D) + p.eps) * post;
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) o[j] *= sc;
+    }
+    store_vec<CPL, DT>(out, (tok * H + head) * D + lane * CPL, o);
+  }
+
+  if (t_end == len && p.cs_out != nullptr) {
+#pragma unroll
+    for (int i = 0; i < KT - 1; ++i)
+      store_vec<CPL, DT>(p.cs_out, (static_cast<int64_t>(seq) * (KT - 1) + i) * C + c0, win[i]);
+  }
+}
+
+template <int DT>
+__global__ __launch_bounds__(256) void conv_commit_kernel(const void* cs_in, const void* qkv,
+                                                          const uint8_t* mask,
+                                                          const int32_t* n_commit, void* cs_out,
+                                                          int T, int C, int KT1, int64_t total) {
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (idx >= total) return;
+  const int c = static_cast<int>(idx % C);
+  const int64_t bi = idx / C;
+  const int i = static_cast<int>(bi % KT1);
+  const int64_t b = bi / KT1;
+  int n = n_commit[b];
+  n = n < 0 ? 0 : (n > T ? T : n);
+  const int xi = n + i;  // row of concat(conv_state, qkv)
+  float val;
+  if (xi < KT1) {
+    val = cs_in != nullptr ? IO<DT>::load1(cs_in, (b * KT1 + xi) * C + c) : 0.0f;
+  } else {
+    const int64_t tok = b * T + (xi - KT1);
+    val = (mask == nullptr || mask[tok] != 0) ? IO<DT>::load1(qkv, tok * C + c) : 0.0f;
+  }
+  IO<DT>::store1(cs_out, idx, val);
+}
+
+}  // namespace
+
+extern "C" int gdn_conv_prologue(const void* qkv, int io_dtype, const void* conv_state_in,
+                                 const void* weight, int w_dtype, const uint8_t* mask,
+                                 const int32_t* cu_seqlens, void* q_out, void* k_out,
+                                 void* v_out, void* conv_state_out, int64_t B, int64_t S,
+                                 int64_t Hk, int64_t Hv, int64_t Dk, int64_t Dv, int64_t Kt,
+                                 float eps, void* stream) {
+  using gdn_host::fail;
+  if (B < 0 || S < 0 || Hk <= 0 || Hv <= 0)
+    return fail(GDN_ERR_INVALID, "gdn_conv_prologue: bad sizes");
+  if (Dk != Dv || (Dk != 64 && Dk != 128 && Dk != 256))
+    return fail(GDN_ERR_UNSUPPORTED, "gdn_conv_prologue: needs Dk == Dv in {64,128,256} (got %lld, %lld)",
+                (long long)Dk, (long long)Dv);
+  if (Kt != KT) return fail(GDN_ERR_UNSUPPORTED, "gdn_conv_prologue: only Kt=4 is built (got %lld)", (long long)Kt);
+  if (!gdn_host::dtype_ok(io_dtype) || !gdn_host::dtype_ok(w_dtype))
+    return fail(GDN_ERR_INVALID, "gdn_conv_prologue: bad dtype code");
+  if (qkv == nullptr || weight == nullptr || q_out == nullptr || k_out == nullptr || v_out == nullptr)
+    return fail(GDN_ERR_INVALID, "gdn_conv_prologue: qkv, weight and q/k/v outputs are required");
+  if (conv_state_out != nullptr && conv_state_out == conv_state_in)
+    return fail(GDN_ERR_INVALID, "gdn_conv_prologue: conv_state_out must not alias conv_state_in");
+  if (!(eps >= 0.0f)) return fail(GDN_ERR_INVALID, "gdn_conv_prologue: eps must be >= 0");
+  const size_t al = io_dtype == GDN_DTYPE_F32 ? 16 : 8;
+  if (!gdn_host::aligned(qkv, al) || !gdn_host::aligned(q_out, al) || !gdn_host::aligned(k_out, al) ||
+      !gdn_host::aligned(v_out, al) || !gdn_host::aligned(conv_state_in, al) ||
+      !gdn_host::aligned(conv_state_out, al))
+    return fail(GDN_ERR_INVALID, "gdn_conv_prologue: misaligned pointer");
+  if (B == 0) return GDN_OK;
+  if (B > 65535 || S > INT32_MAX / 2)
+    return fail(GDN_ERR_UNSUPPORTED, "gdn_conv_prologue: B or S too large");
+
+  ProParams p;
+  p.qkv = qkv;
+  p.cs_in = conv_state_in;
+  p.weight = weight;
+  p.w_dtype = w_dtype;
+  p.mask = mask;
+  p.cu_seqlens = cu_seqlens;
+  p.q_out = q_out;
+  p.k_out = k_out;
+  p.v_out = v_out;
+  p.cs_out = conv_state_out;
+  p.n_seqs = static_cast<int>(B);
+  p.S = static_cast<int>(S);
+  p.Hk = static_cast<int>(Hk);
+  p.Hv = static_cast<int>(Hv);
+  p.C = static_cast<int>(2 * Hk * Dk + Hv * Dv);
+  p.eps = eps;
+
+  constexpr int RW = kRun * kWaves;
+  dim3 block(64 * kWaves);
+  dim3 grid;
+  grid.x = static_cast<unsigned>(2 * Hk + Hv);
+  if (cu_seqlens != nullptr) {
+    grid.y = static_cast<unsigned>((S + RW - 1) / RW + B);
+    grid.z = 1;
+  } else {
+    grid.y = static_cast<unsigned>(S > 0 ? (S + RW - 1) / RW : 1);
+    grid.z = static_cast<unsigned>(B);
+  }
+  hipStream_t st = static_cast<hipStream_t>(stream);
+#define GDN_PRO_LAUNCH(D_, DT_) \
+  hipLaunchKernelGGL((prologue_kernel<D_, DT_>), grid, block, 0, st, p)
+#define GDN_PRO_DT(D_)                                             \
+  switch (io_dtype) {                                             \
+    case GDN_DTYPE_BF16: GDN_PRO_LAUNCH(D_, GDN_DTYPE_BF16); break; \
+    case GDN_DTYPE_F16: GDN_PRO_LAUNCH(D_, GDN_DTYPE_F16); break;   \
+    default: GDN_PRO_LAUNCH(D_, GDN_DTYPE_F32); break;              \
+  }
+  switch (Dk) {
+    case 64: GDN_PRO_DT(64); break;
+    case 128: GDN_PRO_DT(128); break;
+    default: GDN_PRO_DT(256); break;
+  }
+#undef GDN_PRO_DT
+#undef GDN_PRO_LAUNCH
+  return gdn_host::check_launch("gdn_conv_prologue");
+}
+
+extern "C" int gdn_conv_state_commit(const void* conv_state_in, const void* qkv, int io_dtype,
+                                     const uint8_t* mask, const int32_t* n_commit,
+                                     void* conv_state_out, int64_t B, int64_t T, int64_t C,
+                                     int64_t Kt, void* stream) {
+  using gdn_host::fail;
+  if (B < 0 || T < 0 || C <= 0 || Kt < 2)
+    return fail(GDN_ERR_INVALID, "gdn_conv_state_commit: bad sizes");
+  if (!gdn_host::dtype_ok(io_dtype)) return fail(GDN_ERR_INVALID, "gdn_conv_state_commit: bad dtype");
+  if (qkv == nullptr || n_commit == nullptr || conv_state_out == nullptr)
+    return fail(GDN_ERR_INVALID, "gdn_conv_state_commit: qkv, n_commit and conv_state_out are required");
+  if (conv_state_out == conv_state_in)
+    return fail(GDN_ERR_INVALID, "gdn_conv_state_commit: conv_state_out must not alias conv_state_in");
+  const int64_t total = B * (Kt - 1) * C;
+  if (total == 0) return GDN_OK;
+  if (T > INT32_MAX || C > INT32_MAX) return fail(GDN_ERR_UNSUPPORTED, "gdn_conv_state_commit: too large");
+  const int threads = 256;
+  const int64_t blocks = (total + threads - 1) / threads;
+  if (blocks > INT32_MAX) return fail(GDN_ERR_UNSUPPORTED, "gdn_conv_state_commit: too large");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int Ti = static_cast<int>(T), Ci = static_cast<int>(C), K1 = static_cast<int>(Kt - 1);
+  switch (io_dtype) {
+    case GDN_DTYPE_BF16:
+      hipLaunchKernelGGL((conv_commit_kernel<GDN_DTYPE_BF16>), dim3(blocks), dim3(threads), 0, st,
+                         conv_state_in, qkv, mask, n_commit, conv_state_out, Ti, Ci, K1, total);
+      break;
+    case GDN_DTYPE_F16:
+      hipLaunchKernelGGL((conv_commit_kernel<GDN_DTYPE_F16>), dim3(blocks), dim3(threads), 0, st,
+                         conv_state_in, qkv, mask, n_commit, conv_state_out, Ti, Ci, K1, total);
+      break;
+    default:
+      hipLaunchKernelGGL((conv_commit_kernel<GDN_DTYPE_F32>), dim3(blocks), dim3(threads), 0, st,
+                         conv_state_in, qkv, mask, n_commit, conv_state_out, Ti, Ci, K1, total);
+      break;
+  }
+  return gdn_host::check_launch("gdn_conv_state_commit");
+}

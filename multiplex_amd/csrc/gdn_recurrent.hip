@@ -1,0 +1,321 @@
+// Recurrent gated delta rule for decode, MTP verify and commit (gfx950).
+//
+// One launch advances independent (row, v-head) states by up to T tokens.
+// The state S[Dv][Dk] of a (row, v-head) is fp32 and lives in VGPRs for the
+// whole launch: it is read from HBM once and written at most once (plus the
+// optional per-token snapshots).  Rows of S (one dv index each) are
+// independent in the recurrence, so the kernel parallelises over dv:
+//
+//   * 8 lanes own one state row of Dk floats; lane `sub` holds the float4s
+//     at offsets i*32 + sub*4 (i < Dk/32), so one load instruction of a wave
+//     covers 8 rows x 128 contiguous bytes (whole cache lines).
+//   * the two dot products per token (S k and S q) are 8-lane DPP sums.
+//   * a workgroup holds 8 rows per wave; the grid is (dv blocks, Hv, rows).
+//
+// Algorithmic traffic per (row, head): Dv*Dk*4 bytes read + the same written
+// (once), plus q/k/v/y/gates per token; the kernel is HBM-bound.
+#include "gdn_common.hpp"
+
+namespace {
+
+using namespace gdn;
+
+struct RecParams {
+  const void* q;
+  const void* k;
+  const void* v;
+  const void* gx;
+  const void* gy;
+  const void* A_log;
+  const void* dt_bias;
+  int gate_mode, gate_dtype, param_dtype;
+  const float* state_in;
+  float* state_out;
+  float* snapshots;
+  void* y;
+  const uint8_t* mask;
+  const int32_t* cu_seqlens;
+  const int32_t* commit_len;
+  int T, Hk, Hv, Dv, group;  // group = Hv / Hk
+};
+
+constexpr int kLanesPerRow = 8;
+
+template <int EPL>
+__device__ __forceinline__ void store_row(float* dst, int sub, const float (&s)[EPL]) {
+  constexpr int NV = EPL / 4;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    f32x4 x = {s[4 * i], s[4 * i + 1], s[4 * i + 2], s[4 * i + 3]};
+    __builtin_nontemporal_store(x, reinterpret_cast<f32x4*>(dst + i * 32 + sub * 4));
+  }
+}
+
+template <int DK, int DT>
+__global__ __launch_bounds__(256) void recurrent_kernel(const RecParams p) {
+  constexpr int EPL = DK / kLanesPerRow;  // fp32 state elements per lane
+  constexpr int NV = EPL / 4;             // float4 per lane
+  const int sub = threadIdx.x & (kLanesPerRow - 1);
+  const int dv = blockIdx.x * (blockDim.x / kLanesPerRow) + threadIdx.x / kLanesPerRow;
+  const bool row_ok = dv < p.Dv;
+  const int hv = blockIdx.y;
+  const int row = blockIdx.z;
+  const int hk = hv / p.group;
+
+  int64_t tok0;
+  int L;
+  if (p.cu_seqlens != nullptr) {
+    tok0 = p.cu_seqlens[row];
+    L = p.cu_seqlens[row + 1] - p.cu_seqlens[row];
+  } else {
+    tok0 = static_cast<int64_t>(row) * p.T;
+    L = p.T;
+  }
+  bool write_state = p.state_out != nullptr;
+  int commit = L;
+  if (p.commit_len != nullptr) {
+    const int c = p.commit_len[row];
+    if (c < 0) write_state = false;
+    commit = c < 0 ? 0 : (c < L ? c : L);
+  }
+  const bool need_all = (p.y != nullptr) || (p.snapshots != nullptr);
+  const int steps = need_all ? L : (write_state ? commit : 0);
+
+  const int64_t srow = ((static_cast<int64_t>(row) * p.Hv + hv) * p.Dv + dv) * DK;
+  float s[EPL];
+  if (p.state_in != nullptr && row_ok) {
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const f32x4 x = __builtin_nontemporal_load(
+          reinterpret_cast<const f32x4*>(p.state_in + srow + i * 32 + sub * 4));
+      s[4 * i] = x.x;
+      s[4 * i + 1] = x.y;
+      s[4 * i + 2] = x.z;
+      s[4 * i + 3] = x.w;
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) s[e] = 0.0f;
+  }
+  if (write_state && commit == 0 && row_ok) store_row<EPL>(p.state_out + srow, sub, s);
+
+  for (int t = 0; t < steps; ++t) {
+    const int64_t tok = tok0 + t;
+    const bool active = p.mask == nullptr || p.mask[tok] != 0;
+    float yv = 0.0f;
+    if (active) {
+      float g, beta;
+      load_gates(p.gate_mode, p.gx, p.gy, p.gate_dtype, p.A_log, p.dt_bias, p.param_dtype,
+                 tok * p.Hv + hv, hv, g, beta);
+      const int64_t kq = (tok * p.Hk + hk) * DK + sub * 4;
+      float kf[EPL];
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        const f32x4 x = IO<DT>::load4(p.k, kq + i * 32);
+        kf[4 * i] = x.x;
+        kf[4 * i + 1] = x.y;
+        kf[4 * i + 2] = x.z;
+        kf[4 * i + 3] = x.w;
+      }
+      const float vv = row_ok ? IO<DT>::load1(p.v, (tok * p.Hv + hv) * p.Dv + dv) : 0.0f;
+      float kv = 0.0f;
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) {
+        s[e] *= g;
+        kv = fmaf(s[e], kf[e], kv);
+      }
+      kv = sum8(kv);
+      const float delta = beta * (vv - kv);
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) s[e] = fmaf(kf[e], delta, s[e]);
+      if (p.y != nullptr) {
+        float yp = 0.0f;
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+          const f32x4 x = IO<DT>::load4(p.q, kq + i * 32);
+          yp = fmaf(s[4 * i], x.x, yp);
+          yp = fmaf(s[4 * i + 1], x.y, yp);
+          yp = fmaf(s[4 * i + 2], x.z, yp);
+          yp = fmaf(s[4 * i + 3], x.w, yp);
+        }
+        yv = sum8(yp);
+      }
+    }
+    if (p.y != nullptr && row_ok && sub == 0) {
+      IO<DT>::store1(p.y, (tok * p.Hv + hv) * p.Dv + dv, yv);
+    }
+    if (p.snapshots != nullptr && row_ok) {
+      store_row<EPL>(p.snapshots + ((tok * p.Hv + hv) * p.Dv + dv) * DK, sub, s);
+    }
+    if (write_state && t + 1 == commit && row_ok) store_row<EPL>(p.state_out + srow, sub, s);
+  }
+}
+
+template <int DK>
+int launch_dk(int dt, dim3 grid, dim3 block, hipStream_t st, const RecParams& p) {
+  switch (dt) {
+    case GDN_DTYPE_BF16:
+      hipLaunchKernelGGL((recurrent_kernel<DK, GDN_DTYPE_BF16>), grid, block, 0, st, p);
+      break;
+    case GDN_DTYPE_F16:
+      hipLaunchKernelGGL((recurrent_kernel<DK, GDN_DTYPE_F16>), grid, block, 0, st, p);
+      break;
+    default:
+      hipLaunchKernelGGL((recurrent_kernel<DK, GDN_DTYPE_F32>), grid, block, 0, st, p);
+      break;
+  }
+  return gdn_host::check_launch("gdn_recurrent");
+}
+
+int run_recurrent(const gdn_recurrent_args* a) {
+  using gdn_host::fail;
+  if (a == nullptr) return fail(GDN_ERR_INVALID, "gdn_recurrent: args is NULL");
+  if (a->B < 0 || a->T < 0 || a->Hk <= 0 || a->Hv <= 0 || a->Dv <= 0)
+    return fail(GDN_ERR_INVALID, "gdn_recurrent: bad sizes B=%lld T=%lld Hk=%lld Hv=%lld Dv=%lld",
+                (long long)a->B, (long long)a->T, (long long)a->Hk, (long long)a->Hv,
+                (long long)a->Dv);
+  if (a->Hv % a->Hk != 0)
+    return fail(GDN_ERR_INVALID, "gdn_recurrent: Hv=%lld is not a multiple of Hk=%lld",
+                (long long)a->Hv, (long long)a->Hk);
+  if (a->Dk != 64 && a->Dk != 128 && a->Dk != 256)
+    return fail(GDN_ERR_UNSUPPORTED, "gdn_recurrent: Dk=%lld not built (64, 128, 256)",
+                (long long)a->Dk);
+  if (a->Hv > 65535 || a->B > 65535 || a->Dv > (1 << 20))
+    return fail(GDN_ERR_UNSUPPORTED, "gdn_recurrent: Hv or B above 65535");
+  if (!gdn_host::dtype_ok(a->qkv_dtype) || !gdn_host::dtype_ok(a->gate_dtype))
+    return fail(GDN_ERR_INVALID, "gdn_recurrent: bad dtype code");
+  if (a->gate_mode != GDN_GATES_RAW && a->gate_mode != GDN_GATES_PRE)
+    return fail(GDN_ERR_INVALID, "gdn_recurrent: bad gate_mode %d", a->gate_mode);
+  if (a->gate_mode == GDN_GATES_RAW &&
+      (a->A_log == nullptr || a->dt_bias == nullptr || !gdn_host::dtype_ok(a->param_dtype)))
+    return fail(GDN_ERR_INVALID, "gdn_recurrent: raw gates need A_log, dt_bias and their dtype");
+  if (a->k == nullptr || a->v == nullptr || a->gx == nullptr || a->gy == nullptr)
+    return fail(GDN_ERR_INVALID, "gdn_recurrent: k, v and gates are required");
+  if (a->y != nullptr && a->q == nullptr)
+    return fail(GDN_ERR_INVALID, "gdn_recurrent: q is required when y is requested");
+  const size_t el = a->qkv_dtype == GDN_DTYPE_F32 ? 16 : 8;
+  if (!gdn_host::aligned(a->q, el) || !gdn_host::aligned(a->k, el) ||
+      !gdn_host::aligned(a->state_in, 16) || !gdn_host::aligned(a->state_out, 16) ||
+      !gdn_host::aligned(a->snapshots, 16))
+    return fail(GDN_ERR_INVALID, "gdn_recurrent: q/k or state pointers are misaligned");
+  if (a->B == 0) return GDN_OK;
+  if (a->T > INT32_MAX) return fail(GDN_ERR_UNSUPPORTED, "gdn_recurrent: T too large");
+
+  RecParams p;
+  p.q = a->q;
+  p.k = a->k;
+  p.v = a->v;
+  p.gx = a->gx;
+  p.gy = a->gy;
+  p.A_log = a->A_log;
+  p.dt_bias = a->dt_bias;
+  p.gate_mode = a->gate_mode;
+  p.gate_dtype = a->gate_dtype;
+  p.param_dtype = a->param_dtype;
+  p.state_in = a->state_in;
+  p.state_out = a->state_out;
+  p.snapshots = a->snapshots;
+  p.y = a->y;
+  p.mask = a->mask;
+  p.cu_seqlens = a->cu_seqlens;
+  p.commit_len = a->commit_len;
+  p.T = static_cast<int>(a->T);
+  p.Hk = static_cast<int>(a->Hk);
+  p.Hv = static_cast<int>(a->Hv);
+  p.Dv = static_cast<int>(a->Dv);
+  p.group = static_cast<int>(a->Hv / a->Hk);
+
+  // Waves per workgroup: the largest of 4/2/1 that still gives >= 1024
+  // workgroups (4 per CU), so small batches spread over the 256 CUs.
+  int waves = 1;
+  for (int w = 4; w >= 1; w >>= 1) {
+    const int64_t rows_per_wg = 8 * w;
+    const int64_t wgs = a->B * a->Hv * ((a->Dv + rows_per_wg - 1) / rows_per_wg);
+    if (wgs >= 1024 || w == 1) {
+      waves = w;
+      break;
+    }
+  }
+  const int rows_per_wg = 8 * waves;
+  dim3 block(64 * waves);
+  dim3 grid(static_cast<unsigned>((a->Dv + rows_per_wg - 1) / rows_per_wg),
+            static_cast<unsigned>(a->Hv), static_cast<unsigned>(a->B));
+  hipStream_t st = static_cast<hipStream_t>(a->stream);
+  switch (a->Dk) {
+    case 64:
+      return launch_dk<64>(a->qkv_dtype, grid, block, st, p);
+    case 128:
+      return launch_dk<128>(a->qkv_dtype, grid, block, st, p);
+    default:
+      return launch_dk<256>(a->qkv_dtype, grid, block, st, p);
+  }
+}
+
+}  // namespace
+
+extern "C" int gdn_recurrent(const gdn_recurrent_args* args) { return run_recurrent(args); }
+
+extern "C" int gdn_gated_delta_update(const void* q, const void* k, const void* v, int qkv_dtype,
+                                      const void* a, const void* b, int ab_dtype,
+                                      const void* A_log, const void* dt_bias, int param_dtype,
+                                      const float* state_in, const uint8_t* mask, void* y,
+                                      float* state_out, int64_t B, int64_t T, int64_t Hk,
+                                      int64_t Hv, int64_t Dk, int64_t Dv, void* stream) {
+  if (y == nullptr || state_out == nullptr || q == nullptr)
+    return gdn_host::fail(GDN_ERR_INVALID, "gdn_gated_delta_update: q, y and state_out are required");
+  gdn_recurrent_args r = {};
+  r.q = q;
+  r.k = k;
+  r.v = v;
+  r.qkv_dtype = qkv_dtype;
+  r.gate_mode = GDN_GATES_RAW;
+  r.gx = a;
+  r.gy = b;
+  r.gate_dtype = ab_dtype;
+  r.param_dtype = param_dtype;
+  r.A_log = A_log;
+  r.dt_bias = dt_bias;
+  r.state_in = state_in;
+  r.state_out = state_out;
+  r.y = y;
+  r.mask = mask;
+  r.B = B;
+  r.T = T;
+  r.Hk = Hk;
+  r.Hv = Hv;
+  r.Dk = Dk;
+  r.Dv = Dv;
+  r.stream = stream;
+  return run_recurrent(&r);
+}
+
+extern "C" int gdn_gated_delta_kernel(const void* q, const void* k, const void* v, int qkv_dtype,
+                                      const void* g, const void* beta, int gb_dtype,
+                                      const float* state_in, const uint8_t* mask, void* y,
+                                      float* state_out, int64_t B, int64_t T, int64_t Hk,
+                                      int64_t Hv, int64_t Dk, int64_t Dv, void* stream) {
+  if (y == nullptr || state_out == nullptr || q == nullptr)
+    return gdn_host::fail(GDN_ERR_INVALID, "gdn_gated_delta_kernel: q, y and state_out are required");
+  gdn_recurrent_args r = {};
+  r.q = q;
+  r.k = k;
+  r.v = v;
+  r.qkv_dtype = qkv_dtype;
+  r.gate_mode = GDN_GATES_PRE;
+  r.gx = g;
+  r.gy = beta;
+  r.gate_dtype = gb_dtype;
+  r.param_dtype = GDN_DTYPE_F32;
+  r.state_in = state_in;
+  r.state_out = state_out;
+  r.y = y;
+  r.mask = mask;
+  r.B = B;
+  r.T = T;
+  r.Hk = Hk;
+  r.Hv = Hv;
+  r.Dk = Dk;
+  r.Dv = Dv;
+  r.stream = stream;
+  return run_recurrent(&r);
+}

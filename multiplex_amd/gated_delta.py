@@ -1,0 +1,479 @@
+"""Gated DeltaNet update on MI355X: the torch-facing mirror of mlx-lm's
+``mlx_lm.models.gated_delta`` module, backed by ``libgdn.so``.
+
+multiplex calls ``gated_delta_update(q, k, v, a, b, A_log, dt_bias, state,
+mask, use_kernel=True)`` from the GatedDeltaNet mixer
+(``multiplex/kernel/dflash.py:372-374``) and from its rollback replay
+(``dflash.py:417-422``); the engine reaches the mixer through
+``multiplex/kernel/engine.py:164-167``.  The same positional signature and
+return value ``(y, new_state)`` are kept here; new capabilities are
+keyword-only with defaults so unchanged callers keep working.
+
+Semantics (as in mlx-lm): the call is functional -- ``state`` is never
+mutated and a new state tensor is returned -- unless ``state_out=`` names a
+destination (which may be ``state`` itself for in-place use).  ``state=None``
+means a zero state.  A masked token keeps the state; its y is 0.
+
+Every tensor must live on one ROCm device; there is no CPU path.
+"""
+
+from __future__ import annotations
+
+from typing import Optional, Sequence, Union
+
+import torch
+
+from . import _lib
+
+__all__ = [
+    "compute_g",
+    "compute_beta",
+    "gated_delta_ops",
+    "gated_delta_kernel",
+    "gated_delta_update",
+    "gated_delta_verify",
+    "gated_delta_commit",
+    "chunk_workspace_bytes",
+    "prepare_recurrent",
+    "PreparedRecurrent",
+    "CHUNK_MIN_TOKENS",
+]
+
+# Packed / long rows at or above this many tokens use the chunked MFMA
+# kernel by default (shorter rows use the recurrent kernel).
+CHUNK_MIN_TOKENS = 128
+CHUNK = 64
+
+_DT = {torch.float32: _lib.DTYPE_F32, torch.bfloat16: _lib.DTYPE_BF16, torch.float16: _lib.DTYPE_F16}
+
+IntSeq = Union[Sequence[int], torch.Tensor]
+
+
+# ----------------------------------------------------------------- helpers
+
+def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def _dtype_code(t: torch.Tensor, what: str) -> int:
+    try:
+        return _DT[t.dtype]
+    except KeyError:
+        raise ValueError(f"{what}: unsupported dtype {t.dtype} (float32, bfloat16, float16)") from None
+
+
+def _require_device(tensors, names) -> torch.device:
+    dev = None
+    for t, n in zip(tensors, names):
+        if t is None:
+            continue
+        if not isinstance(t, torch.Tensor):
+            raise TypeError(f"{n} must be a torch.Tensor")
+        if t.device.type != "cuda":
+            raise ValueError(f"{n} is on {t.device}; the GDN kernels run on a ROCm device only")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise ValueError(f"{n} is on {t.device}, expected {dev}")
+    if dev is None:
+        raise ValueError("no device tensor given")
+    return dev
+
+
+def _contig(t: Optional[torch.Tensor]) -> Optional[torch.Tensor]:
+    return None if t is None else t.contiguous()
+
+
+def _stream(dev: torch.device) -> int:
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+def _mask_u8(mask: Optional[torch.Tensor], shape, what="mask") -> Optional[torch.Tensor]:
+    if mask is None:
+        return None
+    if tuple(mask.shape) != tuple(shape):
+        raise ValueError(f"{what} has shape {tuple(mask.shape)}, expected {tuple(shape)}")
+    if mask.dtype == torch.bool:
+        return mask.contiguous().view(torch.uint8)
+    if mask.dtype == torch.uint8:
+        return mask.contiguous()
+    return (mask != 0).contiguous().view(torch.uint8)
+
+
+def _check_state(state: Optional[torch.Tensor], shape, what="state"):
+    if state is None:
+        return None
+    if state.dtype != torch.float32:
+        raise ValueError(f"{what} must be float32 (got {state.dtype})")
+    if tuple(state.shape) != tuple(shape):
+        raise ValueError(f"{what} has shape {tuple(state.shape)}, expected {tuple(shape)}")
+    return state.contiguous()
+
+
+def _out_state(state_out, shape, dev, what="state_out"):
+    if state_out is None:
+        return torch.empty(shape, dtype=torch.float32, device=dev)
+    if state_out.dtype != torch.float32 or tuple(state_out.shape) != tuple(shape):
+        raise ValueError(f"{what} must be float32 of shape {tuple(shape)}")
+    if not state_out.is_contiguous():
+        raise ValueError(f"{what} must be contiguous")
+    return state_out
+
+
+def _cu_seqlens(cu: Optional[IntSeq], n_tok: int, dev) -> Optional[torch.Tensor]:
+    """Validates packed-sequence offsets on the host and returns them on ``dev``.
+
+    Offsets must start at 0, be non-decreasing and end at ``n_tok``; a device
+    tensor is copied to the host for the check (one synchronisation).
+    """
+    if cu is None:
+        return None
+    host = torch.as_tensor(cu).to("cpu", torch.int64)
+    if host.dim() != 1 or host.numel() < 2:
+        raise ValueError("cu_seqlens must be a 1-D sequence of at least 2 offsets")
+    if int(host[0]) != 0 or int(host[-1]) != n_tok:
+        raise ValueError(f"cu_seqlens must start at 0 and end at {n_tok}")
+    if bool((host[1:] < host[:-1]).any()):
+        raise ValueError("cu_seqlens must be non-decreasing")
+    if n_tok >= 2**31:
+        raise ValueError("too many packed tokens")
+    if isinstance(cu, torch.Tensor) and cu.device == dev and cu.dtype == torch.int32 and cu.is_contiguous():
+        return cu
+    return host.to(torch.int32).to(dev, non_blocking=False)
+
+
+def _int_rows(x: IntSeq, n: int, dev, what: str) -> torch.Tensor:
+    t = torch.as_tensor(x)
+    if t.dim() != 1 or t.numel() != n:
+        raise ValueError(f"{what} must have {n} entries")
+    if t.device == dev and t.dtype == torch.int32:
+        return t.contiguous()
+    return t.to(torch.int32).to(dev)
+
+
+class _Shapes:
+    """Validated problem shape of a (q, k, v, gates) set."""
+
+    def __init__(self, q, k, v, gx, gy, packed: bool):
+        if k.dim() != 4 or v.dim() != 4:
+            raise ValueError("k and v must be 4-D: [B, T, H, D]")
+        B, T, Hk, Dk = k.shape
+        if q is not None and tuple(q.shape) != (B, T, Hk, Dk):
+            raise ValueError(f"q has shape {tuple(q.shape)}, expected {(B, T, Hk, Dk)}")
+        if v.shape[0] != B or v.shape[1] != T:
+            raise ValueError("v must share the [B, T] leading dims of q/k")
+        Hv, Dv = v.shape[2], v.shape[3]
+        if Hv % Hk != 0:
+            raise ValueError(f"Hv={Hv} must be a multiple of Hk={Hk}")
+        for g, name in ((gx, "a/g"), (gy, "b/beta")):
+            if tuple(g.shape) != (B, T, Hv):
+                raise ValueError(f"{name} has shape {tuple(g.shape)}, expected {(B, T, Hv)}")
+        dt = k.dtype
+        for t, name in ((q, "q"), (v, "v")):
+            if t is not None and t.dtype != dt:
+                raise ValueError(f"q, k and v must share one dtype (k is {dt}, {name} is {t.dtype})")
+        if packed and B != 1:
+            raise ValueError("packed sequences (cu_seqlens) need a leading batch dim of 1")
+        self.B, self.T, self.Hk, self.Dk, self.Hv, self.Dv = B, T, Hk, Dk, Hv, Dv
+
+
+def _gate_codes(gx, gy):
+    if gx.dtype != gy.dtype:
+        raise ValueError(f"gates must share one dtype ({gx.dtype} vs {gy.dtype})")
+    return _dtype_code(gx, "gates")
+
+
+def _param_codes(A_log, dt_bias, Hv):
+    if A_log.shape != (Hv,) or dt_bias.shape != (Hv,):
+        raise ValueError(f"A_log and dt_bias must have shape ({Hv},)")
+    if A_log.dtype != dt_bias.dtype:
+        raise ValueError("A_log and dt_bias must share one dtype")
+    return _dtype_code(A_log, "A_log/dt_bias")
+
+
+# -------------------------------------------------------- gate transforms
+
+def compute_g(A_log: torch.Tensor, a: torch.Tensor, dt_bias: torch.Tensor) -> torch.Tensor:
+    """Decay ``g = exp(-exp(A_log) * softplus(a + dt_bias))`` in float32 (mlx-lm ``compute_g``)."""
+    _require_device([A_log, a, dt_bias], ["A_log", "a", "dt_bias"])
+    x = a.float() + dt_bias.float()
+    return torch.exp(-torch.exp(A_log.float()) * torch.nn.functional.softplus(x))
+
+
+def compute_beta(b: torch.Tensor) -> torch.Tensor:
+    """Write strength ``beta = sigmoid(b)`` in float32."""
+    _require_device([b], ["b"])
+    return torch.sigmoid(b.float())
+
+
+def gated_delta_ops(q, k, v, g, beta, state=None, mask=None):
+    """The ops path of mlx-lm (``use_kernel=False``), as device torch ops.
+
+    A step-by-step loop over T built from elementwise ops and reductions; it is
+    the slow reference form that mlx-lm runs when its fused kernel is not
+    used, kept for API parity.  It runs on the ROCm device like everything
+    else here, never silently in place of the HIP kernel.
+    """
+    dev = _require_device([q, k, v, g, beta, state, mask], ["q", "k", "v", "g", "beta", "state", "mask"])
+    sh = _Shapes(q, k, v, g, beta, packed=False)
+    r = sh.Hv // sh.Hk
+    qf = q.float().repeat_interleave(r, dim=2)
+    kf = k.float().repeat_interleave(r, dim=2)
+    vf = v.float()
+    S = (torch.zeros(sh.B, sh.Hv, sh.Dv, sh.Dk, device=dev) if state is None
+         else _check_state(state, (sh.B, sh.Hv, sh.Dv, sh.Dk)).clone())
+    ys = []
+    for t in range(sh.T):
+        Sg = S * g[:, t, :, None, None].float()
+        kv = (Sg * kf[:, t, :, None, :]).sum(-1)
+        delta = (vf[:, t] - kv) * beta[:, t, :, None].float()
+        Sn = Sg + kf[:, t, :, None, :] * delta[..., None]
+        y = (Sn * qf[:, t, :, None, :]).sum(-1)
+        if mask is not None:
+            m = mask[:, t].bool()
+            Sn = torch.where(m[:, None, None, None], Sn, S)
+            y = torch.where(m[:, None, None], y, torch.zeros_like(y))
+        S = Sn
+        ys.append(y)
+    y = torch.stack(ys, dim=1) if ys else torch.zeros(sh.B, 0, sh.Hv, sh.Dv, device=dev)
+    return y.to(q.dtype), S
+
+
+# ------------------------------------------------------------ HIP launches
+
+def _recurrent(q, k, v, gx, gy, gate_mode, A_log, dt_bias, state, mask, *,
+               y=True, state_out=None, write_state=True, snapshots=False,
+               cu_seqlens=None, commit_len=None):
+    names = ["q", "k", "v", "a/g", "b/beta", "A_log", "dt_bias", "state", "mask", "state_out"]
+    dev = _require_device([q, k, v, gx, gy, A_log, dt_bias, state, mask, state_out], names)
+    packed = cu_seqlens is not None
+    sh = _Shapes(q, k, v, gx, gy, packed)
+    q, k, v, gx, gy = (_contig(t) for t in (q, k, v, gx, gy))
+    qkv_code = _dtype_code(k, "q/k/v")
+    gate_code = _gate_codes(gx, gy)
+    if gate_mode == _lib.GATES_RAW:
+        if A_log is None or dt_bias is None:
+            raise ValueError("A_log and dt_bias are required")
+        param_code = _param_codes(A_log, dt_bias, sh.Hv)
+        A_log, dt_bias = _contig(A_log), _contig(dt_bias)
+    else:
+        param_code = _lib.DTYPE_F32
+    cu = _cu_seqlens(cu_seqlens, sh.T, dev)
+    n_rows = (cu.numel() - 1) if packed else sh.B
+    st_shape = (n_rows, sh.Hv, sh.Dv, sh.Dk)
+    state = _check_state(state, st_shape)
+    mask_u8 = _mask_u8(mask, (sh.B, sh.T))
+    out_state = _out_state(state_out, st_shape, dev) if write_state else None
+    y_t = torch.empty(sh.B, sh.T, sh.Hv, sh.Dv, dtype=k.dtype, device=dev) if y else None
+    snaps = (torch.empty(sh.B, sh.T, sh.Hv, sh.Dv, sh.Dk, dtype=torch.float32, device=dev)
+             if snapshots else None)
+    commit = None if commit_len is None else _int_rows(commit_len, n_rows, dev, "commit_len")
+    args = _lib.RecurrentArgs(
+        q=_ptr(q), k=_ptr(k), v=_ptr(v), qkv_dtype=qkv_code, gate_mode=gate_mode,
+        gx=_ptr(gx), gy=_ptr(gy), gate_dtype=gate_code, param_dtype=param_code,
+        A_log=_ptr(A_log), dt_bias=_ptr(dt_bias), state_in=_ptr(state),
+        state_out=_ptr(out_state), snapshots=_ptr(snaps), y=_ptr(y_t), mask=_ptr(mask_u8),
+        cu_seqlens=_ptr(cu), commit_len=_ptr(commit), B=n_rows, T=sh.T, Hk=sh.Hk, Hv=sh.Hv,
+        Dk=sh.Dk, Dv=sh.Dv, stream=_stream(dev),
+    )
+    with torch.cuda.device(dev):
+        _lib.call("gdn_recurrent", _lib.ctypes.byref(args))
+    return y_t, out_state, snaps
+
+
+class PreparedRecurrent:
+    """A validated recurrent launch that can be re-issued without re-validation.
+
+    Holds the argument block and keeps every tensor it points to alive.  Each
+    ``launch()`` enqueues the same kernel on the stream current at
+    ``prepare`` time (the same work a serving loop repeats every step, e.g.
+    decode with ``state_out=state``).  Safe to capture in a HIP graph.
+    """
+
+    def __init__(self, args, keep, dev):
+        self._args = args
+        self._keep = keep
+        self.device = dev
+        self._lib = _lib.load()
+
+    def launch(self):
+        st = self._lib.gdn_recurrent(_lib.ctypes.byref(self._args))
+        if st != _lib.OK:
+            _lib.check("gdn_recurrent", st)
+
+    @property
+    def outputs(self):
+        return self._keep["y"], self._keep["state_out"], self._keep["snapshots"]
+
+
+def prepare_recurrent(q, k, v, a, b, A_log, dt_bias, state, mask=None, *, y=True, state_out=None,
+                      write_state=True, snapshots=False, commit_len=None, cu_seqlens=None,
+                      gates_precomputed=False) -> PreparedRecurrent:
+    """Validates once and returns a :class:`PreparedRecurrent` (same arguments as the entry points)."""
+    mode = _lib.GATES_PRE if gates_precomputed else _lib.GATES_RAW
+    names = ["q", "k", "v", "a/g", "b/beta", "A_log", "dt_bias", "state", "mask", "state_out"]
+    dev = _require_device([q, k, v, a, b, A_log, dt_bias, state, mask, state_out], names)
+    packed = cu_seqlens is not None
+    sh = _Shapes(q, k, v, a, b, packed)
+    for t, n in ((q, "q"), (k, "k"), (v, "v"), (a, "a"), (b, "b")):
+        if t is not None and not t.is_contiguous():
+            raise ValueError(f"{n} must be contiguous for a prepared launch")
+    qkv_code = _dtype_code(k, "q/k/v")
+    gate_code = _gate_codes(a, b)
+    param_code = _param_codes(A_log, dt_bias, sh.Hv) if mode == _lib.GATES_RAW else _lib.DTYPE_F32
+    cu = _cu_seqlens(cu_seqlens, sh.T, dev)
+    n_rows = (cu.numel() - 1) if packed else sh.B
+    st_shape = (n_rows, sh.Hv, sh.Dv, sh.Dk)
+    if state is not None and (not state.is_contiguous()):
+        raise ValueError("state must be contiguous for a prepared launch")
+    state = _check_state(state, st_shape)
+    mask_u8 = _mask_u8(mask, (sh.B, sh.T))
+    out_state = _out_state(state_out, st_shape, dev) if write_state else None
+    y_t = torch.empty(sh.B, sh.T, sh.Hv, sh.Dv, dtype=k.dtype, device=dev) if y else None
+    snaps = (torch.empty(sh.B, sh.T, sh.Hv, sh.Dv, sh.Dk, dtype=torch.float32, device=dev)
+             if snapshots else None)
+    commit = None if commit_len is None else _int_rows(commit_len, n_rows, dev, "commit_len")
+    args = _lib.RecurrentArgs(
+        q=_ptr(q), k=_ptr(k), v=_ptr(v), qkv_dtype=qkv_code, gate_mode=mode,
+        gx=_ptr(a), gy=_ptr(b), gate_dtype=gate_code, param_dtype=param_code,
+        A_log=_ptr(A_log) if mode == _lib.GATES_RAW else None,
+        dt_bias=_ptr(dt_bias) if mode == _lib.GATES_RAW else None, state_in=_ptr(state),
+        state_out=_ptr(out_state), snapshots=_ptr(snaps), y=_ptr(y_t), mask=_ptr(mask_u8),
+        cu_seqlens=_ptr(cu), commit_len=_ptr(commit), B=n_rows, T=sh.T, Hk=sh.Hk, Hv=sh.Hv,
+        Dk=sh.Dk, Dv=sh.Dv, stream=_stream(dev),
+    )
+    keep = dict(q=q, k=k, v=v, a=a, b=b, A_log=A_log, dt_bias=dt_bias, state=state, mask=mask_u8,
+                cu=cu, commit=commit, y=y_t, state_out=out_state, snapshots=snaps)
+    return PreparedRecurrent(args, keep, dev)
+
+
+def chunk_workspace_bytes(n_seqs: int, n_tok: int, Hv: int, Dk: int, Dv: int, chunk: int = CHUNK) -> int:
+    return int(_lib.load().gdn_chunk_workspace_bytes(n_seqs, n_tok, Hv, Dk, Dv, chunk))
+
+
+def _chunked(q, k, v, gx, gy, gate_mode, A_log, dt_bias, state, *, cu_seqlens=None,
+             state_out=None, workspace=None):
+    names = ["q", "k", "v", "a/g", "b/beta", "A_log", "dt_bias", "state", "state_out"]
+    dev = _require_device([q, k, v, gx, gy, A_log, dt_bias, state, state_out], names)
+    packed = cu_seqlens is not None
+    sh = _Shapes(q, k, v, gx, gy, packed)
+    q, k, v, gx, gy = (_contig(t) for t in (q, k, v, gx, gy))
+    qkv_code = _dtype_code(k, "q/k/v")
+    gate_code = _gate_codes(gx, gy)
+    if gate_mode == _lib.GATES_RAW:
+        param_code = _param_codes(A_log, dt_bias, sh.Hv)
+        A_log, dt_bias = _contig(A_log), _contig(dt_bias)
+    else:
+        param_code = _lib.DTYPE_F32
+    cu = _cu_seqlens(cu_seqlens, sh.T, dev)
+    n_seqs = (cu.numel() - 1) if packed else sh.B
+    n_tok = sh.B * sh.T
+    st_shape = (n_seqs, sh.Hv, sh.Dv, sh.Dk)
+    state = _check_state(state, st_shape)
+    out_state = _out_state(state_out, st_shape, dev)
+    y_t = torch.empty(sh.B, sh.T, sh.Hv, sh.Dv, dtype=k.dtype, device=dev)
+    ws_bytes = chunk_workspace_bytes(n_seqs, n_tok, sh.Hv, sh.Dk, sh.Dv, CHUNK)
+    if workspace is None or workspace.numel() * workspace.element_size() < ws_bytes:
+        workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    with torch.cuda.device(dev):
+        _lib.call(
+            "gdn_chunk_fwd", _ptr(q), _ptr(k), _ptr(v), qkv_code, gate_mode, _ptr(gx), _ptr(gy),
+            gate_code, _ptr(A_log), _ptr(dt_bias), param_code, _ptr(state), _ptr(y_t),
+            _ptr(out_state), _ptr(cu), n_seqs, n_tok, sh.Hk, sh.Hv, sh.Dk, sh.Dv, CHUNK,
+            _ptr(workspace), ws_bytes, _stream(dev),
+        )
+    return y_t, out_state
+
+
+def _use_chunked(chunked, k, mask, cu_seqlens, T):
+    if chunked is not None:
+        return bool(chunked)
+    if mask is not None or k.dtype != torch.bfloat16 or k.shape[-1] != 128:
+        return False
+    return T >= CHUNK_MIN_TOKENS
+
+
+# ------------------------------------------------------------ entry points
+
+def gated_delta_kernel(q, k, v, g, beta, state, mask=None, *, state_out=None):
+    """mlx-lm ``gated_delta_kernel``: the fused recurrence with g and beta given.
+
+    Returns ``(y, new_state)``.
+    """
+    y, s, _ = _recurrent(q, k, v, g, beta, _lib.GATES_PRE, None, None, state, mask,
+                         state_out=state_out)
+    return y, s
+
+
+def gated_delta_update(q, k, v, a, b, A_log, dt_bias, state=None, mask=None, use_kernel=True, *,
+                       cu_seqlens: Optional[IntSeq] = None, state_out=None,
+                       chunked: Optional[bool] = None, workspace=None):
+    """mlx-lm ``gated_delta_update`` on MI355X.
+
+    Args (as mlx-lm): q, k ``[B,T,Hk,Dk]``; v ``[B,T,Hv,Dv]``; a, b ``[B,T,Hv]``;
+    A_log, dt_bias ``[Hv]``; state ``[B,Hv,Dv,Dk]`` float32 or None; mask
+    ``[B,T]`` bool or None.  ``use_kernel=False`` selects the ops path
+    (:func:`gated_delta_ops`) on the device.
+
+    Keyword-only additions: ``cu_seqlens`` packs ragged sequences in a
+    ``[1, N_tok, ...]`` layout (state then has one row per sequence);
+    ``state_out`` receives the new state (may be ``state``); ``chunked``
+    forces the chunked MFMA prefill kernel on/off (default: long unmasked
+    bf16 rows with Dk = 128); ``workspace`` is a reusable uint8 buffer for it.
+
+    Returns ``(y [B,T,Hv,Dv] in q's dtype, new_state [rows,Hv,Dv,Dk] float32)``.
+    """
+    if not use_kernel:
+        if cu_seqlens is not None:
+            raise ValueError("the ops path does not take cu_seqlens")
+        y, s = gated_delta_ops(q, k, v, compute_g(A_log, a, dt_bias), compute_beta(b), state, mask)
+        if state_out is not None:
+            state_out.copy_(s)
+            s = state_out
+        return y, s
+    T = k.shape[1]
+    if cu_seqlens is not None:
+        cu_host = torch.as_tensor(cu_seqlens).to("cpu", torch.int64)
+        T = int((cu_host[1:] - cu_host[:-1]).max()) if cu_host.numel() > 1 else 0
+    if _use_chunked(chunked, k, mask, cu_seqlens, T):
+        if mask is not None:
+            raise ValueError("the chunked kernel does not take a mask")
+        return _chunked(q, k, v, a, b, _lib.GATES_RAW, A_log, dt_bias, state,
+                        cu_seqlens=cu_seqlens, state_out=state_out, workspace=workspace)
+    y, s, _ = _recurrent(q, k, v, a, b, _lib.GATES_RAW, A_log, dt_bias, state, mask,
+                         state_out=state_out, cu_seqlens=cu_seqlens)
+    return y, s
+
+
+def gated_delta_verify(q, k, v, a, b, A_log, dt_bias, state, mask=None, *, snapshots=False,
+                       cu_seqlens: Optional[IntSeq] = None):
+    """Speculative verify: y for all T draft tokens without writing the state.
+
+    With ``snapshots=True`` also returns the float32 state after every token
+    (``[B,T,Hv,Dv,Dk]``) so a rollback is an index, at T extra state writes.
+    The default pairs with :func:`gated_delta_commit`, which re-reads the
+    pre-verify state once and writes the accepted prefix's state once.
+    Returns ``(y, snapshots or None)``.
+    """
+    y, _, snaps = _recurrent(q, k, v, a, b, _lib.GATES_RAW, A_log, dt_bias, state, mask,
+                             write_state=False, snapshots=snapshots, cu_seqlens=cu_seqlens)
+    return y, snaps
+
+
+def gated_delta_commit(k, v, a, b, A_log, dt_bias, state, n_commit: IntSeq, mask=None, *,
+                       state_out=None, cu_seqlens: Optional[IntSeq] = None):
+    """Commit the accepted prefix of a verify: the state after ``n_commit[b]`` tokens.
+
+    Equivalent to the reference rollback, which re-runs ``gated_delta_update``
+    on ``[:, :n]`` from the pre-verify state (``dflash.py:403-426``,
+    ``engine.py:337-359``), but ragged per row and in one launch that reads
+    each state once and writes it once.  ``n_commit[b]`` in ``[0, T]``
+    (0 keeps the state; a negative value skips row b).  ``state_out`` may be
+    ``state`` (in place).  Returns the new state.
+    """
+    n_rows = (len(torch.as_tensor(cu_seqlens)) - 1) if cu_seqlens is not None else k.shape[0]
+    dev = _require_device([k], ["k"])
+    commit = _int_rows(n_commit, n_rows, dev, "n_commit")
+    _, s, _ = _recurrent(None, k, v, a, b, _lib.GATES_RAW, A_log, dt_bias, state, mask,
+                         y=False, state_out=state_out, cu_seqlens=cu_seqlens, commit_len=commit)
+    return s

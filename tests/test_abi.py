@@ -1,0 +1,154 @@
+"""C-ABI checks that need no GPU: the library loads, exports every symbol
+``include/gdn.h`` declares, and rejects bad arguments before any HIP call
+(fake, never-dereferenced pointers are enough for that)."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+from multiplex_amd import _lib
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "gdn.h"
+
+FAKE = 0x10000  # 64 KiB-aligned dummy address; only ever compared, never read
+
+
+def header_functions():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(gdn_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return _lib.load()
+
+
+def test_exports_match_header(lib):
+    names = header_functions()
+    assert names == sorted(_lib.EXPORTS)
+    for n in names:
+        assert hasattr(lib, n), n
+
+
+def test_abi_version(lib):
+    assert lib.gdn_abi_version() == _lib.GDN_ABI_VERSION == 1
+
+
+def test_struct_layout_matches_header():
+    # gdn_recurrent_args: 25 fields; pointers 8 B, int32 fields packed in pairs.
+    assert ctypes.sizeof(_lib.RecurrentArgs) == 8 * 3 + 4 * 2 + 8 * 2 + 4 * 2 + 8 * 9 + 8 * 6 + 8
+
+
+def _update(lib, **kw):
+    args = dict(q=FAKE, k=FAKE, v=FAKE, qkv=_lib.DTYPE_BF16, a=FAKE, b=FAKE, ab=_lib.DTYPE_BF16,
+                A_log=FAKE, dt_bias=FAKE, pdt=_lib.DTYPE_F32, state_in=FAKE, mask=None, y=FAKE,
+                state_out=FAKE, B=2, T=1, Hk=16, Hv=32, Dk=128, Dv=128)
+    args.update(kw)
+    return lib.gdn_gated_delta_update(
+        args["q"], args["k"], args["v"], args["qkv"], args["a"], args["b"], args["ab"], args["A_log"],
+        args["dt_bias"], args["pdt"], args["state_in"], args["mask"], args["y"], args["state_out"],
+        args["B"], args["T"], args["Hk"], args["Hv"], args["Dk"], args["Dv"], None)
+
+
+@pytest.mark.parametrize(
+    "kw,status",
+    [
+        (dict(y=None), _lib.ERR_INVALID),
+        (dict(state_out=None), _lib.ERR_INVALID),
+        (dict(Dk=100), _lib.ERR_UNSUPPORTED),
+        (dict(Hv=30), _lib.ERR_INVALID),
+        (dict(qkv=7), _lib.ERR_INVALID),
+        (dict(A_log=None), _lib.ERR_INVALID),
+        (dict(B=-1), _lib.ERR_INVALID),
+        (dict(q=FAKE + 2), _lib.ERR_INVALID),
+        (dict(state_out=FAKE + 4), _lib.ERR_INVALID),
+    ],
+)
+def test_update_rejects_bad_arguments(lib, kw, status):
+    assert _update(lib, **kw) == status
+    assert _lib.last_error()
+
+
+def test_empty_batch_is_a_no_op(lib):
+    assert _update(lib, B=0) == _lib.OK
+
+
+def test_recurrent_null_args(lib):
+    assert lib.gdn_recurrent(None) == _lib.ERR_INVALID
+    a = _lib.RecurrentArgs(k=FAKE, v=FAKE, gx=FAKE, gy=FAKE, gate_mode=5, B=1, T=1, Hk=1, Hv=1, Dk=128, Dv=128)
+    assert lib.gdn_recurrent(ctypes.byref(a)) == _lib.ERR_INVALID
+    a.gate_mode = _lib.GATES_PRE
+    a.y = FAKE  # y without q
+    assert lib.gdn_recurrent(ctypes.byref(a)) == _lib.ERR_INVALID
+
+
+def test_prologue_rejects_bad_arguments(lib):
+    def call(**kw):
+        args = dict(qkv=FAKE, io=_lib.DTYPE_BF16, cs=None, w=FAKE, wdt=_lib.DTYPE_BF16, mask=None,
+                    cu=None, q=FAKE, k=FAKE, v=FAKE, cso=FAKE, B=1, S=4, Hk=16, Hv=32, Dk=128, Dv=128,
+                    Kt=4, eps=1e-6)
+        args.update(kw)
+        return lib.gdn_conv_prologue(args["qkv"], args["io"], args["cs"], args["w"], args["wdt"], args["mask"],
+                                     args["cu"], args["q"], args["k"], args["v"], args["cso"], args["B"],
+                                     args["S"], args["Hk"], args["Hv"], args["Dk"], args["Dv"], args["Kt"],
+                                     args["eps"], None)
+
+    assert call(Dk=64) == _lib.ERR_UNSUPPORTED
+    assert call(Kt=3) == _lib.ERR_UNSUPPORTED
+    assert call(cs=FAKE, cso=FAKE) == _lib.ERR_INVALID
+    assert call(q=None) == _lib.ERR_INVALID
+    assert call(eps=-1.0) == _lib.ERR_INVALID
+    assert call(B=0) == _lib.OK
+
+
+def test_conv_commit_rejects_bad_arguments(lib):
+    assert lib.gdn_conv_state_commit(FAKE, FAKE, _lib.DTYPE_BF16, None, None, FAKE, 2, 4, 8192, 4, None) == _lib.ERR_INVALID
+    assert lib.gdn_conv_state_commit(FAKE, FAKE, _lib.DTYPE_BF16, None, FAKE, FAKE, 2, 4, 8192, 1, None) == _lib.ERR_INVALID
+    assert lib.gdn_conv_state_commit(FAKE, FAKE, _lib.DTYPE_BF16, None, FAKE, 2 * FAKE, 0, 4, 8192, 4, None) == _lib.OK
+    assert lib.gdn_conv_state_commit(FAKE, FAKE, _lib.DTYPE_BF16, None, FAKE, FAKE, 2, 4, 8192, 4, None) == _lib.ERR_INVALID
+
+
+def test_chunk_rejects_bad_arguments(lib):
+    def call(**kw):
+        args = dict(q=FAKE, k=FAKE, v=FAKE, qkv=_lib.DTYPE_BF16, mode=_lib.GATES_RAW, gx=FAKE, gy=FAKE,
+                    gdt=_lib.DTYPE_BF16, A_log=FAKE, dt_bias=FAKE, pdt=_lib.DTYPE_F32, s_in=None, y=FAKE,
+                    s_out=FAKE, cu=None, n_seqs=1, n_tok=4096, Hk=16, Hv=32, Dk=128, Dv=128, chunk=64,
+                    ws=FAKE, ws_bytes=1 << 40)
+        args.update(kw)
+        return lib.gdn_chunk_fwd(*args.values(), None)
+
+    assert call(chunk=32) == _lib.ERR_UNSUPPORTED
+    assert call(qkv=_lib.DTYPE_F32) == _lib.ERR_UNSUPPORTED
+    assert call(Dk=64) == _lib.ERR_UNSUPPORTED
+    assert call(ws_bytes=0) == _lib.ERR_INVALID
+    assert call(y=None) == _lib.ERR_INVALID
+    assert call(n_seqs=2, n_tok=4095) == _lib.ERR_INVALID  # not n_seqs rows of equal length
+    assert call(n_seqs=0, n_tok=0) == _lib.OK
+
+
+def test_workspace_size_is_monotone(lib):
+    small = lib.gdn_chunk_workspace_bytes(1, 64, 32, 128, 128, 64)
+    big = lib.gdn_chunk_workspace_bytes(1, 4096, 32, 128, 128, 64)
+    assert 0 < small < big
+    assert lib.gdn_chunk_workspace_bytes(1, 64, 32, 128, 128, 32) == 0  # unsupported chunk
+
+
+def test_python_rejects_host_tensors():
+    import multiplex_amd as mx
+
+    q = torch.zeros(1, 1, 16, 128, dtype=torch.bfloat16)
+    v = torch.zeros(1, 1, 32, 128, dtype=torch.bfloat16)
+    g = torch.zeros(1, 1, 32)
+    p = torch.zeros(32)
+    with pytest.raises(ValueError, match="ROCm device"):
+        mx.gated_delta_update(q, q, v, g, g, p, p)
+    with pytest.raises(ValueError, match="ROCm device"):
+        mx.gated_delta_ops(q, q, v, g, g)
+    with pytest.raises(ValueError, match="ROCm device"):
+        mx.gdn_conv_prologue(torch.zeros(1, 1, 8192), torch.zeros(8192, 4), 16, 32, 128, 128)

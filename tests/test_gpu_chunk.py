@@ -1,0 +1,115 @@
+"""GPU parity of the chunked (WY/UT, bf16 MFMA) prefill kernel.
+
+Against the float64 oracle on subsets of heads (heads are independent, so a
+head subset of the full-size problem is an exact sub-problem), and against
+the recurrent HIP kernel at full size.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import multiplex_amd as mx
+from gdn_cases import STATE_TOL, Y_TOL, draw, head_errs_state, rel_err, row_errs_y, to_torch
+from oracle import gdn
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def chunked(t, state, cu=None):
+    return mx.gated_delta_update(t["q"], t["k"], t["v"], t["a"], t["b"], t["A_log"], t["dt_bias"], state,
+                                 cu_seqlens=cu, chunked=True)
+
+
+def oracle_heads(r, heads, Hv, Hk, state, cu=None):
+    """Oracle on v-heads ``heads`` only (q/k heads h // (Hv/Hk) selected per v-head)."""
+    grp = Hv // Hk
+    hk = [h // grp for h in heads]
+    g = gdn.compute_g(r["A_log"][heads], r["a"][:, :, heads], r["dt_bias"][heads])
+    beta = gdn.compute_beta(r["b"][:, :, heads])
+    st = None if state is None else state[:, heads]
+    args = (r["q"][:, :, hk], r["k"][:, :, hk], r["v"][:, :, heads], g, beta)
+    if cu is None:
+        return gdn.recurrent(*args, st)
+    return gdn.recurrent_varlen(*args, cu, st)
+
+
+@pytest.mark.parametrize("T", [1, 37, 64, 65, 200])
+def test_short_sequences_match_oracle(T):
+    d = draw(300 + T, 2, T, 2, 4, 128, 128)
+    t, r = to_torch(d, DEV)
+    y, S = chunked(t, t["state"])
+    y_ref, S_ref = oracle_heads(r, [0, 1, 2, 3], 4, 2, r["state"])
+    assert row_errs_y(y.float().cpu().numpy(), y_ref).max() <= Y_TOL
+    assert head_errs_state(S.cpu().numpy(), S_ref).max() <= STATE_TOL
+
+
+def test_prefill_4096_full_heads_subset_oracle():
+    # One long sequence at the prefill shape: B=1, T=4096, Hk=16, Hv=32, zero state.
+    d = draw(1003, 1, 4096, 16, 32, 128, 128, state=False)
+    t, r = to_torch(d, DEV)
+    y, S = chunked(t, None)
+    heads = [0, 1, 17, 31]
+    y_ref, S_ref = oracle_heads(r, heads, 32, 16, None)
+    yh = y[:, :, heads].float().cpu().numpy()
+    assert row_errs_y(yh, y_ref).max() <= Y_TOL
+    assert head_errs_state(S[:, heads].cpu().numpy(), S_ref).max() <= STATE_TOL
+    # all heads: chunked vs the recurrent kernel (two different algorithms)
+    y2, S2 = mx.gated_delta_update(t["q"], t["k"], t["v"], t["a"], t["b"], t["A_log"], t["dt_bias"], None,
+                                   chunked=False)
+    assert row_errs_y(y.float().cpu().numpy(), y2.float().cpu().numpy()).max() <= Y_TOL
+    assert head_errs_state(S.cpu().numpy(), S2.cpu().numpy()).max() <= STATE_TOL
+
+
+def test_packed_prefills_with_prefix_states():
+    lens = [1024, 2560, 7168]
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    d = draw(1004, 1, int(cu[-1]), 16, 32, 128, 128, state=False)
+    t, r = to_torch(d, DEV)
+    S0 = np.random.default_rng(4).normal(0, 0.02, (3, 32, 128, 128)).astype(np.float32)
+    y, S = chunked(t, torch.tensor(S0, device=DEV), cu=torch.tensor(cu))
+    heads = [3, 30]
+    y_ref, S_ref = oracle_heads(r, heads, 32, 16, S0.astype(np.float64), cu=cu)
+    for n in range(3):
+        sl = slice(int(cu[n]), int(cu[n + 1]))
+        assert rel_err(y[:, sl][:, :, heads].float().cpu().numpy(), y_ref[:, sl]) <= Y_TOL
+    assert head_errs_state(S[:, heads].cpu().numpy(), S_ref).max() <= STATE_TOL
+
+
+def test_ragged_packed_small():
+    lens = [70, 0, 1, 128, 63]
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    d = draw(305, 1, int(cu[-1]), 2, 4, 128, 128, state=False)
+    t, r = to_torch(d, DEV)
+    S0 = np.random.default_rng(6).normal(0, 0.02, (len(lens), 4, 128, 128)).astype(np.float32)
+    y, S = chunked(t, torch.tensor(S0, device=DEV), cu=cu)
+    y_ref, S_ref = oracle_heads(r, [0, 1, 2, 3], 4, 2, S0.astype(np.float64), cu=cu)
+    assert rel_err(y.float().cpu().numpy(), y_ref) <= Y_TOL
+    assert head_errs_state(S.cpu().numpy(), S_ref).max() <= STATE_TOL
+    np.testing.assert_array_equal(S[1].cpu().numpy(), S0[1])
+
+
+def test_strong_decay_is_finite_and_exact():
+    d = draw(306, 1, 256, 2, 4, 128, 128)
+    d["a"][:] = 4.0
+    d["A_log"][:] = np.log(15.0)
+    t, r = to_torch(d, DEV)
+    y, S = chunked(t, t["state"])
+    assert torch.isfinite(y.float()).all() and torch.isfinite(S).all()
+    y_ref, S_ref = oracle_heads(r, [0, 1, 2, 3], 4, 2, r["state"])
+    assert row_errs_y(y.float().cpu().numpy(), y_ref).max() <= Y_TOL
+    assert head_errs_state(S.cpu().numpy(), S_ref).max() <= STATE_TOL
+
+
+def test_in_place_state():
+    d = draw(307, 2, 100, 2, 4, 128, 128)
+    t, _ = to_torch(d, DEV)
+    y1, S1 = chunked(t, t["state"])
+    st = t["state"].clone()
+    y2, S2 = mx.gated_delta_update(t["q"], t["k"], t["v"], t["a"], t["b"], t["A_log"], t["dt_bias"], st,
+                                   state_out=st, chunked=True)
+    assert S2.data_ptr() == st.data_ptr()
+    assert torch.equal(S2, S1) and torch.equal(y2, y1)

@@ -1,0 +1,113 @@
+"""GPU parity of the fused conv1d + SiLU + q/k norm prologue and of the
+conv-state commit, against the float64 oracle and the torch golden fixture."""
+
+from __future__ import annotations
+
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+import multiplex_amd as mx
+from gdn_cases import Y_TOL, rel_err
+from oracle import gdn
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+GOLD = Path(__file__).resolve().parent / "golden"
+
+
+def draw_prologue(seed, B, S, Hk, Hv, D, with_state=True, mask_p=None, dtype=torch.bfloat16):
+    rng = np.random.default_rng(seed)
+    C = 2 * Hk * D + Hv * D
+    qkv = torch.tensor(rng.standard_normal((B, S, C))).to(dtype)
+    w = torch.tensor(rng.normal(0.0, 0.1, (C, 4))).to(dtype)
+    cs = torch.tensor(rng.standard_normal((B, 3, C))).to(dtype) if with_state else None
+    mask = torch.tensor(rng.random((B, S)) >= mask_p) if mask_p is not None else None
+    return qkv, w, cs, mask
+
+
+def check(qkv, w, cs, mask, Hk, Hv, D, cu=None):
+    dev = [None if x is None else x.to(DEV) for x in (qkv, w, cs, mask)]
+    q, k, v, cs_out = mx.gdn_conv_prologue(dev[0], dev[1], Hk, Hv, D, D, dev[2], dev[3], cu_seqlens=cu)
+    if cu is None:
+        qr, kr, vr, csr, _ = gdn.conv_prologue(qkv.double().numpy(), w.double().numpy(), Hk, Hv, D, D,
+                                               None if cs is None else cs.double().numpy(),
+                                               None if mask is None else mask.numpy())
+    else:
+        cu = np.asarray(cu)
+        outs = []
+        for n in range(len(cu) - 1):
+            sl = slice(int(cu[n]), int(cu[n + 1]))
+            outs.append(gdn.conv_prologue(qkv[:, sl].double().numpy(), w.double().numpy(), Hk, Hv, D, D,
+                                          None if cs is None else cs[n:n + 1].double().numpy(),
+                                          None if mask is None else mask[:, sl].numpy()))
+        qr, kr, vr = (np.concatenate([o[i] for o in outs], axis=1) for i in range(3))
+        csr = np.concatenate([o[3] for o in outs], axis=0)
+    for got, ref in ((q, qr), (k, kr), (v, vr)):
+        assert rel_err(got.float().cpu().numpy(), ref) <= Y_TOL
+    # the conv state is a copy of (rounded) inputs: exact
+    np.testing.assert_array_equal(cs_out.float().cpu().numpy(), csr)
+    return q, k, v, cs_out
+
+
+@pytest.mark.parametrize("D", [64, 128, 256])
+def test_prefill_prologue(D):
+    qkv, w, cs, mask = draw_prologue(20 + D, 2, 77, 2, 4, D)
+    check(qkv, w, cs, mask, 2, 4, D)
+
+
+def test_decode_prologue_full_layout():
+    # decode step at the batched shape: conv_dim = 2*16*128 + 32*128 = 8192
+    qkv, w, cs, mask = draw_prologue(21, 64, 1, 16, 32, 128)
+    check(qkv, w, cs, mask, 16, 32, 128)
+
+
+def test_verify_prologue_with_mask_and_no_state():
+    qkv, w, _, mask = draw_prologue(22, 4, 4, 2, 4, 128, with_state=False, mask_p=0.4)
+    check(qkv, w, None, mask, 2, 4, 128)
+
+
+def test_packed_sequences():
+    lens = [5, 0, 130, 1, 64]
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    qkv, w, _, _ = draw_prologue(23, 1, int(cu[-1]), 2, 4, 128)
+    cs = torch.tensor(np.random.default_rng(1).standard_normal((len(lens), 3, qkv.shape[-1]))).to(torch.bfloat16)
+    check(qkv, w, cs, None, 2, 4, 128, cu=cu)
+
+
+def test_fp32_golden_fixture():
+    with np.load(GOLD / "prologue_small.npz") as z:
+        f = {k: z[k] for k in z.files}
+    B, S, Hk, Hv, D, Kt = (int(x) for x in f["dims"])
+    # D = 16 is not built: the same channels, zero-padded per head to D = 64,
+    # leave conv, SiLU and the per-head sums unchanged but change the rms
+    # mean's divisor, so compare against the oracle at D = 64 instead.
+    qkv = torch.tensor(f["qkv"], dtype=torch.float32)
+    w = torch.tensor(f["weight"], dtype=torch.float32)
+    cs = torch.tensor(f["conv_state"], dtype=torch.float32)
+    mask = torch.tensor(f["mask"] > 0)
+
+    def pad_heads(x, H):
+        sh = x.shape[:-1]
+        return torch.nn.functional.pad(x.reshape(*sh, H, D), (0, 64 - D)).reshape(*sh, H * 64)
+
+    def widen(x):
+        kd = Hk * D
+        return torch.cat([pad_heads(x[..., :kd], Hk), pad_heads(x[..., kd:2 * kd], Hk),
+                          pad_heads(x[..., 2 * kd:], Hv)], dim=-1)
+
+    wq = widen(w.T).T.contiguous()
+    check(widen(qkv), wq, widen(cs), mask, Hk, Hv, 64)
+
+
+def test_conv_state_commit():
+    B, T = 16, 4
+    qkv, w, cs, mask = draw_prologue(24, B, T, 2, 4, 128, mask_p=0.2)
+    n = np.random.default_rng(2).integers(0, T + 1, B)
+    out = mx.conv_state_commit(cs.to(DEV), qkv.to(DEV), torch.tensor(n, dtype=torch.int32), mask.to(DEV))
+    _, _, _, _, ci = gdn.conv_prologue(qkv.double().numpy(), w.double().numpy(), 2, 4, 128, 128,
+                                       cs.double().numpy(), mask.numpy())
+    ref = gdn.conv_state_commit(ci, n, 4)
+    np.testing.assert_array_equal(out.float().cpu().numpy(), ref)

@@ -1,0 +1,233 @@
+"""GPU parity of the recurrent kernel (decode / MTP verify / commit) against
+the float64 oracle, through the C ABI (via the multiplex_amd wrappers).
+
+Tolerances: see ``gdn_cases`` (2e-3 norm-wise on bf16 y per row, 1e-4
+norm-wise on the fp32 state per (row, head)).
+"""
+
+from __future__ import annotations
+
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+import multiplex_amd as mx
+from gdn_cases import STATE_TOL, Y_TOL, draw, head_errs_state, rel_err, row_errs_y, to_torch
+from oracle import gdn
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+GOLD = Path(__file__).resolve().parent / "golden"
+
+
+def run_update(t, **kw):
+    return mx.gated_delta_update(t["q"], t["k"], t["v"], t["a"], t["b"], t["A_log"], t["dt_bias"],
+                                 t["state"], t["mask"], **kw)
+
+
+def oracle_update(r):
+    return gdn.gated_delta_update(r["q"], r["k"], r["v"], r["a"], r["b"], r["A_log"], r["dt_bias"],
+                                  r["state"], r["mask"])
+
+
+def assert_close(y, S, y_ref, S_ref, y_tol=Y_TOL, s_tol=STATE_TOL):
+    y = y.float().cpu().numpy()
+    S = S.cpu().numpy()
+    ye = row_errs_y(y, y_ref)
+    se = head_errs_state(S, S_ref)
+    assert ye.max() <= y_tol, f"y rel err {ye.max():.3e}"
+    assert se.max() <= s_tol, f"state rel err {se.max():.3e}"
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f16", "f32"])
+@pytest.mark.parametrize("Dk,Dv", [(128, 128), (64, 64), (256, 256), (128, 96)])
+def test_decode_matches_oracle(dtype, Dk, Dv):
+    d = draw(100 + Dk + Dv, 3, 1, 2, 4, Dk, Dv)
+    t, r = to_torch(d, DEV, dtype=dtype, gate_dtype=dtype)
+    y, S = run_update(t)
+    assert y.dtype == t["q"].dtype and S.dtype == torch.float32
+    assert_close(y, S, *oracle_update(r))
+
+
+def test_decode_b64_full_heads():
+    # Batched decode at the dynamic-batching shape: B=64, Hk=16, Hv=32, Dk=Dv=128.
+    d = draw(1001, 64, 1, 16, 32, 128, 128)
+    t, r = to_torch(d, DEV)
+    y, S = run_update(t)
+    assert_close(y, S, *oracle_update(r))
+
+
+def test_decode_b1_full_heads():
+    d = draw(1000, 1, 1, 16, 32, 128, 128)
+    t, r = to_torch(d, DEV)
+    y, S = run_update(t)
+    assert_close(y, S, *oracle_update(r))
+
+
+@pytest.mark.parametrize("mask_p", [None, 0.35])
+def test_multi_token_gqa_mask(mask_p):
+    d = draw(7, 3, 9, 2, 6, 128, 128, mask_p=mask_p)
+    if mask_p is not None:
+        d["mask"][1, :] = False
+        d["mask"][2, 0] = False
+    t, r = to_torch(d, DEV)
+    y, S = run_update(t)
+    y_ref, S_ref = oracle_update(r)
+    assert_close(y, S, y_ref, S_ref)
+    if mask_p is not None:
+        yc = y.float().cpu().numpy()
+        assert np.all(yc[~r["mask"]] == 0.0)
+        np.testing.assert_array_equal(S[1].cpu().numpy(), t["state"][1].cpu().numpy())
+
+
+def test_zero_state_when_none():
+    d = draw(8, 2, 5, 2, 4, 128, 128, state=False)
+    t, r = to_torch(d, DEV)
+    y, S = run_update(t)
+    assert_close(y, S, *oracle_update(r))
+
+
+@pytest.mark.parametrize("name", ["recurrent_small", "recurrent_hd128"])
+def test_golden_fixtures_fp32(name):
+    with np.load(GOLD / f"{name}.npz") as z:
+        f = {k: torch.tensor(z[k]) for k in z.files}
+    if f["q"].shape[-1] not in (64, 128, 256):
+        # Dk = 16 is not built; run the fixture with keys zero-padded to Dk = 64,
+        # which leaves every dot product (and so y and the state) unchanged.
+        pad = 64 - f["q"].shape[-1]
+        for key in ("q", "k"):
+            f[key] = torch.nn.functional.pad(f[key], (0, pad))
+        f["state"] = torch.nn.functional.pad(f["state"], (0, pad))
+        f["state_out"] = torch.nn.functional.pad(f["state_out"], (0, pad))
+    t = {k: v.to(DEV) for k, v in f.items()}
+    y, S = mx.gated_delta_update(t["q"], t["k"], t["v"], t["a"], t["b"], t["A_log"], t["dt_bias"], t["state"])
+    assert rel_err(y.cpu().numpy(), f["y"].numpy()) < 1e-5
+    assert rel_err(S.cpu().numpy(), f["state_out"].numpy()) < 1e-5
+
+
+def test_kernel_with_precomputed_gates_matches_update():
+    d = draw(9, 4, 3, 2, 4, 128, 128)
+    t, _ = to_torch(d, DEV)
+    g = mx.compute_g(t["A_log"], t["a"], t["dt_bias"])
+    beta = mx.compute_beta(t["b"])
+    y1, S1 = run_update(t)
+    y2, S2 = mx.gated_delta_kernel(t["q"], t["k"], t["v"], g, beta, t["state"])
+    assert rel_err(y2.float().cpu().numpy(), y1.float().cpu().numpy()) < 1e-3
+    assert rel_err(S2.cpu().numpy(), S1.cpu().numpy()) < 1e-5
+
+
+def test_functional_state_not_mutated_and_in_place():
+    d = draw(10, 2, 2, 2, 4, 128, 128)
+    t, r = to_torch(d, DEV)
+    before = t["state"].clone()
+    y, S = run_update(t)
+    assert torch.equal(t["state"], before)
+    y2, S2 = run_update(t, state_out=t["state"])
+    assert S2.data_ptr() == t["state"].data_ptr()
+    assert torch.equal(S2, S) and torch.equal(y2, y)
+
+
+def test_rows_bitwise_independent():
+    d = draw(11, 5, 3, 2, 4, 128, 128)
+    t, _ = to_torch(d, DEV)
+    y, S = run_update(t)
+    for b in (0, 3):
+        tb = {k: (None if v is None else (v[b:b + 1] if v.dim() >= 2 and v.shape[0] == 5 else v))
+              for k, v in t.items()}
+        yb, Sb = run_update(tb)
+        assert torch.equal(yb, y[b:b + 1]) and torch.equal(Sb, S[b:b + 1])
+
+
+def test_split_T_is_bitwise():
+    d = draw(12, 2, 7, 2, 4, 128, 128)
+    t, _ = to_torch(d, DEV)
+    y, S = run_update(t)
+    t1 = {k: (v[:, :3] if k in ("q", "k", "v", "a", "b") else v) for k, v in t.items()}
+    t2 = {k: (v[:, 3:] if k in ("q", "k", "v", "a", "b") else v) for k, v in t.items()}
+    y1, S1 = run_update(t1)
+    t2["state"] = S1
+    y2, S2 = run_update(t2)
+    assert torch.equal(torch.cat([y1, y2], 1), y) and torch.equal(S2, S)
+
+
+def test_verify_snapshots_and_commit():
+    B, T = 32, 4
+    d = draw(2002, B, T, 16, 32, 128, 128)
+    t, r = to_torch(d, DEV)
+    before = t["state"].clone()
+    y, snaps = mx.gated_delta_verify(t["q"], t["k"], t["v"], t["a"], t["b"], t["A_log"], t["dt_bias"],
+                                     t["state"], snapshots=True)
+    assert torch.equal(t["state"], before)
+    g, beta = gdn.compute_g(r["A_log"], r["a"], r["dt_bias"]), gdn.compute_beta(r["b"])
+    y_ref, _ = gdn.recurrent(r["q"], r["k"], r["v"], g, beta, r["state"])
+    assert row_errs_y(y.float().cpu().numpy(), y_ref).max() <= Y_TOL
+    n = np.random.default_rng(5).integers(1, T + 1, B)
+    S_ref = gdn.commit(r["q"], r["k"], r["v"], g, beta, r["state"], n)
+    # snapshot n-1 is the committed state
+    snap_pick = snaps[torch.arange(B), torch.tensor(n - 1)].cpu().numpy()
+    assert head_errs_state(snap_pick, S_ref).max() <= STATE_TOL
+    # commit kernel: re-reads the pre-verify state, writes the accepted prefix once
+    S_c = mx.gated_delta_commit(t["k"], t["v"], t["a"], t["b"], t["A_log"], t["dt_bias"], t["state"],
+                                torch.tensor(n, dtype=torch.int32))
+    assert head_errs_state(S_c.cpu().numpy(), S_ref).max() <= STATE_TOL
+    assert torch.equal(S_c, snaps[torch.arange(B), torch.tensor(n - 1)])
+    # in place, with a zero and a skipped row
+    n2 = n.copy()
+    n2[0], n2[1] = 0, -1
+    st = t["state"].clone()
+    mx.gated_delta_commit(t["k"], t["v"], t["a"], t["b"], t["A_log"], t["dt_bias"], st,
+                          torch.tensor(n2, dtype=torch.int32), state_out=st)
+    assert torch.equal(st[0], t["state"][0]) and torch.equal(st[1], t["state"][1])
+    assert torch.equal(st[2:], S_c[2:])
+
+
+def test_packed_ragged_rows():
+    lens = [1, 4, 0, 3, 1, 7]
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    d = draw(13, 1, int(cu[-1]), 2, 4, 128, 128, state=False)
+    t, r = to_torch(d, DEV)
+    S0 = np.random.default_rng(3).normal(0, 0.02, (len(lens), 4, 128, 128)).astype(np.float32)
+    st = torch.tensor(S0, device=DEV)
+    y, S = mx.gated_delta_update(t["q"], t["k"], t["v"], t["a"], t["b"], t["A_log"], t["dt_bias"], st,
+                                 cu_seqlens=torch.tensor(cu), chunked=False)
+    g, beta = gdn.compute_g(r["A_log"], r["a"], r["dt_bias"]), gdn.compute_beta(r["b"])
+    y_ref, S_ref = gdn.recurrent_varlen(r["q"], r["k"], r["v"], g, beta, cu, S0.astype(np.float64))
+    assert rel_err(y.float().cpu().numpy(), y_ref) <= Y_TOL
+    assert head_errs_state(S.cpu().numpy(), S_ref).max() <= STATE_TOL
+    np.testing.assert_array_equal(S[2].cpu().numpy(), S0[2])
+
+
+def test_carried_state_many_steps():
+    B, steps = 4, 40
+    d = draw(14, B, steps, 16, 32, 128, 128)
+    t, r = to_torch(d, DEV)
+    st = t["state"].clone()
+    ys = []
+    for s in range(steps):
+        y, st = mx.gated_delta_update(t["q"][:, s:s + 1], t["k"][:, s:s + 1], t["v"][:, s:s + 1],
+                                      t["a"][:, s:s + 1], t["b"][:, s:s + 1], t["A_log"], t["dt_bias"], st,
+                                      state_out=st)
+        ys.append(y)
+    y_ref, S_ref = oracle_update(r)
+    assert_close(torch.cat(ys, 1), st, y_ref, S_ref)
+
+
+def test_zero_tokens_copies_state():
+    d = draw(15, 3, 0, 2, 4, 128, 128)
+    t, _ = to_torch(d, DEV)
+    y, S = run_update(t)
+    assert y.shape == (3, 0, 4, 128)
+    assert torch.equal(S, t["state"])
+
+
+def test_ops_path_on_device_matches_kernel():
+    d = draw(16, 2, 3, 2, 4, 128, 128, mask_p=0.3)
+    t, r = to_torch(d, DEV)
+    y1, S1 = run_update(t)
+    y2, S2 = run_update(t, use_kernel=False)
+    assert y2.device.type == "cuda"
+    y_ref, S_ref = oracle_update(r)
+    assert_close(y2, S2, y_ref, S_ref)
+    assert rel_err(S1.cpu().numpy(), S2.cpu().numpy()) < 1e-5
