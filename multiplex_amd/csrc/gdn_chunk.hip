@@ -9,22 +9,23 @@
 //   S_C    = gamma_C S0 + (diag(e) U)^T K
 //
 // Two launches:
-//   chunk_prep  (grid: chunks x Hv)      -- all chunks in parallel: K K^T and
-//               Q K^T on MFMA, the decay masks, and T = (I + A)^{-1} by a
-//               blocked (16x16) forward substitution in fp32.  Writes T, P,
-//               gamma, e, beta per (chunk, head) to the workspace.
+//   chunk_prep  (grid: chunks x Hv)      -- every chunk in parallel: K K^T
+//               and Q K^T on MFMA, the decay masks, T = (I + A)^{-1} by a
+//               blocked (16x16) forward substitution in fp32.  Writes T and
+//               P as hi/lo bf16 planes (MFMA-ready) plus gamma, e, beta.
 //   chunk_scan  (grid: Dv/16 x Hv x seqs) -- sequential over the chunks of a
-//               sequence; each workgroup owns 16 rows of the state, which
-//               are independent in the recurrence, so the state chain of a
-//               head is split over 8 workgroups.  Per chunk: X = [Q;K] S0^T,
-//               R, U = T R, Y = gamma X_Q + P U, S update, all on MFMA.
+//               sequence; a workgroup owns 16 rows of the state (rows are
+//               independent in the recurrence, so one head's chain is split
+//               over 8 workgroups).  Per chunk: X = [Q;K] S0^T, R, U = T R,
+//               Y = gamma X_Q + P U, S update, all on MFMA.  The operands of
+//               chunk c+1 are loaded into registers while chunk c computes.
 //
 // Precision: q, k, v are bf16 and enter MFMA exactly.  fp32 operands (S0, T,
 // P, R, U) are split as hi + lo bf16 and multiplied in 2 (one exact operand)
 // or 3 (both split; lo*lo dropped) passes, ~2^-16 relative per product, so
 // the fp32 state meets a 1e-4 norm-wise tolerance.  Log-decay prefix sums
-// are accumulated in fp64 so exp(L_t - L_i) does not lose digits when
-// |L| is large.
+// are accumulated in fp64 so exp(L_t - L_i) keeps its digits when |L| is
+// large.
 #include "gdn_common.hpp"
 
 namespace {
@@ -33,30 +34,28 @@ using namespace gdn;
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
-constexpr int CH = 64;    // chunk length
-constexpr int DK = 128;   // key head dim
-constexpr int DV = 128;   // value head dim
-constexpr int DVT = 16;   // state rows per scan workgroup
+constexpr int CH = 64;      // chunk length
+constexpr int DK = 128;     // key head dim
+constexpr int DV = 128;     // value head dim
+constexpr int DVT = 16;     // state rows per scan workgroup
 constexpr int KP = DK + 8;  // padded LDS row (bf16) for 128-wide rows
 constexpr int CP = CH + 8;  // padded LDS row (bf16) for 64-wide rows
 
 // Workspace record per (chunk, v-head).
-constexpr size_t kOffT = 0;                        // float[64][64]  (I + A)^{-1}
-constexpr size_t kOffP = kOffT + CH * CH * 4;      // float[64][64]  decayed Q K^T (lower)
-constexpr size_t kOffGam = kOffP + CH * CH * 4;    // float[64]      exp(L_t)
-constexpr size_t kOffE = kOffGam + CH * 4;         // float[64]      exp(L_C - L_t)
-constexpr size_t kOffBeta = kOffE + CH * 4;        // float[64]
-constexpr size_t kRecBytes = kOffBeta + CH * 4;    // 33536 (multiple of 256)
+constexpr size_t kOffTh = 0;                        // bf16[64][64]  hi((I + A)^{-1})
+constexpr size_t kOffTl = kOffTh + CH * CH * 2;     // bf16[64][64]  lo
+constexpr size_t kOffPh = kOffTl + CH * CH * 2;     // bf16[64][64]  hi(decayed Q K^T)
+constexpr size_t kOffPl = kOffPh + CH * CH * 2;     // bf16[64][64]  lo
+constexpr size_t kOffGam = kOffPl + CH * CH * 2;    // float[64]     exp(L_t)
+constexpr size_t kOffE = kOffGam + CH * 4;          // float[64]     exp(L_C - L_t)
+constexpr size_t kOffBeta = kOffE + CH * 4;         // float[64]
+constexpr size_t kRecBytes = kOffBeta + CH * 4 + 256;  // 33792 (multiple of 256)
 
 struct ChunkParams {
   const uint16_t* q;
   const uint16_t* k;
   const uint16_t* v;
-  const void* gx;
-  const void* gy;
-  const void* A_log;
-  const void* dt_bias;
-  int gate_mode, gate_dtype, param_dtype;
+  GateArgs ga;
   const float* state_in;
   uint16_t* y;
   float* state_out;
@@ -71,8 +70,6 @@ __device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
-__device__ __forceinline__ uint16_t bf16_hi(float x) { return f32_to_bf16(x); }
-
 __device__ __forceinline__ void split_bf16(float x, uint16_t& hi, uint16_t& lo) {
   hi = f32_to_bf16(x);
   lo = f32_to_bf16(x - bf16_to_f32(hi));
@@ -80,6 +77,24 @@ __device__ __forceinline__ void split_bf16(float x, uint16_t& hi, uint16_t& lo) 
 
 __device__ __forceinline__ bf16x8 lds8(const uint16_t* p) {
   return *reinterpret_cast<const bf16x8*>(p);
+}
+
+// K^T in LDS is stored with its 16-byte token groups XOR-swizzled by the
+// row's dk group, so the column-wise (transposing) stores of 16 threads hit
+// different banks; readers apply the same swizzle to whole 16-byte groups.
+__device__ __forceinline__ int kt_col(int dk, int tok) {
+  return ((((tok >> 3) ^ (dk >> 3)) & 7) << 3) | (tok & 7);
+}
+
+// Component-wise "keep or zero" (a ternary on the uint4 struct would be
+// lowered through memory).
+__device__ __forceinline__ uint4 keep_if(bool c, const uint4& a) {
+  return uint4{c ? a.x : 0u, c ? a.y : 0u, c ? a.z : 0u, c ? a.w : 0u};
+}
+
+__device__ __forceinline__ void pack4(uint16_t* dst, uint16_t a, uint16_t b, uint16_t c, uint16_t d) {
+  u16x4 v = {a, b, c, d};
+  *reinterpret_cast<u16x4*>(dst) = v;
 }
 
 struct SeqRange {
@@ -146,31 +161,28 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(const ChunkParams p) {
   __shared__ __align__(16) uint16_t Qs[CH][KP];
   __shared__ float As[CH][CH + 1];
   __shared__ float Ti[CH][CH + 1];
-  __shared__ float Ms[16][17];
+  __shared__ float Ms[3][16][17];
   __shared__ double Ld[CH];
   __shared__ float Bs[CH];
 
-  for (int i = tid; i < CH * (DK / 8); i += 256) {
+  // All row loads first (rows past the chunk's end read its last row and
+  // are zeroed at the LDS store), then the LDS stores.
+  uint4 kr[4], qr[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int i = tid + 256 * j;
     const int r = i / (DK / 8), cc = (i % (DK / 8)) * 8;
-    uint4 kv = {0, 0, 0, 0}, qv = {0, 0, 0, 0};
-    if (r < len) {
-      const int64_t off = ((tok0 + r) * p.Hk + hk) * DK + cc;
-      kv = *reinterpret_cast<const uint4*>(p.k + off);
-      qv = *reinterpret_cast<const uint4*>(p.q + off);
-    }
-    *reinterpret_cast<uint4*>(&Ks[r][cc]) = kv;
-    *reinterpret_cast<uint4*>(&Qs[r][cc]) = qv;
+    const int64_t off = ((tok0 + min(r, len - 1)) * p.Hk + hk) * DK + cc;
+    kr[j] = *reinterpret_cast<const uint4*>(p.k + off);
+    qr[j] = *reinterpret_cast<const uint4*>(p.q + off);
   }
-  for (int i = tid; i < CH * (CH + 1); i += 256) (&Ti[0][0])[i] = 0.0f;
-
   unsigned char* rec = p.ws + (static_cast<size_t>(c) * p.Hv + hv) * kRecBytes;
   if (wave == 0) {
-    float lg = 0.0f, bt = 0.0f;
-    if (lane < len) {
-      load_log_gates(p.gate_mode, p.gx, p.gy, p.gate_dtype, p.A_log, p.dt_bias, p.param_dtype,
-                     (tok0 + lane) * p.Hv + hv, hv, lg, bt);
-    }
-    lg = fmaxf(lg, -1.0e30f);  // g = 0 (pre-transformed gates) stays finite
+    float lg, bt;
+    load_log_gates(p.ga, (tok0 + min(lane, len - 1)) * p.Hv + hv, hv, lg, bt);
+    // padding tokens: no decay, no write; g = 0 (pre-transformed) stays finite
+    lg = lane < len ? fmaxf(lg, -1.0e30f) : 0.0f;
+    bt = lane < len ? bt : 0.0f;
     double L = lg;
     for (int off = 1; off < 64; off <<= 1) {
       const double o = __shfl_up(L, off, 64);
@@ -183,6 +195,14 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(const ChunkParams p) {
     reinterpret_cast<float*>(rec + kOffE)[lane] = expf(static_cast<float>(LC - L));
     reinterpret_cast<float*>(rec + kOffBeta)[lane] = bt;
   }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int i = tid + 256 * j;
+    const int r = i / (DK / 8), cc = (i % (DK / 8)) * 8;
+    *reinterpret_cast<uint4*>(&Ks[r][cc]) = keep_if(r < len, kr[j]);
+    *reinterpret_cast<uint4*>(&Qs[r][cc]) = keep_if(r < len, qr[j]);
+  }
+  for (int i = tid; i < CH * (CH + 1); i += 256) (&Ti[0][0])[i] = 0.0f;
   __syncthreads();
 
   // K K^T and Q K^T: wave w computes row block w (16 rows) x 4 column blocks.
@@ -205,7 +225,8 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(const ChunkParams p) {
       qk[j] = mfma16(aq, bk, qk[j]);
     }
   }
-  float* Pg = reinterpret_cast<float*>(rec + kOffP);
+  uint16_t* Ph = reinterpret_cast<uint16_t*>(rec + kOffPh);
+  uint16_t* Pl = reinterpret_cast<uint16_t*>(rec + kOffPl);
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
 #pragma unroll
@@ -214,54 +235,105 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(const ChunkParams p) {
       const int col = 16 * j + lr;
       const float dec = col <= t ? expf(static_cast<float>(Ld[t] - Ld[col])) : 0.0f;
       As[t][col] = col < t ? Bs[t] * dec * kk[j][i] : 0.0f;
-      Pg[t * CH + col] = dec * qk[j][i];
+      uint16_t h, l;
+      split_bf16(dec * qk[j][i], h, l);
+      Ph[t * CH + col] = h;
+      Pl[t * CH + col] = l;
     }
   }
   __syncthreads();
 
   // (I + A)^{-1}, A strictly lower.  Diagonal 16x16 blocks by forward
-  // substitution (one lane per (block, column)).
+  // substitution from registers (one lane per (block, column)).
   if (wave == 0) {
     const int base = 16 * (lane >> 4), j = lane & 15;
+    float a[16][16];
+#pragma unroll
+    for (int t = 1; t < 16; ++t)
+#pragma unroll
+      for (int i = 0; i < t; ++i) a[t][i] = As[base + t][base + i];
     float x[16];
 #pragma unroll
     for (int t = 0; t < 16; ++t) {
       float acc = t == j ? 1.0f : 0.0f;
 #pragma unroll
-      for (int i = 0; i < t; ++i) acc = fmaf(-As[base + t][base + i], x[i], acc);
+      for (int i = 0; i < t; ++i) acc = fmaf(-a[t][i], x[i], acc);
       x[t] = t < j ? 0.0f : acc;
     }
 #pragma unroll
     for (int t = 0; t < 16; ++t) Ti[base + t][base + j] = x[t];
   }
   __syncthreads();
-  // Off-diagonal blocks, by distance from the diagonal:
-  //   T_IJ = -T_II * sum_{K=J}^{I-1} A_IK T_KJ
+  // Off-diagonal blocks, by distance from the diagonal (blocks of one
+  // distance in parallel):  T_IJ = -T_II * sum_{K=J}^{I-1} A_IK T_KJ
   {
-    const int r = tid >> 4, cc = tid & 15;
+    const int r = (tid >> 4) & 15, cc = tid & 15;
     for (int lvl = 1; lvl < 4; ++lvl) {
-      for (int I = lvl; I < 4; ++I) {
-        const int J = I - lvl;
+      const int nblk = 4 - lvl;
+      for (int bi = 0; bi < nblk; ++bi) {
+        const int I = lvl + bi, J = bi;
         float m = 0.0f;
         for (int Kb = J; Kb < I; ++Kb) {
 #pragma unroll
           for (int x = 0; x < 16; ++x) m = fmaf(As[16 * I + r][16 * Kb + x], Ti[16 * Kb + x][16 * J + cc], m);
         }
-        Ms[r][cc] = m;
-        __syncthreads();
+        Ms[bi][r][cc] = m;
+      }
+      __syncthreads();
+      for (int bi = 0; bi < nblk; ++bi) {
+        const int I = lvl + bi, J = bi;
         float tv = 0.0f;
 #pragma unroll
-        for (int x = 0; x < 16; ++x) tv = fmaf(-Ti[16 * I + r][16 * I + x], Ms[x][cc], tv);
+        for (int x = 0; x < 16; ++x) tv = fmaf(-Ti[16 * I + r][16 * I + x], Ms[bi][x][cc], tv);
         Ti[16 * I + r][16 * J + cc] = tv;
-        __syncthreads();
       }
+      __syncthreads();
     }
   }
-  float* Tg = reinterpret_cast<float*>(rec + kOffT);
-  for (int i = tid; i < CH * CH; i += 256) Tg[i] = Ti[i / CH][i % CH];
+  uint16_t* Th = reinterpret_cast<uint16_t*>(rec + kOffTh);
+  uint16_t* Tl = reinterpret_cast<uint16_t*>(rec + kOffTl);
+  for (int i = tid; i < CH * CH; i += 256) {
+    uint16_t h, l;
+    split_bf16(Ti[i / CH][i % CH], h, l);
+    Th[i] = h;
+    Tl[i] = l;
+  }
 }
 
 // ------------------------------------------------------------ chunk_scan
+
+// Per-thread registers holding one chunk's operands between the global
+// loads (issued a chunk ahead) and the LDS stores.
+struct Stage {
+  uint4 q[4], k[4];   // 64 x 128 bf16 each: 1024 uint4, 4 per thread
+  uint4 t[4];         // T hi (512 uint4) | T lo (512 uint4)
+  uint4 pm[4];        // P hi | P lo
+  uint4 v;            // 64 tokens x 16 state rows bf16 = 128 uint4 (threads < 128)
+  float g;            // thread < 64: gamma / e / beta of token tid
+  float e;
+  float b;
+};
+
+__device__ __forceinline__ void stage_load(const ChunkParams& p, Stage& s, int64_t t0, int clen,
+                                           const unsigned char* rec, int hk, int hv, int dv0, int tid) {
+  // Unconditional loads: rows past the chunk's end re-read its last row
+  // (zeroed at the LDS store), so no load waits inside a branch.
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int i = tid + 256 * j;
+    const int r = i >> 4, cc = (i & 15) * 8;
+    const int64_t off = ((t0 + min(r, clen - 1)) * p.Hk + hk) * DK + cc;
+    s.k[j] = *reinterpret_cast<const uint4*>(p.k + off);
+    s.q[j] = *reinterpret_cast<const uint4*>(p.q + off);
+    s.t[j] = reinterpret_cast<const uint4*>(rec + kOffTh)[i];
+    s.pm[j] = reinterpret_cast<const uint4*>(rec + kOffPh)[i];
+  }
+  const int vr = (tid & (2 * CH - 1)) >> 1;
+  s.v = *reinterpret_cast<const uint4*>(p.v + ((t0 + min(vr, clen - 1)) * p.Hv + hv) * DV + dv0 + (tid & 1) * 8);
+  s.g = reinterpret_cast<const float*>(rec + kOffGam)[tid & (CH - 1)];
+  s.e = reinterpret_cast<const float*>(rec + kOffE)[tid & (CH - 1)];
+  s.b = reinterpret_cast<const float*>(rec + kOffBeta)[tid & (CH - 1)];
+}
 
 __global__ __launch_bounds__(256) void chunk_scan_kernel(const ChunkParams p) {
   const int dv0 = blockIdx.x * DVT;
@@ -281,6 +353,7 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(const ChunkParams p) {
   __shared__ __align__(16) uint16_t Rh[DVT][CP], Rl[DVT][CP];
   __shared__ __align__(16) uint16_t Uh[DVT][CP], Ul[DVT][CP];
   __shared__ __align__(16) uint16_t Eh[DVT][CP], El[DVT][CP];
+  __shared__ __align__(16) uint16_t Vs[CH][DVT];
   __shared__ float Gs[CH], Es[CH], Bs[CH];
 
   // State tile (16 rows x 128): wave w holds columns [32w, 32w + 32) as two
@@ -296,44 +369,44 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(const ChunkParams p) {
     }
   }
 
+  Stage st;
+  if (nch > 0) {
+    const unsigned char* rec0 = p.ws + (static_cast<size_t>(sr.chunk0) * p.Hv + hv) * kRecBytes;
+    stage_load(p, st, sr.tok0, min(CH, sr.len), rec0, hk, hv, dv0, tid);
+  }
+
   for (int ci = 0; ci < nch; ++ci) {
     const int64_t t0 = sr.tok0 + static_cast<int64_t>(ci) * CH;
     const int clen = min(CH, sr.len - ci * CH);
-    const unsigned char* rec = p.ws + (static_cast<size_t>(sr.chunk0 + ci) * p.Hv + hv) * kRecBytes;
 
     __syncthreads();  // the previous chunk is done with every LDS buffer
-    for (int i = tid; i < CH * (DK / 8); i += 256) {
-      const int r = i / (DK / 8), cc = (i % (DK / 8)) * 8;
-      uint4 kv = {0, 0, 0, 0}, qv = {0, 0, 0, 0};
-      if (r < clen) {
-        const int64_t off = ((t0 + r) * p.Hk + hk) * DK + cc;
-        kv = *reinterpret_cast<const uint4*>(p.k + off);
-        qv = *reinterpret_cast<const uint4*>(p.q + off);
-      }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int i = tid + 256 * j;
+      const int r = i >> 4, cc = (i & 15) * 8;
+      const uint4 kv = keep_if(r < clen, st.k[j]);
       *reinterpret_cast<uint4*>(&Ks[r][cc]) = kv;
-      *reinterpret_cast<uint4*>(&Qs[r][cc]) = qv;
-      const uint16_t* kh = reinterpret_cast<const uint16_t*>(&kv);
+      *reinterpret_cast<uint4*>(&Qs[r][cc]) = keep_if(r < clen, st.q[j]);
+      const uint32_t kw[4] = {kv.x, kv.y, kv.z, kv.w};
 #pragma unroll
-      for (int e = 0; e < 8; ++e) KT[cc + e][r] = kh[e];
-    }
-    {
-      const float* Tg = reinterpret_cast<const float*>(rec + kOffT);
-      const float* Pg = reinterpret_cast<const float*>(rec + kOffP);
-      for (int i = tid; i < CH * CH / 4; i += 256) {
-        const int r = (4 * i) / CH, cc = (4 * i) % CH;
-        const f32x4 tv = *reinterpret_cast<const f32x4*>(Tg + 4 * i);
-        const f32x4 pv = *reinterpret_cast<const f32x4*>(Pg + 4 * i);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          split_bf16(tv[e], Th[r][cc + e], Tl[r][cc + e]);
-          split_bf16(pv[e], Ph[r][cc + e], Pl[r][cc + e]);
-        }
+      for (int e = 0; e < 8; ++e) {
+        KT[cc + e][kt_col(cc + e, r)] = static_cast<uint16_t>(kw[e >> 1] >> ((e & 1) * 16));
+      }
+      // T / P planes: rows 0..31 of hi come from i < 512, lo from i >= 512
+      const int pr = (i & 511) >> 3, pc = (i & 7) * 8;
+      if (i < 512) {
+        *reinterpret_cast<uint4*>(&Th[pr][pc]) = st.t[j];
+        *reinterpret_cast<uint4*>(&Ph[pr][pc]) = st.pm[j];
+      } else {
+        *reinterpret_cast<uint4*>(&Tl[pr][pc]) = st.t[j];
+        *reinterpret_cast<uint4*>(&Pl[pr][pc]) = st.pm[j];
       }
     }
+    if (tid < 2 * CH) *reinterpret_cast<uint4*>(&Vs[tid >> 1][(tid & 1) * 8]) = keep_if((tid >> 1) < clen, st.v);
     if (tid < CH) {
-      Gs[tid] = reinterpret_cast<const float*>(rec + kOffGam)[tid];
-      Es[tid] = reinterpret_cast<const float*>(rec + kOffE)[tid];
-      Bs[tid] = reinterpret_cast<const float*>(rec + kOffBeta)[tid];
+      Gs[tid] = st.g;
+      Es[tid] = st.e;
+      Bs[tid] = st.b;
     }
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
@@ -343,74 +416,72 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(const ChunkParams p) {
                    Sl[4 * lq + i][32 * wave + 16 * j + lr]);
       }
     }
+    // Prefetch the next chunk while this one computes.
+    if (ci + 1 < nch) {
+      const unsigned char* recn = p.ws + (static_cast<size_t>(sr.chunk0 + ci + 1) * p.Hv + hv) * kRecBytes;
+      stage_load(p, st, t0 + CH, min(CH, sr.len - (ci + 1) * CH), recn, hk, hv, dv0, tid);
+    }
     __syncthreads();
 
-    // X = [Q;K] S0^T for this wave's 16 tokens (rows) x 16 state rows (cols).
-    f32x4 xq = {0.0f, 0.0f, 0.0f, 0.0f}, xk = {0.0f, 0.0f, 0.0f, 0.0f};
+    // X_K = K S0^T first (it feeds the chain), then X_Q = Q S0^T.
+    f32x4 xk0 = {0.0f, 0.0f, 0.0f, 0.0f}, xk1 = xk0, xq = xk0;
+#pragma unroll
+    for (int s = 0; s < DK / 32; ++s) {
+      const int kc = s * 32 + lg8;
+      const bf16x8 ak = lds8(&Ks[16 * wave + lr][kc]);
+      xk0 = mfma16(ak, lds8(&Sh[lr][kc]), xk0);
+      xk1 = mfma16(ak, lds8(&Sl[lr][kc]), xk1);
+    }
 #pragma unroll
     for (int s = 0; s < DK / 32; ++s) {
       const int kc = s * 32 + lg8;
       const bf16x8 aq = lds8(&Qs[16 * wave + lr][kc]);
-      const bf16x8 ak = lds8(&Ks[16 * wave + lr][kc]);
-      const bf16x8 bh = lds8(&Sh[lr][kc]);
-      const bf16x8 bl = lds8(&Sl[lr][kc]);
-      xq = mfma16(aq, bh, xq);
-      xq = mfma16(aq, bl, xq);
-      xk = mfma16(ak, bh, xk);
-      xk = mfma16(ak, bl, xk);
+      xq = mfma16(aq, lds8(&Sh[lr][kc]), xq);
+      xq = mfma16(aq, lds8(&Sl[lr][kc]), xq);
     }
-    // R = beta (V - gamma X_K), stored transposed: R^T[state row][token].
+    // R = beta (V - gamma X_K), stored transposed: R^T[state row][token];
+    // a lane's 4 tokens are adjacent, so each plane takes one 8-byte store.
+    {
+      uint16_t rh[4], rl[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int t = 16 * wave + 4 * lq + i;
-      const float vv = t < clen ? bf16_to_f32(p.v[((t0 + t) * p.Hv + hv) * DV + dv0 + lr]) : 0.0f;
-      const float r = Bs[t] * (vv - Gs[t] * xk[i]);
-      split_bf16(r, Rh[lr][t], Rl[lr][t]);
+      for (int i = 0; i < 4; ++i) {
+        const int t = 16 * wave + 4 * lq + i;
+        const float vv = bf16_to_f32(Vs[t][lr]);
+        split_bf16(Bs[t] * (vv - Gs[t] * (xk0[i] + xk1[i])), rh[i], rl[i]);
+      }
+      const int t0l = 16 * wave + 4 * lq;
+      pack4(&Rh[lr][t0l], rh[0], rh[1], rh[2], rh[3]);
+      pack4(&Rl[lr][t0l], rl[0], rl[1], rl[2], rl[3]);
     }
     __syncthreads();
 
     // U = T R: wave w -> tokens 16w..16w+15.
-    f32x4 u = {0.0f, 0.0f, 0.0f, 0.0f};
+    f32x4 u0 = {0.0f, 0.0f, 0.0f, 0.0f}, u1 = u0;
 #pragma unroll
     for (int s = 0; s < CH / 32; ++s) {
       const int kc = s * 32 + lg8;
       const bf16x8 ah = lds8(&Th[16 * wave + lr][kc]);
-      const bf16x8 al = lds8(&Tl[16 * wave + lr][kc]);
       const bf16x8 bh = lds8(&Rh[lr][kc]);
-      const bf16x8 bl = lds8(&Rl[lr][kc]);
-      u = mfma16(ah, bh, u);
-      u = mfma16(ah, bl, u);
-      u = mfma16(al, bh, u);
+      u0 = mfma16(ah, bh, u0);
+      u1 = mfma16(ah, lds8(&Rl[lr][kc]), u1);
+      u1 = mfma16(lds8(&Tl[16 * wave + lr][kc]), bh, u1);
     }
+    {
+      uint16_t uh[4], ul[4], eh[4], el[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int t = 16 * wave + 4 * lq + i;
-      split_bf16(u[i], Uh[lr][t], Ul[lr][t]);
-      split_bf16(Es[t] * u[i], Eh[lr][t], El[lr][t]);
+      for (int i = 0; i < 4; ++i) {
+        const int t = 16 * wave + 4 * lq + i;
+        const float uv = u0[i] + u1[i];
+        split_bf16(uv, uh[i], ul[i]);
+        split_bf16(Es[t] * uv, eh[i], el[i]);
+      }
+      const int t0l = 16 * wave + 4 * lq;
+      pack4(&Uh[lr][t0l], uh[0], uh[1], uh[2], uh[3]);
+      pack4(&Ul[lr][t0l], ul[0], ul[1], ul[2], ul[3]);
+      pack4(&Eh[lr][t0l], eh[0], eh[1], eh[2], eh[3]);
+      pack4(&El[lr][t0l], el[0], el[1], el[2], el[3]);
     }
     __syncthreads();
-
-    // Y = gamma X_Q + P U for this wave's 16 tokens.
-    f32x4 yacc = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-    for (int s = 0; s < CH / 32; ++s) {
-      const int kc = s * 32 + lg8;
-      const bf16x8 ah = lds8(&Ph[16 * wave + lr][kc]);
-      const bf16x8 al = lds8(&Pl[16 * wave + lr][kc]);
-      const bf16x8 bh = lds8(&Uh[lr][kc]);
-      const bf16x8 bl = lds8(&Ul[lr][kc]);
-      yacc = mfma16(ah, bh, yacc);
-      yacc = mfma16(ah, bl, yacc);
-      yacc = mfma16(al, bh, yacc);
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int t = 16 * wave + 4 * lq + i;
-      if (t < clen) {
-        const float yv = fmaf(Gs[t], xq[i], yacc[i]);
-        p.y[((t0 + t) * p.Hv + hv) * DV + dv0 + lr] = f32_to_bf16(yv);
-      }
-    }
 
     // S = gamma_C S0 + (diag(e) U)^T K: wave w -> state columns [32w, 32w+32).
     const float gC = Gs[CH - 1];
@@ -423,9 +494,30 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(const ChunkParams p) {
       const bf16x8 el = lds8(&El[lr][kc]);
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
-        const bf16x8 bk = lds8(&KT[32 * wave + 16 * j + lr][kc]);
+        const int dk = 32 * wave + 16 * j + lr;
+        const bf16x8 bk = lds8(&KT[dk][kt_col(dk, kc)]);
         sacc[j] = mfma16(eh, bk, sacc[j]);
         sacc[j] = mfma16(el, bk, sacc[j]);
+      }
+    }
+
+    // Y = gamma X_Q + P U for this wave's 16 tokens.
+    f32x4 y0 = {0.0f, 0.0f, 0.0f, 0.0f}, y1 = y0;
+#pragma unroll
+    for (int s = 0; s < CH / 32; ++s) {
+      const int kc = s * 32 + lg8;
+      const bf16x8 ah = lds8(&Ph[16 * wave + lr][kc]);
+      const bf16x8 bh = lds8(&Uh[lr][kc]);
+      y0 = mfma16(ah, bh, y0);
+      y1 = mfma16(ah, lds8(&Ul[lr][kc]), y1);
+      y1 = mfma16(lds8(&Pl[16 * wave + lr][kc]), bh, y1);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int t = 16 * wave + 4 * lq + i;
+      if (t < clen) {
+        const float yv = fmaf(Gs[t], xq[i], y0[i] + y1[i]);
+        p.y[((t0 + t) * p.Hv + hv) * DV + dv0 + lr] = f32_to_bf16(yv);
       }
     }
   }
@@ -477,19 +569,20 @@ extern "C" int gdn_chunk_fwd(const void* q, const void* k, const void* v, int qk
   if (!gdn_host::dtype_ok(gate_dtype) ||
       (gate_mode == GDN_GATES_RAW && (!gdn_host::dtype_ok(param_dtype) || !A_log || !dt_bias)))
     return fail(GDN_ERR_INVALID, "gdn_chunk_fwd: bad gate arguments");
-  if (!q || !k || !v || !gx || !gy || !y || !state_out)
-    return fail(GDN_ERR_INVALID, "gdn_chunk_fwd: q, k, v, gates, y and state_out are required");
   const bool packed = cu_seqlens != nullptr;
   if (!packed && n_seqs > 0 && n_tok % n_seqs != 0)
     return fail(GDN_ERR_INVALID, "gdn_chunk_fwd: n_tok=%lld is not n_seqs=%lld rows of equal length",
                 (long long)n_tok, (long long)n_seqs);
+  if (n_tok > 0 && (!q || !k || !v || !gx || !gy || !y))
+    return fail(GDN_ERR_INVALID, "gdn_chunk_fwd: q, k, v, gates and y are required");
+  if (!state_out) return fail(GDN_ERR_INVALID, "gdn_chunk_fwd: state_out is required");
   if (n_seqs == 0) return GDN_OK;
   const size_t need = gdn_chunk_workspace_bytes(n_seqs, n_tok, Hv, Dk, Dv, chunk);
   if (workspace == nullptr || workspace_bytes < need)
     return fail(GDN_ERR_INVALID, "gdn_chunk_fwd: workspace of %zu bytes is below the %zu needed", workspace_bytes,
                 need);
   if (!gdn_host::aligned(workspace, 256) || !gdn_host::aligned(q, 16) || !gdn_host::aligned(k, 16) ||
-      !gdn_host::aligned(state_in, 16) || !gdn_host::aligned(state_out, 16))
+      !gdn_host::aligned(v, 16) || !gdn_host::aligned(state_in, 16) || !gdn_host::aligned(state_out, 16))
     return fail(GDN_ERR_INVALID, "gdn_chunk_fwd: misaligned pointer");
   if (n_tok > INT32_MAX / 2 || n_seqs > 65535 || Hv > 65535)
     return fail(GDN_ERR_UNSUPPORTED, "gdn_chunk_fwd: problem too large");
@@ -498,13 +591,13 @@ extern "C" int gdn_chunk_fwd(const void* q, const void* k, const void* v, int qk
   p.q = static_cast<const uint16_t*>(q);
   p.k = static_cast<const uint16_t*>(k);
   p.v = static_cast<const uint16_t*>(v);
-  p.gx = gx;
-  p.gy = gy;
-  p.A_log = A_log;
-  p.dt_bias = dt_bias;
-  p.gate_mode = gate_mode;
-  p.gate_dtype = gate_dtype;
-  p.param_dtype = param_dtype;
+  p.ga.gx = gx;
+  p.ga.gy = gy;
+  p.ga.A_log = A_log;
+  p.ga.dt_bias = dt_bias;
+  p.ga.mode = gate_mode;
+  p.ga.gdt = gate_dtype;
+  p.ga.pdt = param_dtype;
   p.state_in = state_in;
   p.y = static_cast<uint16_t*>(y);
   p.state_out = state_out;

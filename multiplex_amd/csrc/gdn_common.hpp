@@ -125,37 +125,83 @@ __device__ __forceinline__ float softplus_f(float x) {
 
 __device__ __forceinline__ float sigmoid_f(float x) { return 1.0f / (1.0f + expf(-x)); }
 
-// Decay and write strength of token index gi (= token * Hv + hv).
-__device__ __forceinline__ void load_gates(int mode, const void* gx, const void* gy, int gdt,
-                                           const void* A_log, const void* dt_bias, int pdt,
-                                           int64_t gi, int hv, float& g, float& beta) {
-  if (mode == GDN_GATES_PRE) {
-    g = load_any(gx, gdt, gi);
-    beta = load_any(gy, gdt, gi);
+// Gate encodings.  GF_ANY reads runtime dtypes (and GDN_GATES_PRE); the
+// typed formats cover the usual layouts with plain typed loads, which keeps
+// the loads free of per-dtype branches (and of the waits those force).
+enum GateFormat : int {
+  GF_ANY = 0,     // any dtypes, raw or pre-transformed gates
+  GF_IO_F32 = 1,  // raw: a, b in the q/k/v dtype; A_log, dt_bias fp32
+  GF_IO_IO = 2,   // raw: a, b, A_log, dt_bias all in the q/k/v dtype
+};
+
+struct GateArgs {
+  const void* gx;  // a or g
+  const void* gy;  // b or beta
+  const void* A_log;
+  const void* dt_bias;
+  int mode, gdt, pdt;
+};
+
+// Raw gate inputs of token index gi (= token * Hv + hv).
+template <int GF, int DT>
+__device__ __forceinline__ void gate_load(const GateArgs& ga, int64_t gi, float& x, float& y) {
+  if constexpr (GF == GF_ANY) {
+    x = load_any(ga.gx, ga.gdt, gi);
+    y = load_any(ga.gy, ga.gdt, gi);
   } else {
-    const float a = load_any(gx, gdt, gi);
-    const float bb = load_any(gy, gdt, gi);
-    const float al = load_any(A_log, pdt, hv);
-    const float db = load_any(dt_bias, pdt, hv);
-    g = expf(-expf(al) * softplus_f(a + db));
-    beta = sigmoid_f(bb);
+    x = IO<DT>::load1(ga.gx, gi);
+    y = IO<DT>::load1(ga.gy, gi);
   }
 }
 
-// Log of the decay (for chunked cumulative sums): -exp(A_log) softplus(a+dt_bias).
-__device__ __forceinline__ void load_log_gates(int mode, const void* gx, const void* gy, int gdt,
-                                               const void* A_log, const void* dt_bias, int pdt,
-                                               int64_t gi, int hv, float& logg, float& beta) {
-  if (mode == GDN_GATES_PRE) {
-    logg = logf(load_any(gx, gdt, gi));
-    beta = load_any(gy, gdt, gi);
+// Per-head parameters (raw mode): exp(A_log[hv]) and dt_bias[hv].
+template <int GF, int DT>
+__device__ __forceinline__ void param_load(const GateArgs& ga, int hv, float& ea, float& db) {
+  if (ga.mode == GDN_GATES_PRE) {
+    ea = 0.0f;
+    db = 0.0f;
+    return;
+  }
+  float al;
+  if constexpr (GF == GF_ANY) {
+    al = load_any(ga.A_log, ga.pdt, hv);
+    db = load_any(ga.dt_bias, ga.pdt, hv);
+  } else if constexpr (GF == GF_IO_F32) {
+    al = static_cast<const float*>(ga.A_log)[hv];
+    db = static_cast<const float*>(ga.dt_bias)[hv];
   } else {
-    const float a = load_any(gx, gdt, gi);
-    const float bb = load_any(gy, gdt, gi);
-    const float al = load_any(A_log, pdt, hv);
-    const float db = load_any(dt_bias, pdt, hv);
-    logg = -expf(al) * softplus_f(a + db);
-    beta = sigmoid_f(bb);
+    al = IO<DT>::load1(ga.A_log, hv);
+    db = IO<DT>::load1(ga.dt_bias, hv);
+  }
+  ea = expf(al);
+}
+
+// g = exp(-exp(A_log) softplus(a + dt_bias)), beta = sigmoid(b)  (raw mode).
+template <int GF>
+__device__ __forceinline__ void gate_transform(int mode, float x, float y, float ea, float db, float& g,
+                                               float& beta) {
+  if (GF == GF_ANY && mode == GDN_GATES_PRE) {
+    g = x;
+    beta = y;
+  } else {
+    g = expf(-ea * softplus_f(x + db));
+    beta = sigmoid_f(y);
+  }
+}
+
+// Log decay (chunked prefill): -exp(A_log) softplus(a + dt_bias), or log g.
+__device__ __forceinline__ void load_log_gates(const GateArgs& ga, int64_t gi, int hv, float& logg,
+                                               float& beta) {
+  const float x = load_any(ga.gx, ga.gdt, gi);
+  const float y = load_any(ga.gy, ga.gdt, gi);
+  if (ga.mode == GDN_GATES_PRE) {
+    logg = logf(x);
+    beta = y;
+  } else {
+    const float al = load_any(ga.A_log, ga.pdt, hv);
+    const float db = load_any(ga.dt_bias, ga.pdt, hv);
+    logg = -expf(al) * softplus_f(x + db);
+    beta = sigmoid_f(y);
   }
 }
 

@@ -136,20 +136,29 @@ __global__ __launch_bounds__(256) void prologue_kernel(const ProParams p) {
   const int H = role == 2 ? p.Hv : p.Hk;
   const float post = role == 0 ? 1.0f / static_cast<float>(D) : rsqrtf(static_cast<float>(D));
 
-  for (int t = t_begin; t < t_end; ++t) {
+  // Load the whole run first (one memory latency), then walk it.
+  float xs[kRun][CPL];
+#pragma unroll
+  for (int u = 0; u < kRun; ++u) {
+    const int t = t_begin + u;
     const int64_t tok = start + t;
-    float x[CPL];
-    if (p.mask == nullptr || p.mask[tok] != 0) {
-      load_vec<CPL, DT>(p.qkv, tok * C + c0, x);
+    if (t < t_end && (p.mask == nullptr || p.mask[tok] != 0)) {
+      load_vec<CPL, DT>(p.qkv, tok * C + c0, xs[u]);
     } else {
 #pragma unroll
-      for (int j = 0; j < CPL; ++j) x[j] = 0.0f;
+      for (int j = 0; j < CPL; ++j) xs[u][j] = 0.0f;
     }
+  }
+#pragma unroll
+  for (int u = 0; u < kRun; ++u) {
+    const int t = t_begin + u;
+    if (t >= t_end) break;
+    const int64_t tok = start + t;
     float o[CPL];
     float ss = 0.0f;
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
-      float acc = w[KT - 1][j] * x[j];
+      float acc = w[KT - 1][j] * xs[u][j];
 #pragma unroll
       for (int i = 0; i < KT - 1; ++i) acc = fmaf(w[i][j], win[i][j], acc);
       o[j] = acc / (1.0f + expf(-acc));  // SiLU
@@ -160,7 +169,7 @@ __global__ __launch_bounds__(256) void prologue_kernel(const ProParams p) {
 #pragma unroll
       for (int j = 0; j < CPL; ++j) win[i][j] = win[i + 1][j];
 #pragma unroll
-    for (int j = 0; j < CPL; ++j) win[KT - 2][j] = x[j];
+    for (int j = 0; j < CPL; ++j) win[KT - 2][j] = xs[u][j];
     if (role != 2) {
       ss = wave_sum(ss);
       const float sc = rsqrtf(ss / static_cast<float>(D) + p.eps) * post;

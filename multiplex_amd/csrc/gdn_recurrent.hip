@@ -12,23 +12,29 @@
 //   * the two dot products per token (S k and S q) are 8-lane DPP sums.
 //   * a workgroup holds 8 rows per wave; the grid is (dv blocks, Hv, rows).
 //
-// Algorithmic traffic per (row, head): Dv*Dk*4 bytes read + the same written
-// (once), plus q/k/v/y/gates per token; the kernel is HBM-bound.
+// Every load is branch-free (clamped addresses; a device-resident zero row
+// for a missing state, a constant 1 for a missing mask), and a token's
+// inputs are issued ahead of the state stream, so one memory latency covers
+// both.  Algorithmic traffic per (row, head): Dv*Dk*4 bytes read + the same
+// written (once), plus q/k/v/y/gates per token; the kernel is HBM-bound.
 #include "gdn_common.hpp"
 
 namespace {
 
 using namespace gdn;
 
+constexpr int kLanesPerRow = 8;
+constexpr int kMaxDk = 256;
+
+// Read-only stand-ins for absent operands (loads stay unconditional).
+__device__ const float kZeroRow[kMaxDk] = {};
+__device__ const uint8_t kActive = 1;
+
 struct RecParams {
   const void* q;
   const void* k;
   const void* v;
-  const void* gx;
-  const void* gy;
-  const void* A_log;
-  const void* dt_bias;
-  int gate_mode, gate_dtype, param_dtype;
+  GateArgs ga;
   const float* state_in;
   float* state_out;
   float* snapshots;
@@ -38,8 +44,6 @@ struct RecParams {
   const int32_t* commit_len;
   int T, Hk, Hv, Dv, group;  // group = Hv / Hk
 };
-
-constexpr int kLanesPerRow = 8;
 
 template <int EPL>
 __device__ __forceinline__ void store_row(float* dst, int sub, const float (&s)[EPL]) {
@@ -51,13 +55,53 @@ __device__ __forceinline__ void store_row(float* dst, int sub, const float (&s)[
   }
 }
 
-template <int DK, int DT>
+// Inputs of one token for the lanes of one state row (raw gate inputs; the
+// transform runs after the loads have been issued).
+template <int EPL>
+struct TokenIn {
+  float k[EPL];
+  float q[EPL];
+  float v, gx, gy;
+  uint8_t m;
+};
+
+template <int DK, int DT, int GF, bool WANT_Q>
+__device__ __forceinline__ void load_token(const RecParams& p, int64_t tok, int hv, int hk, int dv_c, int sub,
+                                           TokenIn<DK / kLanesPerRow>& in) {
+  constexpr int NV = DK / kLanesPerRow / 4;
+  const uint8_t* mp = p.mask != nullptr ? p.mask + tok : &kActive;
+  in.m = *mp;
+  gate_load<GF, DT>(p.ga, tok * p.Hv + hv, in.gx, in.gy);
+  const int64_t kq = (tok * p.Hk + hk) * DK + sub * 4;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const f32x4 x = IO<DT>::load4(p.k, kq + i * 32);
+    in.k[4 * i] = x.x;
+    in.k[4 * i + 1] = x.y;
+    in.k[4 * i + 2] = x.z;
+    in.k[4 * i + 3] = x.w;
+    if (WANT_Q) {
+      const f32x4 z = IO<DT>::load4(p.q, kq + i * 32);
+      in.q[4 * i] = z.x;
+      in.q[4 * i + 1] = z.y;
+      in.q[4 * i + 2] = z.z;
+      in.q[4 * i + 3] = z.w;
+    }
+  }
+  in.v = IO<DT>::load1(p.v, (tok * p.Hv + hv) * p.Dv + dv_c);
+}
+
+// PF: the inputs of token t+1 are loaded while token t computes (T > 1
+// launches: verify, commit, short prefill); T = 1 decode uses the leaner
+// PF = false body, which keeps occupancy for the state stream.
+template <int DK, int DT, int GF, bool PF>
 __global__ __launch_bounds__(256) void recurrent_kernel(const RecParams p) {
   constexpr int EPL = DK / kLanesPerRow;  // fp32 state elements per lane
   constexpr int NV = EPL / 4;             // float4 per lane
   const int sub = threadIdx.x & (kLanesPerRow - 1);
   const int dv = blockIdx.x * (blockDim.x / kLanesPerRow) + threadIdx.x / kLanesPerRow;
   const bool row_ok = dv < p.Dv;
+  const int dv_c = row_ok ? dv : p.Dv - 1;  // loads use a valid row; stores check row_ok
   const int hv = blockIdx.y;
   const int row = blockIdx.z;
   const int hk = hv / p.group;
@@ -78,93 +122,113 @@ __global__ __launch_bounds__(256) void recurrent_kernel(const RecParams p) {
     if (c < 0) write_state = false;
     commit = c < 0 ? 0 : (c < L ? c : L);
   }
-  const bool need_all = (p.y != nullptr) || (p.snapshots != nullptr);
+  const bool want_y = p.y != nullptr;
+  const bool need_all = want_y || (p.snapshots != nullptr);
   const int steps = need_all ? L : (write_state ? commit : 0);
 
+  // Token 0's inputs and the head parameters first, then the state.
+  TokenIn<EPL> cur;
+  if (steps > 0) {
+    if (PF && want_y) load_token<DK, DT, GF, true>(p, tok0, hv, hk, dv_c, sub, cur);
+    else load_token<DK, DT, GF, false>(p, tok0, hv, hk, dv_c, sub, cur);
+  }
+  float ea, db;
+  param_load<GF, DT>(p.ga, hv, ea, db);
+
   const int64_t srow = ((static_cast<int64_t>(row) * p.Hv + hv) * p.Dv + dv) * DK;
+  const int64_t srow_c = ((static_cast<int64_t>(row) * p.Hv + hv) * p.Dv + dv_c) * DK;
+  const float* src = p.state_in != nullptr ? p.state_in + srow_c : kZeroRow;
   float s[EPL];
-  if (p.state_in != nullptr && row_ok) {
 #pragma unroll
-    for (int i = 0; i < NV; ++i) {
-      const f32x4 x = __builtin_nontemporal_load(
-          reinterpret_cast<const f32x4*>(p.state_in + srow + i * 32 + sub * 4));
-      s[4 * i] = x.x;
-      s[4 * i + 1] = x.y;
-      s[4 * i + 2] = x.z;
-      s[4 * i + 3] = x.w;
-    }
-  } else {
-#pragma unroll
-    for (int e = 0; e < EPL; ++e) s[e] = 0.0f;
+  for (int i = 0; i < NV; ++i) {
+    const f32x4 x = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(src + i * 32 + sub * 4));
+    s[4 * i] = x.x;
+    s[4 * i + 1] = x.y;
+    s[4 * i + 2] = x.z;
+    s[4 * i + 3] = x.w;
   }
   if (write_state && commit == 0 && row_ok) store_row<EPL>(p.state_out + srow, sub, s);
 
   for (int t = 0; t < steps; ++t) {
     const int64_t tok = tok0 + t;
-    const bool active = p.mask == nullptr || p.mask[tok] != 0;
+    TokenIn<EPL> nxt;
+    if (PF && t + 1 < steps) {
+      if (want_y) load_token<DK, DT, GF, true>(p, tok + 1, hv, hk, dv_c, sub, nxt);
+      else load_token<DK, DT, GF, false>(p, tok + 1, hv, hk, dv_c, sub, nxt);
+    }
     float yv = 0.0f;
-    if (active) {
+    if (cur.m != 0) {
       float g, beta;
-      load_gates(p.gate_mode, p.gx, p.gy, p.gate_dtype, p.A_log, p.dt_bias, p.param_dtype,
-                 tok * p.Hv + hv, hv, g, beta);
-      const int64_t kq = (tok * p.Hk + hk) * DK + sub * 4;
-      float kf[EPL];
-#pragma unroll
-      for (int i = 0; i < NV; ++i) {
-        const f32x4 x = IO<DT>::load4(p.k, kq + i * 32);
-        kf[4 * i] = x.x;
-        kf[4 * i + 1] = x.y;
-        kf[4 * i + 2] = x.z;
-        kf[4 * i + 3] = x.w;
-      }
-      const float vv = row_ok ? IO<DT>::load1(p.v, (tok * p.Hv + hv) * p.Dv + dv) : 0.0f;
+      gate_transform<GF>(p.ga.mode, cur.gx, cur.gy, ea, db, g, beta);
       float kv = 0.0f;
 #pragma unroll
       for (int e = 0; e < EPL; ++e) {
         s[e] *= g;
-        kv = fmaf(s[e], kf[e], kv);
+        kv = fmaf(s[e], cur.k[e], kv);
       }
       kv = sum8(kv);
-      const float delta = beta * (vv - kv);
+      const float delta = beta * (cur.v - kv);
 #pragma unroll
-      for (int e = 0; e < EPL; ++e) s[e] = fmaf(kf[e], delta, s[e]);
-      if (p.y != nullptr) {
+      for (int e = 0; e < EPL; ++e) s[e] = fmaf(cur.k[e], delta, s[e]);
+      if (want_y) {
         float yp = 0.0f;
+        if (PF) {
 #pragma unroll
-        for (int i = 0; i < NV; ++i) {
-          const f32x4 x = IO<DT>::load4(p.q, kq + i * 32);
-          yp = fmaf(s[4 * i], x.x, yp);
-          yp = fmaf(s[4 * i + 1], x.y, yp);
-          yp = fmaf(s[4 * i + 2], x.z, yp);
-          yp = fmaf(s[4 * i + 3], x.w, yp);
+          for (int e = 0; e < EPL; ++e) yp = fmaf(s[e], cur.q[e], yp);
+        } else {
+          const int64_t kq = (tok * p.Hk + hk) * DK + sub * 4;
+#pragma unroll
+          for (int i = 0; i < NV; ++i) {
+            const f32x4 x = IO<DT>::load4(p.q, kq + i * 32);
+            yp = fmaf(s[4 * i], x.x, yp);
+            yp = fmaf(s[4 * i + 1], x.y, yp);
+            yp = fmaf(s[4 * i + 2], x.z, yp);
+            yp = fmaf(s[4 * i + 3], x.w, yp);
+          }
         }
         yv = sum8(yp);
       }
     }
-    if (p.y != nullptr && row_ok && sub == 0) {
-      IO<DT>::store1(p.y, (tok * p.Hv + hv) * p.Dv + dv, yv);
-    }
+    if (want_y && row_ok && sub == 0) IO<DT>::store1(p.y, (tok * p.Hv + hv) * p.Dv + dv, yv);
     if (p.snapshots != nullptr && row_ok) {
       store_row<EPL>(p.snapshots + ((tok * p.Hv + hv) * p.Dv + dv) * DK, sub, s);
     }
     if (write_state && t + 1 == commit && row_ok) store_row<EPL>(p.state_out + srow, sub, s);
+    if (t + 1 < steps) {
+      if (PF) cur = nxt;
+      else load_token<DK, DT, GF, false>(p, tok + 1, hv, hk, dv_c, sub, cur);
+    }
   }
 }
 
+template <int DK, int DT, int GF>
+int launch_pf(bool pf, dim3 grid, dim3 block, hipStream_t st, const RecParams& p) {
+  if (pf) hipLaunchKernelGGL((recurrent_kernel<DK, DT, GF, true>), grid, block, 0, st, p);
+  else hipLaunchKernelGGL((recurrent_kernel<DK, DT, GF, false>), grid, block, 0, st, p);
+  return gdn_host::check_launch("gdn_recurrent");
+}
+
+template <int DK, int DT>
+int launch_gf(int gf, bool pf, dim3 grid, dim3 block, hipStream_t st, const RecParams& p) {
+  // Typed gate formats are built for the Dk = 128 kernels; other head
+  // sizes read gates through the runtime-dtype path.
+  if constexpr (DK == 128) {
+    if (gf == GF_IO_F32) return launch_pf<DK, DT, GF_IO_F32>(pf, grid, block, st, p);
+    if (gf == GF_IO_IO) return launch_pf<DK, DT, GF_IO_IO>(pf, grid, block, st, p);
+  }
+  return launch_pf<DK, DT, GF_ANY>(pf, grid, block, st, p);
+}
+
 template <int DK>
-int launch_dk(int dt, dim3 grid, dim3 block, hipStream_t st, const RecParams& p) {
+int launch_dt(int dt, int gf, bool pf, dim3 grid, dim3 block, hipStream_t st, const RecParams& p) {
   switch (dt) {
     case GDN_DTYPE_BF16:
-      hipLaunchKernelGGL((recurrent_kernel<DK, GDN_DTYPE_BF16>), grid, block, 0, st, p);
-      break;
+      return launch_gf<DK, GDN_DTYPE_BF16>(gf, pf, grid, block, st, p);
     case GDN_DTYPE_F16:
-      hipLaunchKernelGGL((recurrent_kernel<DK, GDN_DTYPE_F16>), grid, block, 0, st, p);
-      break;
+      return launch_gf<DK, GDN_DTYPE_F16>(gf, pf, grid, block, st, p);
     default:
-      hipLaunchKernelGGL((recurrent_kernel<DK, GDN_DTYPE_F32>), grid, block, 0, st, p);
-      break;
+      return launch_gf<DK, GDN_DTYPE_F32>(gf, pf, grid, block, st, p);
   }
-  return gdn_host::check_launch("gdn_recurrent");
 }
 
 int run_recurrent(const gdn_recurrent_args* a) {
@@ -189,9 +253,11 @@ int run_recurrent(const gdn_recurrent_args* a) {
   if (a->gate_mode == GDN_GATES_RAW &&
       (a->A_log == nullptr || a->dt_bias == nullptr || !gdn_host::dtype_ok(a->param_dtype)))
     return fail(GDN_ERR_INVALID, "gdn_recurrent: raw gates need A_log, dt_bias and their dtype");
-  if (a->k == nullptr || a->v == nullptr || a->gx == nullptr || a->gy == nullptr)
+  // With no tokens the launch only copies state_in to state_out, and empty
+  // token tensors may legitimately come with NULL data pointers.
+  if (a->T > 0 && (a->k == nullptr || a->v == nullptr || a->gx == nullptr || a->gy == nullptr))
     return fail(GDN_ERR_INVALID, "gdn_recurrent: k, v and gates are required");
-  if (a->y != nullptr && a->q == nullptr)
+  if (a->T > 0 && a->y != nullptr && a->q == nullptr)
     return fail(GDN_ERR_INVALID, "gdn_recurrent: q is required when y is requested");
   const size_t el = a->qkv_dtype == GDN_DTYPE_F32 ? 16 : 8;
   if (!gdn_host::aligned(a->q, el) || !gdn_host::aligned(a->k, el) ||
@@ -205,13 +271,13 @@ int run_recurrent(const gdn_recurrent_args* a) {
   p.q = a->q;
   p.k = a->k;
   p.v = a->v;
-  p.gx = a->gx;
-  p.gy = a->gy;
-  p.A_log = a->A_log;
-  p.dt_bias = a->dt_bias;
-  p.gate_mode = a->gate_mode;
-  p.gate_dtype = a->gate_dtype;
-  p.param_dtype = a->param_dtype;
+  p.ga.gx = a->gx;
+  p.ga.gy = a->gy;
+  p.ga.A_log = a->A_log;
+  p.ga.dt_bias = a->dt_bias;
+  p.ga.mode = a->gate_mode;
+  p.ga.gdt = a->gate_dtype;
+  p.ga.pdt = a->param_dtype;
   p.state_in = a->state_in;
   p.state_out = a->state_out;
   p.snapshots = a->snapshots;
@@ -224,6 +290,12 @@ int run_recurrent(const gdn_recurrent_args* a) {
   p.Hv = static_cast<int>(a->Hv);
   p.Dv = static_cast<int>(a->Dv);
   p.group = static_cast<int>(a->Hv / a->Hk);
+
+  int gf = GF_ANY;
+  if (a->gate_mode == GDN_GATES_RAW && a->gate_dtype == a->qkv_dtype) {
+    if (a->param_dtype == GDN_DTYPE_F32) gf = GF_IO_F32;
+    else if (a->param_dtype == a->qkv_dtype) gf = GF_IO_IO;
+  }
 
   // Waves per workgroup: the largest of 4/2/1 that still gives >= 1024
   // workgroups (4 per CU), so small batches spread over the 256 CUs.
@@ -241,13 +313,15 @@ int run_recurrent(const gdn_recurrent_args* a) {
   dim3 grid(static_cast<unsigned>((a->Dv + rows_per_wg - 1) / rows_per_wg),
             static_cast<unsigned>(a->Hv), static_cast<unsigned>(a->B));
   hipStream_t st = static_cast<hipStream_t>(a->stream);
+  // Tokens per row > 1 (or packed rows): prefetch the next token's inputs.
+  const bool pf = a->T > 1 || a->cu_seqlens != nullptr;
   switch (a->Dk) {
     case 64:
-      return launch_dk<64>(a->qkv_dtype, grid, block, st, p);
+      return launch_dt<64>(a->qkv_dtype, gf, pf, grid, block, st, p);
     case 128:
-      return launch_dk<128>(a->qkv_dtype, grid, block, st, p);
+      return launch_dt<128>(a->qkv_dtype, gf, pf, grid, block, st, p);
     default:
-      return launch_dk<256>(a->qkv_dtype, grid, block, st, p);
+      return launch_dt<256>(a->qkv_dtype, gf, pf, grid, block, st, p);
   }
 }
 
@@ -261,7 +335,7 @@ extern "C" int gdn_gated_delta_update(const void* q, const void* k, const void* 
                                       const float* state_in, const uint8_t* mask, void* y,
                                       float* state_out, int64_t B, int64_t T, int64_t Hk,
                                       int64_t Hv, int64_t Dk, int64_t Dv, void* stream) {
-  if (y == nullptr || state_out == nullptr || q == nullptr)
+  if (state_out == nullptr || (T > 0 && (y == nullptr || q == nullptr)))
     return gdn_host::fail(GDN_ERR_INVALID, "gdn_gated_delta_update: q, y and state_out are required");
   gdn_recurrent_args r = {};
   r.q = q;
@@ -294,7 +368,7 @@ extern "C" int gdn_gated_delta_kernel(const void* q, const void* k, const void* 
                                       const float* state_in, const uint8_t* mask, void* y,
                                       float* state_out, int64_t B, int64_t T, int64_t Hk,
                                       int64_t Hv, int64_t Dk, int64_t Dv, void* stream) {
-  if (y == nullptr || state_out == nullptr || q == nullptr)
+  if (state_out == nullptr || (T > 0 && (y == nullptr || q == nullptr)))
     return gdn_host::fail(GDN_ERR_INVALID, "gdn_gated_delta_kernel: q, y and state_out are required");
   gdn_recurrent_args r = {};
   r.q = q;
