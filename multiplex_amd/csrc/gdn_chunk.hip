@@ -105,6 +105,17 @@ struct SeqRange {
 
 __device__ __forceinline__ int n_chunks(int len) { return (len + CH - 1) / CH; }
 
+// Workgroups are dispatched to the 8 XCDs round-robin by linear block id.
+// This maps block id -> work index so that each XCD gets one contiguous
+// range of work indices (whose consumers of the same data then share that
+// XCD's L2).  Identity when the grid does not split evenly.
+__device__ __forceinline__ int xcd_work_index() {
+  constexpr int kXcds = 8;
+  const int n = gridDim.x, b = blockIdx.x;
+  if (n % kXcds != 0) return b;
+  return (b % kXcds) * (n / kXcds) + b / kXcds;
+}
+
 __device__ __forceinline__ SeqRange seq_range(const ChunkParams& p, int n) {
   SeqRange r;
   if (p.cu == nullptr) {
@@ -149,8 +160,10 @@ __device__ __forceinline__ bool chunk_at(const ChunkParams& p, int c, int64_t& t
 // ------------------------------------------------------------ chunk_prep
 
 __global__ __launch_bounds__(256) void chunk_prep_kernel(const ChunkParams p) {
-  const int c = blockIdx.x;
-  const int hv = blockIdx.y;
+  // work index = chunk * Hv + hv: both v-heads of a k-head (GQA) share an XCD
+  const int w = xcd_work_index();
+  const int c = w / p.Hv;
+  const int hv = w % p.Hv;
   int64_t tok0;
   int len;
   if (!chunk_at(p, c, tok0, len)) return;
@@ -336,9 +349,12 @@ __device__ __forceinline__ void stage_load(const ChunkParams& p, Stage& s, int64
 }
 
 __global__ __launch_bounds__(256) void chunk_scan_kernel(const ChunkParams p) {
-  const int dv0 = blockIdx.x * DVT;
-  const int hv = blockIdx.y;
-  const int seq = blockIdx.z;
+  // work index = (seq * Hv + hv) * 8 + tile: the 8 state-row tiles of a head,
+  // which read the same Q/K/T/P stream, run on one XCD and share its L2.
+  const int w = xcd_work_index();
+  const int dv0 = (w % (DV / DVT)) * DVT;
+  const int hv = (w / (DV / DVT)) % p.Hv;
+  const int seq = w / ((DV / DVT) * p.Hv);
   const int hk = hv / p.group;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int lr = lane & 15, lq = lane >> 4, lg8 = lq * 8;
@@ -584,7 +600,8 @@ extern "C" int gdn_chunk_fwd(const void* q, const void* k, const void* v, int qk
   if (!gdn_host::aligned(workspace, 256) || !gdn_host::aligned(q, 16) || !gdn_host::aligned(k, 16) ||
       !gdn_host::aligned(v, 16) || !gdn_host::aligned(state_in, 16) || !gdn_host::aligned(state_out, 16))
     return fail(GDN_ERR_INVALID, "gdn_chunk_fwd: misaligned pointer");
-  if (n_tok > INT32_MAX / 2 || n_seqs > 65535 || Hv > 65535)
+  if (n_tok > INT32_MAX / 2 || n_seqs > 65535 || Hv > 65535 || max_chunks(n_seqs, n_tok, packed) * Hv > INT32_MAX ||
+      (DV / DVT) * Hv * n_seqs > INT32_MAX)
     return fail(GDN_ERR_UNSUPPORTED, "gdn_chunk_fwd: problem too large");
 
   ChunkParams p;
@@ -612,13 +629,11 @@ extern "C" int gdn_chunk_fwd(const void* q, const void* k, const void* v, int qk
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int64_t chunks = max_chunks(n_seqs, n_tok, packed);
   if (chunks > 0) {
-    hipLaunchKernelGGL(chunk_prep_kernel, dim3(static_cast<unsigned>(chunks), static_cast<unsigned>(Hv)),
-                       dim3(256), 0, st, p);
+    hipLaunchKernelGGL(chunk_prep_kernel, dim3(static_cast<unsigned>(chunks * Hv)), dim3(256), 0, st, p);
     const int rc = gdn_host::check_launch("gdn_chunk_fwd/prep");
     if (rc != GDN_OK) return rc;
   }
-  hipLaunchKernelGGL(chunk_scan_kernel,
-                     dim3(static_cast<unsigned>(DV / DVT), static_cast<unsigned>(Hv), static_cast<unsigned>(n_seqs)),
-                     dim3(256), 0, st, p);
+  hipLaunchKernelGGL(chunk_scan_kernel, dim3(static_cast<unsigned>((DV / DVT) * Hv * n_seqs)), dim3(256), 0, st,
+                     p);
   return gdn_host::check_launch("gdn_chunk_fwd/scan");
 }

@@ -85,9 +85,15 @@ __device__ __forceinline__ bool locate(const ProParams& p, int& seq, int64_t& st
   return false;
 }
 
-template <int D, int DT>
+// Read-only stand-ins for absent operands (loads stay unconditional).
+__device__ const float kZeros[4] = {};
+__device__ const uint8_t kOne = 1;
+
+// W32: conv taps are fp32 (else they share the io dtype DT).
+template <int D, int DT, bool W32>
 __global__ __launch_bounds__(256) void prologue_kernel(const ProParams p) {
   constexpr int CPL = D / 64;
+  constexpr int WDT = W32 ? GDN_DTYPE_F32 : DT;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int grp = blockIdx.x;
@@ -100,34 +106,49 @@ __global__ __launch_bounds__(256) void prologue_kernel(const ProParams p) {
 
   const int c0 = grp * D + lane * CPL;
   const int64_t C = p.C;
-  float w[KT][CPL];
-#pragma unroll
-  for (int j = 0; j < CPL; ++j)
-#pragma unroll
-    for (int i = 0; i < KT; ++i) w[i][j] = load_any(p.weight, p.w_dtype, (c0 + j) * KT + i);
 
+  // Issue every load first: the run's tokens (rows past the end re-read the
+  // last row and are never used), the window of the 3 inputs before the
+  // run, the taps.  A masked token reads as zero (mask byte as multiplier).
+  float xs[kRun][CPL];
+  float xm[kRun];
+  if (t_end > t_begin) {
+#pragma unroll
+    for (int u = 0; u < kRun; ++u) {
+      const int64_t tok = start + min(t_begin + u, t_end - 1);
+      load_vec<CPL, DT>(p.qkv, tok * C + c0, xs[u]);
+      const uint8_t* mp = p.mask != nullptr ? p.mask + tok : &kOne;
+      xm[u] = *mp != 0 ? 1.0f : 0.0f;
+    }
+  }
   // window[i] = X[t + i], X = concat(conv_state (KT-1 rows), masked qkv)
   float win[KT - 1][CPL];
 #pragma unroll
   for (int i = 0; i < KT - 1; ++i) {
     const int xi = t_begin + i;
+    const void* src;
+    float wm = 1.0f;
     if (xi < KT - 1) {
-      if (p.cs_in != nullptr) {
-        load_vec<CPL, DT>(p.cs_in, (static_cast<int64_t>(seq) * (KT - 1) + xi) * C + c0, win[i]);
-      } else {
-#pragma unroll
-        for (int j = 0; j < CPL; ++j) win[i][j] = 0.0f;
-      }
+      src = p.cs_in != nullptr
+                ? static_cast<const void*>(static_cast<const char*>(p.cs_in) +
+                                           ((static_cast<int64_t>(seq) * (KT - 1) + xi) * C + c0) *
+                                               (DT == GDN_DTYPE_F32 ? 4 : 2))
+                : static_cast<const void*>(kZeros);
     } else {
       const int64_t tok = start + xi - (KT - 1);
-      if (p.mask == nullptr || p.mask[tok] != 0) {
-        load_vec<CPL, DT>(p.qkv, tok * C + c0, win[i]);
-      } else {
-#pragma unroll
-        for (int j = 0; j < CPL; ++j) win[i][j] = 0.0f;
-      }
+      src = static_cast<const char*>(p.qkv) + (tok * C + c0) * (DT == GDN_DTYPE_F32 ? 4 : 2);
+      const uint8_t* mp = p.mask != nullptr ? p.mask + tok : &kOne;
+      wm = *mp != 0 ? 1.0f : 0.0f;
     }
+    load_vec<CPL, DT>(src, 0, win[i]);
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) win[i][j] *= wm;
   }
+  float w[KT][CPL];
+#pragma unroll
+  for (int j = 0; j < CPL; ++j)
+#pragma unroll
+    for (int i = 0; i < KT; ++i) w[i][j] = IO<WDT>::load1(p.weight, (c0 + j) * KT + i);
 
   // Head role of this channel group: 0 = q, 1 = k, 2 = v.
   const int role = grp < p.Hk ? 0 : (grp < 2 * p.Hk ? 1 : 2);
@@ -136,29 +157,18 @@ __global__ __launch_bounds__(256) void prologue_kernel(const ProParams p) {
   const int H = role == 2 ? p.Hv : p.Hk;
   const float post = role == 0 ? 1.0f / static_cast<float>(D) : rsqrtf(static_cast<float>(D));
 
-  // Load the whole run first (one memory latency), then walk it.
-  float xs[kRun][CPL];
-#pragma unroll
-  for (int u = 0; u < kRun; ++u) {
-    const int t = t_begin + u;
-    const int64_t tok = start + t;
-    if (t < t_end && (p.mask == nullptr || p.mask[tok] != 0)) {
-      load_vec<CPL, DT>(p.qkv, tok * C + c0, xs[u]);
-    } else {
-#pragma unroll
-      for (int j = 0; j < CPL; ++j) xs[u][j] = 0.0f;
-    }
-  }
 #pragma unroll
   for (int u = 0; u < kRun; ++u) {
     const int t = t_begin + u;
     if (t >= t_end) break;
     const int64_t tok = start + t;
     float o[CPL];
+    float x[CPL];
     float ss = 0.0f;
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
-      float acc = w[KT - 1][j] * xs[u][j];
+      x[j] = xs[u][j] * xm[u];
+      float acc = w[KT - 1][j] * x[j];
 #pragma unroll
       for (int i = 0; i < KT - 1; ++i) acc = fmaf(w[i][j], win[i][j], acc);
       o[j] = acc / (1.0f + expf(-acc));  // SiLU
@@ -169,7 +179,7 @@ __global__ __launch_bounds__(256) void prologue_kernel(const ProParams p) {
 #pragma unroll
       for (int j = 0; j < CPL; ++j) win[i][j] = win[i + 1][j];
 #pragma unroll
-    for (int j = 0; j < CPL; ++j) win[KT - 2][j] = xs[u][j];
+    for (int j = 0; j < CPL; ++j) win[KT - 2][j] = x[j];
     if (role != 2) {
       ss = wave_sum(ss);
       const float sc = rsqrtf(ss / static_cast<float>(D) + p.eps) * post;
@@ -227,6 +237,8 @@ extern "C" int gdn_conv_prologue(const void* qkv, int io_dtype, const void* conv
   if (Kt != KT) return fail(GDN_ERR_UNSUPPORTED, "gdn_conv_prologue: only Kt=4 is built (got %lld)", (long long)Kt);
   if (!gdn_host::dtype_ok(io_dtype) || !gdn_host::dtype_ok(w_dtype))
     return fail(GDN_ERR_INVALID, "gdn_conv_prologue: bad dtype code");
+  if (w_dtype != io_dtype && w_dtype != GDN_DTYPE_F32)
+    return fail(GDN_ERR_UNSUPPORTED, "gdn_conv_prologue: conv weight must be fp32 or the qkv dtype");
   if (qkv == nullptr || weight == nullptr || q_out == nullptr || k_out == nullptr || v_out == nullptr)
     return fail(GDN_ERR_INVALID, "gdn_conv_prologue: qkv, weight and q/k/v outputs are required");
   if (conv_state_out != nullptr && conv_state_out == conv_state_in)
@@ -271,8 +283,11 @@ extern "C" int gdn_conv_prologue(const void* qkv, int io_dtype, const void* conv
     grid.z = static_cast<unsigned>(B);
   }
   hipStream_t st = static_cast<hipStream_t>(stream);
-#define GDN_PRO_LAUNCH(D_, DT_) \
-  hipLaunchKernelGGL((prologue_kernel<D_, DT_>), grid, block, 0, st, p)
+#define GDN_PRO_LAUNCH(D_, DT_)                                                              \
+  if (w_dtype == GDN_DTYPE_F32)                                                             \
+    hipLaunchKernelGGL((prologue_kernel<D_, DT_, true>), grid, block, 0, st, p);          \
+  else                                                                                      \
+    hipLaunchKernelGGL((prologue_kernel<D_, DT_, false>), grid, block, 0, st, p)
 #define GDN_PRO_DT(D_)                                             \
   switch (io_dtype) {                                             \
     case GDN_DTYPE_BF16: GDN_PRO_LAUNCH(D_, GDN_DTYPE_BF16); break; \

@@ -91,120 +91,220 @@ __device__ __forceinline__ void load_token(const RecParams& p, int64_t tok, int 
   in.v = IO<DT>::load1(p.v, (tok * p.Hv + hv) * p.Dv + dv_c);
 }
 
-// PF: the inputs of token t+1 are loaded while token t computes (T > 1
-// launches: verify, commit, short prefill); T = 1 decode uses the leaner
-// PF = false body, which keeps occupancy for the state stream.
-template <int DK, int DT, int GF, bool PF>
-__global__ __launch_bounds__(256) void recurrent_kernel(const RecParams p) {
-  constexpr int EPL = DK / kLanesPerRow;  // fp32 state elements per lane
-  constexpr int NV = EPL / 4;             // float4 per lane
-  const int sub = threadIdx.x & (kLanesPerRow - 1);
-  const int dv = blockIdx.x * (blockDim.x / kLanesPerRow) + threadIdx.x / kLanesPerRow;
-  const bool row_ok = dv < p.Dv;
-  const int dv_c = row_ok ? dv : p.Dv - 1;  // loads use a valid row; stores check row_ok
-  const int hv = blockIdx.y;
-  const int row = blockIdx.z;
-  const int hk = hv / p.group;
+// Shared preamble of both kernels: row / head / sequence bookkeeping.
+struct RowCtx {
+  int sub, dv, dv_c, hv, hk, row, L, commit, steps;
+  bool row_ok, write_state, want_y;
+  int64_t tok0, srow, srow_c;
+};
 
-  int64_t tok0;
-  int L;
+template <int DK>
+__device__ __forceinline__ RowCtx row_ctx(const RecParams& p) {
+  RowCtx c;
+  c.sub = threadIdx.x & (kLanesPerRow - 1);
+  c.dv = blockIdx.x * (blockDim.x / kLanesPerRow) + threadIdx.x / kLanesPerRow;
+  c.row_ok = c.dv < p.Dv;
+  c.dv_c = c.row_ok ? c.dv : p.Dv - 1;  // loads use a valid row; stores check row_ok
+  c.hv = blockIdx.y;
+  c.row = blockIdx.z;
+  c.hk = c.hv / p.group;
   if (p.cu_seqlens != nullptr) {
-    tok0 = p.cu_seqlens[row];
-    L = p.cu_seqlens[row + 1] - p.cu_seqlens[row];
+    c.tok0 = p.cu_seqlens[c.row];
+    c.L = p.cu_seqlens[c.row + 1] - p.cu_seqlens[c.row];
   } else {
-    tok0 = static_cast<int64_t>(row) * p.T;
-    L = p.T;
+    c.tok0 = static_cast<int64_t>(c.row) * p.T;
+    c.L = p.T;
   }
-  bool write_state = p.state_out != nullptr;
-  int commit = L;
+  c.write_state = p.state_out != nullptr;
+  c.commit = c.L;
   if (p.commit_len != nullptr) {
-    const int c = p.commit_len[row];
-    if (c < 0) write_state = false;
-    commit = c < 0 ? 0 : (c < L ? c : L);
+    const int cl = p.commit_len[c.row];
+    if (cl < 0) c.write_state = false;
+    c.commit = cl < 0 ? 0 : (cl < c.L ? cl : c.L);
   }
-  const bool want_y = p.y != nullptr;
-  const bool need_all = want_y || (p.snapshots != nullptr);
-  const int steps = need_all ? L : (write_state ? commit : 0);
+  c.want_y = p.y != nullptr;
+  const bool need_all = c.want_y || (p.snapshots != nullptr);
+  c.steps = need_all ? c.L : (c.write_state ? c.commit : 0);
+  c.srow = ((static_cast<int64_t>(c.row) * p.Hv + c.hv) * p.Dv + c.dv) * DK;
+  c.srow_c = ((static_cast<int64_t>(c.row) * p.Hv + c.hv) * p.Dv + c.dv_c) * DK;
+  return c;
+}
 
-  // Token 0's inputs and the head parameters first, then the state.
-  TokenIn<EPL> cur;
-  if (steps > 0) {
-    if (PF && want_y) load_token<DK, DT, GF, true>(p, tok0, hv, hk, dv_c, sub, cur);
-    else load_token<DK, DT, GF, false>(p, tok0, hv, hk, dv_c, sub, cur);
-  }
-  float ea, db;
-  param_load<GF, DT>(p.ga, hv, ea, db);
-
-  const int64_t srow = ((static_cast<int64_t>(row) * p.Hv + hv) * p.Dv + dv) * DK;
-  const int64_t srow_c = ((static_cast<int64_t>(row) * p.Hv + hv) * p.Dv + dv_c) * DK;
-  const float* src = p.state_in != nullptr ? p.state_in + srow_c : kZeroRow;
-  float s[EPL];
+template <int DK>
+__device__ __forceinline__ void load_state(const RecParams& p, const RowCtx& c, float (&s)[DK / kLanesPerRow]) {
+  constexpr int NV = DK / kLanesPerRow / 4;
+  const float* src = p.state_in != nullptr ? p.state_in + c.srow_c : kZeroRow;
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
-    const f32x4 x = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(src + i * 32 + sub * 4));
+    const f32x4 x = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(src + i * 32 + c.sub * 4));
     s[4 * i] = x.x;
     s[4 * i + 1] = x.y;
     s[4 * i + 2] = x.z;
     s[4 * i + 3] = x.w;
   }
-  if (write_state && commit == 0 && row_ok) store_row<EPL>(p.state_out + srow, sub, s);
+}
 
-  for (int t = 0; t < steps; ++t) {
-    const int64_t tok = tok0 + t;
-    TokenIn<EPL> nxt;
-    if (PF && t + 1 < steps) {
-      if (want_y) load_token<DK, DT, GF, true>(p, tok + 1, hv, hk, dv_c, sub, nxt);
-      else load_token<DK, DT, GF, false>(p, tok + 1, hv, hk, dv_c, sub, nxt);
-    }
+// One token of the recurrence on a lane's slice of a state row:
+// S <- g S;  kv = S k;  S <- S + beta (v - kv) k^T  (kv summed over 8 lanes).
+template <int EPL>
+__device__ __forceinline__ void step_row(float (&s)[EPL], const float (&k)[EPL], float v, float g,
+                                          float beta) {
+  float kv = 0.0f;
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) {
+    s[e] *= g;
+    kv = fmaf(s[e], k[e], kv);
+  }
+  kv = sum8(kv);
+  const float delta = beta * (v - kv);
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) s[e] = fmaf(k[e], delta, s[e]);
+}
+
+// Decode body (one token per row, T = 1): no LDS, no barriers; the token's
+// inputs are issued ahead of the state stream so one latency covers both.
+template <int DK, int DT, int GF>
+__global__ __launch_bounds__(256) void recurrent_kernel(const RecParams p) {
+  constexpr int EPL = DK / kLanesPerRow;  // fp32 state elements per lane
+  constexpr int NV = EPL / 4;             // float4 per lane
+  const RowCtx c = row_ctx<DK>(p);
+
+  TokenIn<EPL> cur;
+  if (c.steps > 0) load_token<DK, DT, GF, false>(p, c.tok0, c.hv, c.hk, c.dv_c, c.sub, cur);
+  float ea, db;
+  param_load<GF, DT>(p.ga, c.hv, ea, db);
+  float s[EPL];
+  load_state<DK>(p, c, s);
+  if (c.write_state && c.commit == 0 && c.row_ok) store_row<EPL>(p.state_out + c.srow, c.sub, s);
+
+  for (int t = 0; t < c.steps; ++t) {
+    const int64_t tok = c.tok0 + t;
     float yv = 0.0f;
     if (cur.m != 0) {
       float g, beta;
       gate_transform<GF>(p.ga.mode, cur.gx, cur.gy, ea, db, g, beta);
-      float kv = 0.0f;
-#pragma unroll
-      for (int e = 0; e < EPL; ++e) {
-        s[e] *= g;
-        kv = fmaf(s[e], cur.k[e], kv);
-      }
-      kv = sum8(kv);
-      const float delta = beta * (cur.v - kv);
-#pragma unroll
-      for (int e = 0; e < EPL; ++e) s[e] = fmaf(cur.k[e], delta, s[e]);
-      if (want_y) {
+      step_row<EPL>(s, cur.k, cur.v, g, beta);
+      if (c.want_y) {
         float yp = 0.0f;
-        if (PF) {
+        const int64_t kq = (tok * p.Hk + c.hk) * DK + c.sub * 4;
 #pragma unroll
-          for (int e = 0; e < EPL; ++e) yp = fmaf(s[e], cur.q[e], yp);
-        } else {
-          const int64_t kq = (tok * p.Hk + hk) * DK + sub * 4;
+        for (int i = 0; i < NV; ++i) {
+          const f32x4 x = IO<DT>::load4(p.q, kq + i * 32);
+          yp = fmaf(s[4 * i], x.x, yp);
+          yp = fmaf(s[4 * i + 1], x.y, yp);
+          yp = fmaf(s[4 * i + 2], x.z, yp);
+          yp = fmaf(s[4 * i + 3], x.w, yp);
+        }
+        yv = sum8(yp);
+      }
+    }
+    if (c.want_y && c.row_ok && c.sub == 0) IO<DT>::store1(p.y, (tok * p.Hv + c.hv) * p.Dv + c.dv, yv);
+    if (p.snapshots != nullptr && c.row_ok) {
+      store_row<EPL>(p.snapshots + ((tok * p.Hv + c.hv) * p.Dv + c.dv) * DK, c.sub, s);
+    }
+    if (c.write_state && t + 1 == c.commit && c.row_ok) store_row<EPL>(p.state_out + c.srow, c.sub, s);
+    if (t + 1 < c.steps) load_token<DK, DT, GF, false>(p, tok + 1, c.hv, c.hk, c.dv_c, c.sub, cur);
+  }
+}
+
+// Multi-token body (verify, commit, packed rows): the workgroup stages a
+// tile of kTile tokens -- k and q as fp32, the transformed gates, the mask
+// and the v values of its rows -- in LDS, then every wave walks the tile
+// from LDS.  All of a tile's global loads are in flight together.
+constexpr int kTile = 16;
+constexpr int kMaxRowsPerWg = 32;
+
+template <int DK, int DT, int GF>
+__global__ __launch_bounds__(256) void recurrent_tile_kernel(const RecParams p) {
+  constexpr int EPL = DK / kLanesPerRow;
+  constexpr int NV = EPL / 4;
+  const RowCtx c = row_ctx<DK>(p);
+  const int tid = threadIdx.x;
+  const int rows_wg = blockDim.x / kLanesPerRow;
+  const int dv0 = blockIdx.x * rows_wg;
+
+  __shared__ __align__(16) float Kt[kTile][DK];
+  __shared__ __align__(16) float Qt[kTile][DK];
+  __shared__ float Vt[kTile][kMaxRowsPerWg];
+  __shared__ float Gt[kTile], Bt[kTile];
+  __shared__ uint8_t Mt[kTile];
+
+  float ea, db;
+  param_load<GF, DT>(p.ga, c.hv, ea, db);
+  float s[EPL];
+  load_state<DK>(p, c, s);
+  if (c.write_state && c.commit == 0 && c.row_ok) store_row<EPL>(p.state_out + c.srow, c.sub, s);
+
+  for (int t0 = 0; t0 < c.steps; t0 += kTile) {
+    const int n = min(kTile, c.steps - t0);
+    __syncthreads();  // the previous tile is consumed
+    // k and q: n tokens x DK, 4 elements per thread per pass
+    for (int i = tid; i < kTile * DK / 4; i += blockDim.x) {
+      const int j = i / (DK / 4), e = (i % (DK / 4)) * 4;
+      const int64_t tok = c.tok0 + t0 + min(j, n - 1);
+      const int64_t off = (tok * p.Hk + c.hk) * DK + e;
+      *reinterpret_cast<f32x4*>(&Kt[j][e]) = IO<DT>::load4(p.k, off);
+      if (c.want_y) *reinterpret_cast<f32x4*>(&Qt[j][e]) = IO<DT>::load4(p.q, off);
+    }
+    for (int i = tid; i < kTile * rows_wg; i += blockDim.x) {
+      const int j = i / rows_wg, r = i % rows_wg;
+      const int64_t tok = c.tok0 + t0 + min(j, n - 1);
+      Vt[j][r] = IO<DT>::load1(p.v, (tok * p.Hv + c.hv) * p.Dv + min(dv0 + r, p.Dv - 1));
+    }
+    if (tid < kTile) {
+      const int64_t tok = c.tok0 + t0 + min(tid, n - 1);
+      const uint8_t* mp = p.mask != nullptr ? p.mask + tok : &kActive;
+      float x, y, g, beta;
+      gate_load<GF, DT>(p.ga, tok * p.Hv + c.hv, x, y);
+      gate_transform<GF>(p.ga.mode, x, y, ea, db, g, beta);
+      Gt[tid] = g;
+      Bt[tid] = beta;
+      Mt[tid] = *mp;
+    }
+    __syncthreads();
+
+    const int rloc = threadIdx.x / kLanesPerRow;
+    for (int j = 0; j < n; ++j) {
+      const int t = t0 + j;
+      const int64_t tok = c.tok0 + t;
+      float yv = 0.0f;
+      if (Mt[j] != 0) {
+        float kf[EPL];
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+          const f32x4 x = *reinterpret_cast<const f32x4*>(&Kt[j][i * 32 + c.sub * 4]);
+          kf[4 * i] = x.x;
+          kf[4 * i + 1] = x.y;
+          kf[4 * i + 2] = x.z;
+          kf[4 * i + 3] = x.w;
+        }
+        step_row<EPL>(s, kf, Vt[j][rloc], Gt[j], Bt[j]);
+        if (c.want_y) {
+          float yp = 0.0f;
 #pragma unroll
           for (int i = 0; i < NV; ++i) {
-            const f32x4 x = IO<DT>::load4(p.q, kq + i * 32);
+            const f32x4 x = *reinterpret_cast<const f32x4*>(&Qt[j][i * 32 + c.sub * 4]);
             yp = fmaf(s[4 * i], x.x, yp);
             yp = fmaf(s[4 * i + 1], x.y, yp);
             yp = fmaf(s[4 * i + 2], x.z, yp);
             yp = fmaf(s[4 * i + 3], x.w, yp);
           }
+          yv = sum8(yp);
         }
-        yv = sum8(yp);
       }
-    }
-    if (want_y && row_ok && sub == 0) IO<DT>::store1(p.y, (tok * p.Hv + hv) * p.Dv + dv, yv);
-    if (p.snapshots != nullptr && row_ok) {
-      store_row<EPL>(p.snapshots + ((tok * p.Hv + hv) * p.Dv + dv) * DK, sub, s);
-    }
-    if (write_state && t + 1 == commit && row_ok) store_row<EPL>(p.state_out + srow, sub, s);
-    if (t + 1 < steps) {
-      if (PF) cur = nxt;
-      else load_token<DK, DT, GF, false>(p, tok + 1, hv, hk, dv_c, sub, cur);
+      if (c.want_y && c.row_ok && c.sub == 0) IO<DT>::store1(p.y, (tok * p.Hv + c.hv) * p.Dv + c.dv, yv);
+      if (p.snapshots != nullptr && c.row_ok) {
+        store_row<EPL>(p.snapshots + ((tok * p.Hv + c.hv) * p.Dv + c.dv) * DK, c.sub, s);
+      }
+      if (c.write_state && t + 1 == c.commit && c.row_ok) store_row<EPL>(p.state_out + c.srow, c.sub, s);
     }
   }
 }
 
 template <int DK, int DT, int GF>
-int launch_pf(bool pf, dim3 grid, dim3 block, hipStream_t st, const RecParams& p) {
-  if (pf) hipLaunchKernelGGL((recurrent_kernel<DK, DT, GF, true>), grid, block, 0, st, p);
-  else hipLaunchKernelGGL((recurrent_kernel<DK, DT, GF, false>), grid, block, 0, st, p);
+int launch_pf(bool tiled, dim3 grid, dim3 block, hipStream_t st, const RecParams& p) {
+  if (tiled) hipLaunchKernelGGL((recurrent_tile_kernel<DK, DT, GF>), grid, block, 0, st, p);
+  else hipLaunchKernelGGL((recurrent_kernel<DK, DT, GF>), grid, block, 0, st, p);
   return gdn_host::check_launch("gdn_recurrent");
 }
 
@@ -313,7 +413,7 @@ int run_recurrent(const gdn_recurrent_args* a) {
   dim3 grid(static_cast<unsigned>((a->Dv + rows_per_wg - 1) / rows_per_wg),
             static_cast<unsigned>(a->Hv), static_cast<unsigned>(a->B));
   hipStream_t st = static_cast<hipStream_t>(a->stream);
-  // Tokens per row > 1 (or packed rows): prefetch the next token's inputs.
+  // Tokens per row > 1 (or packed rows): stage token tiles in LDS.
   const bool pf = a->T > 1 || a->cu_seqlens != nullptr;
   switch (a->Dk) {
     case 64:
