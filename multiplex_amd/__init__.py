@@ -19,8 +19,19 @@ from .gated_delta import (
     prepare_recurrent,
 )
 from .conv import conv_state_commit, gdn_conv_prologue
+from .cache import ArraysCache, clone_ssm, merge_layer, restore_ssm, restore_ssm_snapshot, snapshot_ssm
+from .mixer import GatedDeltaNet, commit_verified, gated_rms_norm
 
 __all__ = [
+    "ArraysCache",
+    "GatedDeltaNet",
+    "clone_ssm",
+    "commit_verified",
+    "gated_rms_norm",
+    "merge_layer",
+    "restore_ssm",
+    "restore_ssm_snapshot",
+    "snapshot_ssm",
     "CHUNK_MIN_TOKENS",
     "chunk_workspace_bytes",
     "compute_beta",

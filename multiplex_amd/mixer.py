@@ -1,0 +1,163 @@
+"""GatedDeltaNet mixer on MI355X, callable like the one multiplex drives.
+
+The reference restates the mixer at ``multiplex/kernel/dflash.py:343-381``
+and the engine calls it as ``mixer(inputs, mask=None, cache=None)`` through
+``_GDNMixerProxy`` (``engine.py:151-170``), finding it by class name
+``GatedDeltaNet`` on ``layer.linear_attn`` (``engine.py:330-335``).  This
+module keeps that class name and call signature, with ``cache[0]`` the conv
+state and ``cache[1]`` the recurrent state.
+
+Data path per call:
+  in_proj_qkv / z / b / a      library GEMMs (hipBLASLt through torch)
+  gdn_conv_prologue            fused conv1d + SiLU + q/k norm (HIP)
+  gated_delta_update           recurrent or chunked kernel (HIP)
+  gated RMSNorm + out_proj     torch ops (the epilogue)
+
+Speculative rounds: ``mixer(inputs, mask, cache, verify=True)`` computes the
+outputs of all T draft tokens without touching ``cache`` and remembers what
+a commit needs; ``mixer.commit(cache, n_commit)`` then advances each row by
+its accepted length in one pass over the state.  This replaces the
+reference's snapshot -> verify -> restore -> replay sequence
+(``engine.py:300-359``, ``dflash.py:403-426``), which moves the state about
+four times as often.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+from typing import Optional, Sequence
+
+import torch
+import torch.nn.functional as F
+
+from .cache import ArraysCache
+from .conv import conv_state_commit, gdn_conv_prologue
+from .gated_delta import IntSeq, gated_delta_commit, gated_delta_update, gated_delta_verify
+
+__all__ = ["GatedDeltaNet", "gated_rms_norm", "commit_verified"]
+
+
+def gated_rms_norm(x: torch.Tensor, gate: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
+    """``rms_norm(x) * weight * silu(gate)`` over the last dim, in float32, cast back to x's dtype."""
+    xf = x.float()
+    xf = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)
+    return (xf * weight.float() * F.silu(gate.float())).to(x.dtype)
+
+
+@dataclass
+class _Pending:
+    qkv: torch.Tensor
+    k: torch.Tensor
+    v: torch.Tensor
+    a: torch.Tensor
+    b: torch.Tensor
+    mask: Optional[torch.Tensor]
+    conv_state: Optional[torch.Tensor]
+    cache: ArraysCache
+
+
+class GatedDeltaNet(torch.nn.Module):
+    """Gated DeltaNet mixer (Qwen3.5 / Qwen3-Next layout)."""
+
+    def __init__(self, hidden_size: int, num_k_heads: int = 16, num_v_heads: int = 32, head_k_dim: int = 128,
+                 head_v_dim: int = 128, conv_kernel_size: int = 4, rms_norm_eps: float = 1e-6,
+                 dtype: torch.dtype = torch.bfloat16, device=None):
+        super().__init__()
+        self.hidden_size = hidden_size
+        self.num_k_heads, self.num_v_heads = num_k_heads, num_v_heads
+        self.head_k_dim, self.head_v_dim = head_k_dim, head_v_dim
+        self.key_dim = num_k_heads * head_k_dim
+        self.value_dim = num_v_heads * head_v_dim
+        self.conv_dim = 2 * self.key_dim + self.value_dim
+        self.conv_kernel_size = conv_kernel_size
+        self.rms_norm_eps = rms_norm_eps
+        self.sharding_group = None
+        kw = dict(dtype=dtype, device=device)
+        self.in_proj_qkv = torch.nn.Linear(hidden_size, self.conv_dim, bias=False, **kw)
+        self.in_proj_z = torch.nn.Linear(hidden_size, self.value_dim, bias=False, **kw)
+        self.in_proj_b = torch.nn.Linear(hidden_size, num_v_heads, bias=False, **kw)
+        self.in_proj_a = torch.nn.Linear(hidden_size, num_v_heads, bias=False, **kw)
+        self.conv1d_weight = torch.nn.Parameter(torch.empty(self.conv_dim, conv_kernel_size, **kw))
+        self.A_log = torch.nn.Parameter(torch.empty(num_v_heads, dtype=torch.float32, device=device))
+        self.dt_bias = torch.nn.Parameter(torch.empty(num_v_heads, dtype=torch.float32, device=device))
+        self.norm_weight = torch.nn.Parameter(torch.ones(head_v_dim, **kw))
+        self.out_proj = torch.nn.Linear(self.value_dim, hidden_size, bias=False, **kw)
+        self._pending: Optional[_Pending] = None
+        self.reset_parameters()
+
+    @torch.no_grad()
+    def reset_parameters(self, generator: Optional[torch.Generator] = None) -> None:
+        """Random init with the benchmark's distributions (no checkpoints here)."""
+        for lin in (self.in_proj_qkv, self.in_proj_z, self.in_proj_b, self.in_proj_a, self.out_proj):
+            w = torch.randn(lin.weight.shape, generator=generator) / math.sqrt(lin.weight.shape[1])
+            lin.weight.copy_(w)
+        self.conv1d_weight.copy_(torch.randn(self.conv1d_weight.shape, generator=generator) * 0.1)
+        self.A_log.copy_(torch.rand(self.num_v_heads, generator=generator) * math.log(16.0))
+        self.dt_bias.copy_(torch.rand(self.num_v_heads, generator=generator) * 2 - 1)
+        self.norm_weight.fill_(1.0)
+
+    def _project(self, inputs):
+        B, S, _ = inputs.shape
+        qkv = self.in_proj_qkv(inputs)
+        z = self.in_proj_z(inputs).reshape(B, S, self.num_v_heads, self.head_v_dim)
+        b = self.in_proj_b(inputs)
+        a = self.in_proj_a(inputs)
+        return qkv, z, a, b
+
+    def _epilogue(self, y, z):
+        B, S = y.shape[:2]
+        out = gated_rms_norm(y, z, self.norm_weight, self.rms_norm_eps)
+        return self.out_proj(out.reshape(B, S, -1))
+
+    def forward(self, inputs: torch.Tensor, mask: Optional[torch.Tensor] = None,
+                cache: Optional[ArraysCache] = None, *, verify: bool = False) -> torch.Tensor:
+        """``inputs [B, S, hidden]`` -> ``[B, S, hidden]``; updates ``cache`` unless ``verify``."""
+        if self.sharding_group is not None:
+            raise NotImplementedError("tensor-parallel sharding of the mixer is not built")
+        qkv, z, a, b = self._project(inputs)
+        conv_state = cache[0] if cache is not None else None
+        state = cache[1] if cache is not None else None
+        q, k, v, new_cs = gdn_conv_prologue(
+            qkv, self.conv1d_weight, self.num_k_heads, self.num_v_heads, self.head_k_dim, self.head_v_dim,
+            conv_state, mask, eps=self.rms_norm_eps, write_conv_state=not verify)
+        if verify:
+            if cache is None:
+                raise ValueError("verify needs the cache the round will be committed into")
+            y, _ = gated_delta_verify(q, k, v, a, b, self.A_log, self.dt_bias, state, mask)
+            self._pending = _Pending(qkv, k, v, a, b, mask, conv_state, cache)
+        else:
+            y, new_state = gated_delta_update(q, k, v, a, b, self.A_log, self.dt_bias, state, mask)
+            if cache is not None:
+                cache[0] = new_cs
+                cache[1] = new_state
+        return self._epilogue(y, z)
+
+    def commit(self, cache: ArraysCache, n_commit: IntSeq) -> None:
+        """Advance every row of ``cache`` by its first ``n_commit[b]`` verified tokens.
+
+        State: one read and one in-place write per row (rows with a zero state
+        get a new tensor).  Conv state: ``concat(conv_state, qkv)[n : n+K-1]``.
+        """
+        p = self._pending
+        if p is None or p.cache is not cache:
+            raise ValueError("commit() must follow verify on the same cache")
+        state = cache[1]
+        if state is None:
+            new_state = gated_delta_commit(p.k, p.v, p.a, p.b, self.A_log, self.dt_bias, None, n_commit, p.mask)
+        else:
+            new_state = gated_delta_commit(p.k, p.v, p.a, p.b, self.A_log, self.dt_bias, state, n_commit, p.mask,
+                                           state_out=state)
+        cache[1] = new_state
+        cache[0] = conv_state_commit(p.conv_state, p.qkv, n_commit, p.mask, self.conv_kernel_size)
+        self._pending = None
+
+
+def commit_verified(mixers: Sequence[GatedDeltaNet], caches: Sequence[ArraysCache], n_commit: IntSeq) -> None:
+    """Engine-level rollback of a partially accepted round for every GDN layer.
+
+    The counterpart of ``Engine.rollback_ssm_replay`` (``engine.py:337-359``):
+    each layer commits its verified prefix instead of restore + replay.
+    """
+    for m, c in zip(mixers, caches):
+        m.commit(c, n_commit)

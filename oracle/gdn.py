@@ -61,6 +61,7 @@ __all__ = [
     "conv_prologue",
     "conv_state_commit",
     "bf16_round",
+    "mixer_forward",
 ]
 
 
@@ -337,3 +338,31 @@ def conv_state_commit(conv_input, n_commit, Kt):
         n = int(n_commit[b])
         out[b] = ci[b, n : n + Kt - 1]
     return out
+
+
+def mixer_forward(params, inputs, Hk, Hv, Dk, Dv, conv_state=None, state=None, mask=None,
+                  eps=1e-6, round_bf16=True):
+    """GatedDeltaNet mixer (``multiplex/kernel/dflash.py:343-381``), float64.
+
+    params: dict of float arrays ``in_proj_qkv [C,H]``, ``in_proj_z [Hv*Dv,H]``,
+    ``in_proj_b [Hv,H]``, ``in_proj_a [Hv,H]``, ``conv1d [C,K]``, ``A_log``,
+    ``dt_bias [Hv]``, ``norm [Dv]``, ``out_proj [H,Hv*Dv]``.  With
+    ``round_bf16`` the activations are rounded to bf16 where a bf16 model
+    materialises them (projection outputs, q/k/v, y, normed y, output).
+    Returns ``(out, new_conv_state, new_state)``.
+    """
+    r = bf16_round if round_bf16 else (lambda t: np.asarray(t, dtype=np.float64))
+    x = _f64(inputs)
+    B, S, _ = x.shape
+    qkv = r(x @ _f64(params["in_proj_qkv"]).T)
+    z = r(x @ _f64(params["in_proj_z"]).T).reshape(B, S, Hv, Dv)
+    b = r(x @ _f64(params["in_proj_b"]).T)
+    a = r(x @ _f64(params["in_proj_a"]).T)
+    q, k, v, new_cs, _ = conv_prologue(qkv, params["conv1d"], Hk, Hv, Dk, Dv, conv_state, mask, eps)
+    q, k, v = r(q), r(k), r(v)
+    y, new_state = gated_delta_update(q, k, v, a, b, params["A_log"], params["dt_bias"], state, mask)
+    y = r(y)
+    yn = y / np.sqrt(np.mean(y * y, axis=-1, keepdims=True) + eps) * _f64(params["norm"])
+    yn = r(yn * _silu(z))
+    out = r(yn.reshape(B, S, -1) @ _f64(params["out_proj"]).T)
+    return out, new_cs, new_state
