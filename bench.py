@@ -309,6 +309,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--decode-only", action="store_true", help="only the B=64 decode workload")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a plain 256 MiB device-to-device copy (counter calibration) and exit")
+    ap.add_argument("--prefill-only", action="store_true", help="only the T=4096 prefill workload")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -330,11 +333,29 @@ def main():
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
     timer = Timer(torch)
+    if args.copy_calibration:
+        # A plain streaming kernel of known size (read 256 MiB, write 256
+        # MiB): what HBM byte counters read for it calibrates their reading
+        # of the GDN kernels.  (A same-dtype copy_ would go to the DMA
+        # engines, not to a kernel the counters see.)
+        src = torch.randn(64 * 1024 * 1024, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(args.steps):
+            torch.mul(src, 2.0, out=dst)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes_per_launch": 2 * src.numel() * 4, "launches": args.steps}), flush=True)
+        return
+    if args.prefill_only:
+        p = bench_prefill(torch, mx, dev, timer, iters=args.steps)
+        print(json.dumps({"prefill_t4096": p}), flush=True)
+        return
 
     dec = bench_decode_b64(torch, mx, dev, args.steps, args.warmup, timer)
     step_bytes = decode_bytes(64)
     value = step_bytes / (dec["ms_per_step"] * 1e-3) / 1e9
-    achieved = step_bytes / (dec["kernel_ms"] * 1e-3) / 1e9
+    # One launch of the decode kernel per step: its average duration is the
+    # timed region's HIP-event span over the steps (back-to-back launches).
+    achieved = value
     configs = {}
     if not args.decode_only:
         configs["decode_b1"] = bench_decode_b1(torch, mx, dev, timer)
@@ -364,7 +385,8 @@ def main():
         "roofline": {
             "bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": read_traffic("decode_b64_traffic.txt"),
-            "kernel": "recurrent_kernel<128,bf16>", "kernel_ms": round(dec["kernel_ms"], 5),
+            "kernel": "recurrent_kernel<128,bf16,GF_IO_F32>", "kernel_ms": round(dec["ms_per_step"], 5),
+            "kernel_ms_event_pairs": round(dec["kernel_ms"], 5),
         },
         "cpu_baseline": None if base is None else {k: base[k] for k in ("value", "unit", "cores", "kind", "sample")},
         "prefill": None,
