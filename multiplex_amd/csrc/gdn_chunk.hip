@@ -13,11 +13,12 @@
 //               and Q K^T on MFMA, the decay masks, T = (I + A)^{-1} by a
 //               blocked (16x16) forward substitution in fp32.  Writes T and
 //               P as hi/lo bf16 planes (MFMA-ready) plus gamma, e, beta.
-//   chunk_scan  (grid: Dv/16 x Hv x seqs) -- sequential over the chunks of a
+//   chunk_scan  (8 workgroups per head)  -- sequential over the chunks of a
 //               sequence; a workgroup owns 16 rows of the state (rows are
 //               independent in the recurrence, so one head's chain is split
 //               over 8 workgroups).  Per chunk: X = [Q;K] S0^T, R, U = T R,
-//               Y = gamma X_Q + P U, S update, all on MFMA.  The operands of
+//               Y = gamma X_Q + P U, S update, all on MFMA, with one
+//               cross-wave exchange (the state) per chunk.  The operands of
 //               chunk c+1 are loaded into registers while chunk c computes.
 //
 // Precision: q, k, v are bf16 and enter MFMA exactly.  fp32 operands (S0, T,
@@ -46,10 +47,12 @@ constexpr size_t kOffTh = 0;                        // bf16[64][64]  hi((I + A)^
 constexpr size_t kOffTl = kOffTh + CH * CH * 2;     // bf16[64][64]  lo
 constexpr size_t kOffPh = kOffTl + CH * CH * 2;     // bf16[64][64]  hi(decayed Q K^T)
 constexpr size_t kOffPl = kOffPh + CH * CH * 2;     // bf16[64][64]  lo
-constexpr size_t kOffGam = kOffPl + CH * CH * 2;    // float[64]     exp(L_t)
+constexpr size_t kOffKT = kOffPl + CH * CH * 2;     // bf16[128][64] K^T (first v-head of a k-head only)
+constexpr size_t kOffGam = kOffKT + DK * CH * 2;    // float[64]     exp(L_t)
 constexpr size_t kOffE = kOffGam + CH * 4;          // float[64]     exp(L_C - L_t)
 constexpr size_t kOffBeta = kOffE + CH * 4;         // float[64]
-constexpr size_t kRecBytes = kOffBeta + CH * 4 + 256;  // 33792 (multiple of 256)
+constexpr size_t kRecBytes = kOffBeta + CH * 4;     // 49920 (multiple of 256)
+static_assert(kRecBytes % 256 == 0, "workspace records must stay 256-byte aligned");
 
 struct ChunkParams {
   const uint16_t* q;
@@ -86,10 +89,22 @@ __device__ __forceinline__ int kt_col(int dk, int tok) {
   return ((((tok >> 3) ^ (dk >> 3)) & 7) << 3) | (tok & 7);
 }
 
-// Component-wise "keep or zero" (a ternary on the uint4 struct would be
+// Component-wise "keep or zero" (a ternary on the u32x4 struct would be
 // lowered through memory).
-__device__ __forceinline__ uint4 keep_if(bool c, const uint4& a) {
-  return uint4{c ? a.x : 0u, c ? a.y : 0u, c ? a.z : 0u, c ? a.w : 0u};
+__device__ __forceinline__ u32x4 keep_if(bool c, const u32x4& a) {
+  return u32x4{c ? a.x : 0u, c ? a.y : 0u, c ? a.z : 0u, c ? a.w : 0u};
+}
+
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+
+// hi = bf16(x), lo = bf16(x - hi) for 4 values, as two 8-byte LDS stores
+// (packed converts: two values per v_cvt_pk_bf16_f32).
+__device__ __forceinline__ void split4_store(f32x4 x, uint16_t* hi, uint16_t* lo) {
+  const bf16x4 h = __builtin_convertvector(x, bf16x4);
+  const f32x4 hb = __builtin_convertvector(h, f32x4);
+  const bf16x4 l = __builtin_convertvector(x - hb, bf16x4);
+  *reinterpret_cast<bf16x4*>(hi) = h;
+  *reinterpret_cast<bf16x4*>(lo) = l;
 }
 
 __device__ __forceinline__ void pack4(uint16_t* dst, uint16_t a, uint16_t b, uint16_t c, uint16_t d) {
@@ -180,14 +195,14 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(const ChunkParams p) {
 
   // All row loads first (rows past the chunk's end read its last row and
   // are zeroed at the LDS store), then the LDS stores.
-  uint4 kr[4], qr[4];
+  u32x4 kr[4], qr[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int i = tid + 256 * j;
     const int r = i / (DK / 8), cc = (i % (DK / 8)) * 8;
     const int64_t off = ((tok0 + min(r, len - 1)) * p.Hk + hk) * DK + cc;
-    kr[j] = *reinterpret_cast<const uint4*>(p.k + off);
-    qr[j] = *reinterpret_cast<const uint4*>(p.q + off);
+    kr[j] = *reinterpret_cast<const u32x4*>(p.k + off);
+    qr[j] = *reinterpret_cast<const u32x4*>(p.q + off);
   }
   unsigned char* rec = p.ws + (static_cast<size_t>(c) * p.Hv + hv) * kRecBytes;
   if (wave == 0) {
@@ -212,8 +227,8 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(const ChunkParams p) {
   for (int j = 0; j < 4; ++j) {
     const int i = tid + 256 * j;
     const int r = i / (DK / 8), cc = (i % (DK / 8)) * 8;
-    *reinterpret_cast<uint4*>(&Ks[r][cc]) = keep_if(r < len, kr[j]);
-    *reinterpret_cast<uint4*>(&Qs[r][cc]) = keep_if(r < len, qr[j]);
+    *reinterpret_cast<u32x4*>(&Ks[r][cc]) = keep_if(r < len, kr[j]);
+    *reinterpret_cast<u32x4*>(&Qs[r][cc]) = keep_if(r < len, qr[j]);
   }
   for (int i = tid; i < CH * (CH + 1); i += 256) (&Ti[0][0])[i] = 0.0f;
   __syncthreads();
@@ -236,6 +251,25 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(const ChunkParams p) {
       const bf16x8 bk = lds8(&Ks[16 * j + lr][kc]);
       kk[j] = mfma16(ak, bk, kk[j]);
       qk[j] = mfma16(aq, bk, qk[j]);
+    }
+  }
+  // K^T [dk][token] for the scan's state update: one 16-byte group of 8
+  // tokens per store, written once per k-head (by its first v-head).
+  if (hv % p.group == 0) {
+    uint16_t* KTg = reinterpret_cast<uint16_t*>(rec + kOffKT);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int i = tid + 256 * j;            // 1024 groups: 128 dk x 8 token groups
+      const int dk = i >> 3, tg = (i & 7) * 8;
+      uint16_t h[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) h[e] = Ks[tg + e][dk];
+      u32x4 v;
+      v.x = h[0] | (static_cast<uint32_t>(h[1]) << 16);
+      v.y = h[2] | (static_cast<uint32_t>(h[3]) << 16);
+      v.z = h[4] | (static_cast<uint32_t>(h[5]) << 16);
+      v.w = h[6] | (static_cast<uint32_t>(h[7]) << 16);
+      *reinterpret_cast<u32x4*>(KTg + dk * CH + tg) = v;
     }
   }
   uint16_t* Ph = reinterpret_cast<uint16_t*>(rec + kOffPh);
@@ -314,238 +348,278 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(const ChunkParams p) {
 }
 
 // ------------------------------------------------------------ chunk_scan
+//
+// One workgroup (4 waves) owns a 16-row tile of one head's state and walks
+// that head's chunks.  Wave w produces the chunk's quantities for tokens
+// [16w, 16w+16) (X_K, X_Q, R, U, Y) and updates state columns
+// [32w, 32w+32).  Every MFMA operand that is specific to a wave -- its K, Q,
+// T and P rows, its K^T columns, its V values and gates -- is loaded from
+// global memory straight into registers in MFMA layout, and reloaded for the
+// next chunk right after its last use, so those loads overlap the rest of
+// the chunk.  LDS only carries what the waves exchange: the state (as hi/lo
+// bf16, the B operand of X_K / X_Q) and R^T, U^T, (eU)^T; three barriers
+// per chunk.
 
-// Per-thread registers holding one chunk's operands between the global
-// loads (issued a chunk ahead) and the LDS stores.
-struct Stage {
-  uint4 q[4], k[4];   // 64 x 128 bf16 each: 1024 uint4, 4 per thread
-  uint4 t[4];         // T hi (512 uint4) | T lo (512 uint4)
-  uint4 pm[4];        // P hi | P lo
-  uint4 v;            // 64 tokens x 16 state rows bf16 = 128 uint4 (threads < 128)
-  float g;            // thread < 64: gamma / e / beta of token tid
-  float e;
-  float b;
+// One wave's operands of one chunk (all in MFMA operand layouts).
+struct WaveOps {
+  bf16x8 k[4];          // K[16w + lr][32s + 8lq ..]    s = 0..3   (A of X_K)
+  bf16x8 q[4];          // Q rows, same layout                     (A of X_Q)
+  bf16x8 th[2], tl[2];  // T[16w + lr][32s + 8lq ..]    s = 0..1   (A of U)
+  bf16x8 ph[2], pl[2];  // P rows, same layout                     (A of P U)
+  bf16x8 kt[2][2];      // K^T[32w + 16j + lr][32s + 8lq ..]       (B of S update)
+  float v[4];           // V[16w + 4lq + i][dv0 + lr]
+  f32x4 g, b, e;        // gamma / beta / e of tokens 16w + 4lq + i
+  float gC;             // gamma of the chunk's last token
 };
 
-__device__ __forceinline__ void stage_load(const ChunkParams& p, Stage& s, int64_t t0, int clen,
-                                           const unsigned char* rec, int hk, int hv, int dv0, int tid) {
-  // Unconditional loads: rows past the chunk's end re-read its last row
-  // (zeroed at the LDS store), so no load waits inside a branch.
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int i = tid + 256 * j;
-    const int r = i >> 4, cc = (i & 15) * 8;
-    const int64_t off = ((t0 + min(r, clen - 1)) * p.Hk + hk) * DK + cc;
-    s.k[j] = *reinterpret_cast<const uint4*>(p.k + off);
-    s.q[j] = *reinterpret_cast<const uint4*>(p.q + off);
-    s.t[j] = reinterpret_cast<const uint4*>(rec + kOffTh)[i];
-    s.pm[j] = reinterpret_cast<const uint4*>(rec + kOffPh)[i];
-  }
-  const int vr = (tid & (2 * CH - 1)) >> 1;
-  s.v = *reinterpret_cast<const uint4*>(p.v + ((t0 + min(vr, clen - 1)) * p.Hv + hv) * DV + dv0 + (tid & 1) * 8);
-  s.g = reinterpret_cast<const float*>(rec + kOffGam)[tid & (CH - 1)];
-  s.e = reinterpret_cast<const float*>(rec + kOffE)[tid & (CH - 1)];
-  s.b = reinterpret_cast<const float*>(rec + kOffBeta)[tid & (CH - 1)];
+struct ChunkSrc {
+  const uint16_t* kq_row;  // K row (token) of this lane, at column 8lq: add s*32
+  const uint16_t* q_row;
+  const uint16_t* v_tok;   // V of token 16w + 4lq (+ i * Hv * DV), state row dv0 + lr
+  const unsigned char* rec;
+  const unsigned char* rec_k;
+  int v_stride;            // elements between tokens of V
+  int v_rows;              // valid rows among the lane's 4 V tokens
+};
+
+__device__ __forceinline__ ChunkSrc chunk_src(const ChunkParams& p, int64_t t0, int clen, const unsigned char* rec,
+                                             const unsigned char* rec_k, int hk, int hv, int dv0, int wave, int lr,
+                                             int lq) {
+  ChunkSrc c;
+  // rows past the chunk's end read its last row (finite; products with them
+  // are discarded or multiplied by a zero beta)
+  const int krow = min(16 * wave + lr, clen - 1);
+  c.kq_row = p.k + ((t0 + krow) * p.Hk + hk) * DK + 8 * lq;
+  c.q_row = p.q + ((t0 + krow) * p.Hk + hk) * DK + 8 * lq;
+  c.v_tok = p.v + (t0 * p.Hv + hv) * DV + dv0 + lr;
+  c.v_stride = p.Hv * DV;
+  c.v_rows = clen;
+  c.rec = rec;
+  c.rec_k = rec_k;
+  return c;
 }
 
+__device__ __forceinline__ void load_kq(WaveOps& o, const ChunkSrc& c) {
+  static_for<4>([&](auto s) {
+    o.k[s.value] = *reinterpret_cast<const bf16x8*>(c.kq_row + 32 * s.value);
+    o.q[s.value] = *reinterpret_cast<const bf16x8*>(c.q_row + 32 * s.value);
+  });
+}
+
+__device__ __forceinline__ void load_vg(WaveOps& o, const ChunkSrc& c, int wave, int lq) {
+  const int tb = 16 * wave + 4 * lq;
+  static_for<4>([&](auto i) {
+    o.v[i.value] = bf16_to_f32(c.v_tok[min(tb + i.value, c.v_rows - 1) * c.v_stride]);
+  });
+  o.g = *reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(c.rec + kOffGam) + tb);
+  o.b = *reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(c.rec + kOffBeta) + tb);
+}
+
+__device__ __forceinline__ void load_t(WaveOps& o, const ChunkSrc& c, int wave, int lr, int lq) {
+  const uint16_t* th = reinterpret_cast<const uint16_t*>(c.rec + kOffTh) + (16 * wave + lr) * CH + 8 * lq;
+  const uint16_t* tl = reinterpret_cast<const uint16_t*>(c.rec + kOffTl) + (16 * wave + lr) * CH + 8 * lq;
+  static_for<2>([&](auto s) {
+    o.th[s.value] = *reinterpret_cast<const bf16x8*>(th + 32 * s.value);
+    o.tl[s.value] = *reinterpret_cast<const bf16x8*>(tl + 32 * s.value);
+  });
+}
+
+__device__ __forceinline__ void load_e(WaveOps& o, const ChunkSrc& c, int wave, int lq) {
+  o.e = *reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(c.rec + kOffE) + 16 * wave + 4 * lq);
+}
+
+__device__ __forceinline__ void load_kt(WaveOps& o, const ChunkSrc& c, int wave, int lr, int lq) {
+  const uint16_t* kt = reinterpret_cast<const uint16_t*>(c.rec_k + kOffKT) + (32 * wave + lr) * CH + 8 * lq;
+  static_for<2>([&](auto j) {
+    static_for<2>([&](auto s) {
+      o.kt[j.value][s.value] = *reinterpret_cast<const bf16x8*>(kt + 16 * j.value * CH + 32 * s.value);
+    });
+  });
+  o.gC = reinterpret_cast<const float*>(c.rec + kOffGam)[CH - 1];
+}
+
+__device__ __forceinline__ void load_p(WaveOps& o, const ChunkSrc& c, int wave, int lr, int lq) {
+  const uint16_t* ph = reinterpret_cast<const uint16_t*>(c.rec + kOffPh) + (16 * wave + lr) * CH + 8 * lq;
+  const uint16_t* pl = reinterpret_cast<const uint16_t*>(c.rec + kOffPl) + (16 * wave + lr) * CH + 8 * lq;
+  static_for<2>([&](auto s) {
+    o.ph[s.value] = *reinterpret_cast<const bf16x8*>(ph + 32 * s.value);
+    o.pl[s.value] = *reinterpret_cast<const bf16x8*>(pl + 32 * s.value);
+  });
+}
+
+// Rank of sequence n when sequences are ordered by length, longest first
+// (ties by index); used to start the longest chains first.
+__device__ __forceinline__ int seq_by_rank(const ChunkParams& p, int rank) {
+  if (p.cu == nullptr || p.n_seqs > 256) return rank;
+  for (int n = 0; n < p.n_seqs; ++n) {
+    const int ln = p.cu[n + 1] - p.cu[n];
+    int r = 0;
+    for (int m = 0; m < p.n_seqs; ++m) {
+      const int lm = p.cu[m + 1] - p.cu[m];
+      r += (lm > ln) || (lm == ln && m < n);
+    }
+    if (r == rank) return n;
+  }
+  return rank;
+}
+
+constexpr int kTiles = DV / DVT;  // state-row tiles per head (8)
+constexpr int kXcds = 8;
+
 __global__ __launch_bounds__(256) void chunk_scan_kernel(const ChunkParams p) {
-  // work index = (seq * Hv + hv) * 8 + tile: the 8 state-row tiles of a head,
-  // which read the same Q/K/T/P stream, run on one XCD and share its L2.
-  const int w = xcd_work_index();
-  const int dv0 = (w % (DV / DVT)) * DVT;
-  const int hv = (w / (DV / DVT)) % p.Hv;
-  const int seq = w / ((DV / DVT) * p.Hv);
+  // Block b runs on XCD b % 8.  Heads (over all sequences, longest sequence
+  // first) are dealt to XCDs round-robin, and the 8 tiles of a head go to
+  // the head's XCD, where they share its K/T/P stream in L2.
+  const int blk = blockIdx.x;
+  const int xcd = blk % kXcds, r8 = blk / kXcds;
+  const int tile = r8 % kTiles;
+  const int head_rank = (r8 / kTiles) * kXcds + xcd;
+  if (head_rank >= p.n_seqs * p.Hv) return;
+  const int seq = seq_by_rank(p, head_rank / p.Hv);
+  const int hv = head_rank % p.Hv;
+  const int dv0 = tile * DVT;
   const int hk = hv / p.group;
+  const int hv_k = hk * p.group;  // the v-head whose record holds this k-head's K^T
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int lr = lane & 15, lq = lane >> 4, lg8 = lq * 8;
   const SeqRange sr = seq_range(p, seq);
   const int nch = n_chunks(sr.len);
 
-  __shared__ __align__(16) uint16_t Qs[CH][KP];
-  __shared__ __align__(16) uint16_t Ks[CH][KP];
-  __shared__ __align__(16) uint16_t KT[DK][CP];
-  __shared__ __align__(16) uint16_t Th[CH][CP], Tl[CH][CP], Ph[CH][CP], Pl[CH][CP];
-  __shared__ __align__(16) uint16_t Sh[DVT][KP], Sl[DVT][KP];
-  __shared__ __align__(16) uint16_t Rh[DVT][CP], Rl[DVT][CP];
-  __shared__ __align__(16) uint16_t Uh[DVT][CP], Ul[DVT][CP];
-  __shared__ __align__(16) uint16_t Eh[DVT][CP], El[DVT][CP];
-  __shared__ __align__(16) uint16_t Vs[CH][DVT];
-  __shared__ float Gs[CH], Es[CH], Bs[CH];
+  __shared__ __align__(16) uint16_t Sh[DVT][KP], Sl[DVT][KP];  // S0 [row][dk], hi / lo
+  __shared__ __align__(16) uint16_t Rh[DVT][CP], Rl[DVT][CP];  // R^T [row][token]
+  __shared__ __align__(16) uint16_t Uh[DVT][CP], Ul[DVT][CP];  // U^T
+  __shared__ __align__(16) uint16_t Eh[DVT][CP], El[DVT][CP];  // (diag(e) U)^T
 
-  // State tile (16 rows x 128): wave w holds columns [32w, 32w + 32) as two
-  // 16x16 MFMA accumulator tiles; lane: rows 4*lq + i, column 16*j + lr.
+  // This wave's 16 x 32 slice of the state: columns [32w, 32w+32) as two
+  // 16x16 accumulator tiles; lane holds rows 4*lq + i, column 16*j + lr.
   const int64_t srow0 = (static_cast<int64_t>(seq) * p.Hv + hv) * DV + dv0;
   f32x4 sacc[2];
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
+  for (int j = 0; j < 2; ++j)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int64_t idx = (srow0 + 4 * lq + i) * DK + 32 * wave + 16 * j + lr;
       sacc[j][i] = p.state_in != nullptr ? p.state_in[idx] : 0.0f;
     }
-  }
 
-  Stage st;
+  auto src_of = [&](int ci) {
+    const unsigned char* rec = p.ws + (static_cast<size_t>(sr.chunk0 + ci) * p.Hv + hv) * kRecBytes;
+    const unsigned char* rec_k = p.ws + (static_cast<size_t>(sr.chunk0 + ci) * p.Hv + hv_k) * kRecBytes;
+    return chunk_src(p, sr.tok0 + static_cast<int64_t>(ci) * CH, min(CH, sr.len - ci * CH), rec, rec_k, hk, hv,
+                     dv0, wave, lr, lq);
+  };
+  auto write_state = [&]() {
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        split_bf16(sacc[j][i], Sh[4 * lq + i][32 * wave + 16 * j + lr], Sl[4 * lq + i][32 * wave + 16 * j + lr]);
+  };
+
+  WaveOps o;
   if (nch > 0) {
-    const unsigned char* rec0 = p.ws + (static_cast<size_t>(sr.chunk0) * p.Hv + hv) * kRecBytes;
-    stage_load(p, st, sr.tok0, min(CH, sr.len), rec0, hk, hv, dv0, tid);
+    const ChunkSrc c0 = src_of(0);
+    load_kq(o, c0);
+    load_vg(o, c0, wave, lq);
+    load_t(o, c0, wave, lr, lq);
+    load_e(o, c0, wave, lq);
+    load_kt(o, c0, wave, lr, lq);
+    load_p(o, c0, wave, lr, lq);
   }
+  write_state();
+  const f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
 
   for (int ci = 0; ci < nch; ++ci) {
     const int64_t t0 = sr.tok0 + static_cast<int64_t>(ci) * CH;
     const int clen = min(CH, sr.len - ci * CH);
+    // the next chunk's operands (the last chunk reloads its own: no branches
+    // around the loads, so their waits are not forced early)
+    const ChunkSrc cn = src_of(min(ci + 1, nch - 1));
+    __syncthreads();  // state hi/lo of this chunk is in LDS
 
-    __syncthreads();  // the previous chunk is done with every LDS buffer
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int i = tid + 256 * j;
-      const int r = i >> 4, cc = (i & 15) * 8;
-      const uint4 kv = keep_if(r < clen, st.k[j]);
-      *reinterpret_cast<uint4*>(&Ks[r][cc]) = kv;
-      *reinterpret_cast<uint4*>(&Qs[r][cc]) = keep_if(r < clen, st.q[j]);
-      const uint32_t kw[4] = {kv.x, kv.y, kv.z, kv.w};
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        KT[cc + e][kt_col(cc + e, r)] = static_cast<uint16_t>(kw[e >> 1] >> ((e & 1) * 16));
-      }
-      // T / P planes: rows 0..31 of hi come from i < 512, lo from i >= 512
-      const int pr = (i & 511) >> 3, pc = (i & 7) * 8;
-      if (i < 512) {
-        *reinterpret_cast<uint4*>(&Th[pr][pc]) = st.t[j];
-        *reinterpret_cast<uint4*>(&Ph[pr][pc]) = st.pm[j];
-      } else {
-        *reinterpret_cast<uint4*>(&Tl[pr][pc]) = st.t[j];
-        *reinterpret_cast<uint4*>(&Pl[pr][pc]) = st.pm[j];
-      }
-    }
-    if (tid < 2 * CH) *reinterpret_cast<uint4*>(&Vs[tid >> 1][(tid & 1) * 8]) = keep_if((tid >> 1) < clen, st.v);
-    if (tid < CH) {
-      Gs[tid] = st.g;
-      Es[tid] = st.e;
-      Bs[tid] = st.b;
-    }
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        split_bf16(sacc[j][i], Sh[4 * lq + i][32 * wave + 16 * j + lr],
-                   Sl[4 * lq + i][32 * wave + 16 * j + lr]);
-      }
-    }
-    // Prefetch the next chunk while this one computes.
-    if (ci + 1 < nch) {
-      const unsigned char* recn = p.ws + (static_cast<size_t>(sr.chunk0 + ci + 1) * p.Hv + hv) * kRecBytes;
-      stage_load(p, st, t0 + CH, min(CH, sr.len - (ci + 1) * CH), recn, hk, hv, dv0, tid);
-    }
-    __syncthreads();
+    // ---- X_K = K S0^T and X_Q = Q S0^T for this wave's 16 tokens
+    f32x4 xk0 = z, xk1 = z, xq0 = z, xq1 = z;
+    static_for<4>([&](auto s) {
+      const int kc = 32 * s.value + lg8;
+      const bf16x8 bh = lds8(&Sh[lr][kc]);
+      const bf16x8 bl = lds8(&Sl[lr][kc]);
+      xk0 = mfma16(o.k[s.value], bh, xk0);
+      xk1 = mfma16(o.k[s.value], bl, xk1);
+      xq0 = mfma16(o.q[s.value], bh, xq0);
+      xq1 = mfma16(o.q[s.value], bl, xq1);
+    });
+    load_kq(o, cn);
 
-    // X_K = K S0^T first (it feeds the chain), then X_Q = Q S0^T.
-    f32x4 xk0 = {0.0f, 0.0f, 0.0f, 0.0f}, xk1 = xk0, xq = xk0;
-#pragma unroll
-    for (int s = 0; s < DK / 32; ++s) {
-      const int kc = s * 32 + lg8;
-      const bf16x8 ak = lds8(&Ks[16 * wave + lr][kc]);
-      xk0 = mfma16(ak, lds8(&Sh[lr][kc]), xk0);
-      xk1 = mfma16(ak, lds8(&Sl[lr][kc]), xk1);
-    }
-#pragma unroll
-    for (int s = 0; s < DK / 32; ++s) {
-      const int kc = s * 32 + lg8;
-      const bf16x8 aq = lds8(&Qs[16 * wave + lr][kc]);
-      xq = mfma16(aq, lds8(&Sh[lr][kc]), xq);
-      xq = mfma16(aq, lds8(&Sl[lr][kc]), xq);
-    }
-    // R = beta (V - gamma X_K), stored transposed: R^T[state row][token];
-    // a lane's 4 tokens are adjacent, so each plane takes one 8-byte store.
+    // ---- R = beta (V - gamma X_K) -> R^T
     {
-      uint16_t rh[4], rl[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int t = 16 * wave + 4 * lq + i;
-        const float vv = bf16_to_f32(Vs[t][lr]);
-        split_bf16(Bs[t] * (vv - Gs[t] * (xk0[i] + xk1[i])), rh[i], rl[i]);
-      }
-      const int t0l = 16 * wave + 4 * lq;
-      pack4(&Rh[lr][t0l], rh[0], rh[1], rh[2], rh[3]);
-      pack4(&Rl[lr][t0l], rl[0], rl[1], rl[2], rl[3]);
+      f32x4 r;
+      static_for<4>([&](auto i) { r[i.value] = o.b[i.value] * (o.v[i.value] - o.g[i.value] * (xk0[i.value] + xk1[i.value])); });
+      split4_store(r, &Rh[lr][16 * wave + 4 * lq], &Rl[lr][16 * wave + 4 * lq]);
     }
-    __syncthreads();
+    const f32x4 gam = o.g;  // kept for Y
+    load_vg(o, cn, wave, lq);
+    __syncthreads();  // R^T complete
 
-    // U = T R: wave w -> tokens 16w..16w+15.
-    f32x4 u0 = {0.0f, 0.0f, 0.0f, 0.0f}, u1 = u0;
-#pragma unroll
-    for (int s = 0; s < CH / 32; ++s) {
-      const int kc = s * 32 + lg8;
-      const bf16x8 ah = lds8(&Th[16 * wave + lr][kc]);
+    // ---- U = T R for this wave's 16 tokens
+    f32x4 u0 = z, u1 = z;
+    static_for<2>([&](auto s) {
+      const int kc = 32 * s.value + lg8;
       const bf16x8 bh = lds8(&Rh[lr][kc]);
-      u0 = mfma16(ah, bh, u0);
-      u1 = mfma16(ah, lds8(&Rl[lr][kc]), u1);
-      u1 = mfma16(lds8(&Tl[16 * wave + lr][kc]), bh, u1);
-    }
+      u0 = mfma16(o.th[s.value], bh, u0);
+      u1 = mfma16(o.th[s.value], lds8(&Rl[lr][kc]), u1);
+      u1 = mfma16(o.tl[s.value], bh, u1);
+    });
+    load_t(o, cn, wave, lr, lq);
     {
-      uint16_t uh[4], ul[4], eh[4], el[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int t = 16 * wave + 4 * lq + i;
-        const float uv = u0[i] + u1[i];
-        split_bf16(uv, uh[i], ul[i]);
-        split_bf16(Es[t] * uv, eh[i], el[i]);
-      }
-      const int t0l = 16 * wave + 4 * lq;
-      pack4(&Uh[lr][t0l], uh[0], uh[1], uh[2], uh[3]);
-      pack4(&Ul[lr][t0l], ul[0], ul[1], ul[2], ul[3]);
-      pack4(&Eh[lr][t0l], eh[0], eh[1], eh[2], eh[3]);
-      pack4(&El[lr][t0l], el[0], el[1], el[2], el[3]);
+      const f32x4 uv = u0 + u1;
+      split4_store(uv, &Uh[lr][16 * wave + 4 * lq], &Ul[lr][16 * wave + 4 * lq]);
+      split4_store(o.e * uv, &Eh[lr][16 * wave + 4 * lq], &El[lr][16 * wave + 4 * lq]);
     }
-    __syncthreads();
+    load_e(o, cn, wave, lq);
+    __syncthreads();  // U^T, (eU)^T complete
 
-    // S = gamma_C S0 + (diag(e) U)^T K: wave w -> state columns [32w, 32w+32).
-    const float gC = Gs[CH - 1];
+    // ---- S = gamma_C S0 + (diag(e) U)^T K on this wave's 32 columns
 #pragma unroll
-    for (int j = 0; j < 2; ++j) sacc[j] *= gC;
-#pragma unroll
-    for (int s = 0; s < CH / 32; ++s) {
-      const int kc = s * 32 + lg8;
+    for (int j = 0; j < 2; ++j) sacc[j] *= o.gC;
+    static_for<2>([&](auto s) {
+      const int kc = 32 * s.value + lg8;
       const bf16x8 eh = lds8(&Eh[lr][kc]);
       const bf16x8 el = lds8(&El[lr][kc]);
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int dk = 32 * wave + 16 * j + lr;
-        const bf16x8 bk = lds8(&KT[dk][kt_col(dk, kc)]);
-        sacc[j] = mfma16(eh, bk, sacc[j]);
-        sacc[j] = mfma16(el, bk, sacc[j]);
-      }
-    }
+      static_for<2>([&](auto j) {
+        sacc[j.value] = mfma16(eh, o.kt[j.value][s.value], sacc[j.value]);
+        sacc[j.value] = mfma16(el, o.kt[j.value][s.value], sacc[j.value]);
+      });
+    });
+    load_kt(o, cn, wave, lr, lq);
 
-    // Y = gamma X_Q + P U for this wave's 16 tokens.
-    f32x4 y0 = {0.0f, 0.0f, 0.0f, 0.0f}, y1 = y0;
-#pragma unroll
-    for (int s = 0; s < CH / 32; ++s) {
-      const int kc = s * 32 + lg8;
-      const bf16x8 ah = lds8(&Ph[16 * wave + lr][kc]);
-      const bf16x8 bh = lds8(&Uh[lr][kc]);
-      y0 = mfma16(ah, bh, y0);
-      y1 = mfma16(ah, lds8(&Ul[lr][kc]), y1);
-      y1 = mfma16(lds8(&Pl[16 * wave + lr][kc]), bh, y1);
-    }
+    // ---- Y = gamma X_Q + P U for this wave's 16 tokens
+    f32x4 y0 = z, y1 = z;
+    static_for<2>([&](auto s) {
+      const int kc = 32 * s.value + lg8;
+      const bf16x8 uh = lds8(&Uh[lr][kc]);
+      y0 = mfma16(o.ph[s.value], uh, y0);
+      y1 = mfma16(o.ph[s.value], lds8(&Ul[lr][kc]), y1);
+      y1 = mfma16(o.pl[s.value], uh, y1);
+    });
+    load_p(o, cn, wave, lr, lq);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int t = 16 * wave + 4 * lq + i;
       if (t < clen) {
-        const float yv = fmaf(Gs[t], xq[i], y0[i] + y1[i]);
+        const float yv = fmaf(gam[i], xq0[i] + xq1[i], y0[i] + y1[i]);
         p.y[((t0 + t) * p.Hv + hv) * DV + dv0 + lr] = f32_to_bf16(yv);
       }
     }
+    write_state();  // every wave read S0 before the R^T barrier
   }
 
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
+  for (int j = 0; j < 2; ++j)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int64_t idx = (srow0 + 4 * lq + i) * DK + 32 * wave + 16 * j + lr;
       p.state_out[idx] = sacc[j][i];
     }
-  }
 }
 
 int64_t max_chunks(int64_t n_seqs, int64_t n_tok, bool packed) {
@@ -601,7 +675,7 @@ extern "C" int gdn_chunk_fwd(const void* q, const void* k, const void* v, int qk
       !gdn_host::aligned(v, 16) || !gdn_host::aligned(state_in, 16) || !gdn_host::aligned(state_out, 16))
     return fail(GDN_ERR_INVALID, "gdn_chunk_fwd: misaligned pointer");
   if (n_tok > INT32_MAX / 2 || n_seqs > 65535 || Hv > 65535 || max_chunks(n_seqs, n_tok, packed) * Hv > INT32_MAX ||
-      (DV / DVT) * Hv * n_seqs > INT32_MAX)
+      (DV / DVT) * (Hv * n_seqs + 8) > INT32_MAX)
     return fail(GDN_ERR_UNSUPPORTED, "gdn_chunk_fwd: problem too large");
 
   ChunkParams p;
@@ -633,7 +707,8 @@ extern "C" int gdn_chunk_fwd(const void* q, const void* k, const void* v, int qk
     const int rc = gdn_host::check_launch("gdn_chunk_fwd/prep");
     if (rc != GDN_OK) return rc;
   }
-  hipLaunchKernelGGL(chunk_scan_kernel, dim3(static_cast<unsigned>((DV / DVT) * Hv * n_seqs)), dim3(256), 0, st,
-                     p);
+  const int64_t heads = n_seqs * Hv;
+  const int64_t scan_blocks = kTiles * kXcds * ((heads + kXcds - 1) / kXcds);
+  hipLaunchKernelGGL(chunk_scan_kernel, dim3(static_cast<unsigned>(scan_blocks)), dim3(256), 0, st, p);
   return gdn_host::check_launch("gdn_chunk_fwd/scan");
 }

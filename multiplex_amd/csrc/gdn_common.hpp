@@ -6,6 +6,7 @@
 #include <cstdint>
 #include <cstdio>
 #include <string>
+#include <type_traits>
 
 #include "../../include/gdn.h"
 
@@ -15,6 +16,9 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
 typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
+// Native 128-bit integer vector: plain loads/stores, unlike HIP's uint4
+// struct, whose copies lower to memcpy and keep values out of registers.
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 // ---------------------------------------------------------------- dtypes
 
@@ -22,12 +26,10 @@ __device__ __forceinline__ float bf16_to_f32(uint16_t h) {
   return __uint_as_float(static_cast<uint32_t>(h) << 16);
 }
 
-// Round-to-nearest-even fp32 -> bf16 (NaN stays NaN).
+// Round-to-nearest-even fp32 -> bf16 (NaN stays NaN): gfx950's
+// v_cvt_pk_bf16_f32, one instruction, no branches.
 __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return static_cast<uint16_t>(u >> 16);
+  return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
 }
 
 __device__ __forceinline__ float f16_to_f32(uint16_t h) {
@@ -203,6 +205,25 @@ __device__ __forceinline__ void load_log_gates(const GateArgs& ga, int64_t gi, i
     logg = -expf(al) * softplus_f(x + db);
     beta = sigmoid_f(y);
   }
+}
+
+// ------------------------------------------------------------- unrolling
+
+// static_for<N>(f) calls f(std::integral_constant<int, i>) for i = 0..N-1.
+// Indexing register-staged arrays with these constants keeps them in VGPRs:
+// the alloca promotion pass runs before loop unrolling, and a loop index
+// would make it move such arrays to LDS or scratch.
+template <int I, int N, typename F>
+__device__ __forceinline__ void static_for_impl(F&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    static_for_impl<I + 1, N>(f);
+  }
+}
+
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl<0, N>(f);
 }
 
 // ------------------------------------------------------- cross-lane sums
