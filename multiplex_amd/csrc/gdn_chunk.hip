@@ -42,16 +42,30 @@ constexpr int DVT = 16;     // state rows per scan workgroup
 constexpr int KP = DK + 8;  // padded LDS row (bf16) for 128-wide rows
 constexpr int CP = CH + 8;  // padded LDS row (bf16) for 64-wide rows
 
-// Workspace record per (chunk, v-head).
-constexpr size_t kOffTh = 0;                        // bf16[64][64]  hi((I + A)^{-1})
-constexpr size_t kOffTl = kOffTh + CH * CH * 2;     // bf16[64][64]  lo
-constexpr size_t kOffPh = kOffTl + CH * CH * 2;     // bf16[64][64]  hi(decayed Q K^T)
-constexpr size_t kOffPl = kOffPh + CH * CH * 2;     // bf16[64][64]  lo
-constexpr size_t kOffKT = kOffPl + CH * CH * 2;     // bf16[128][64] K^T (first v-head of a k-head only)
-constexpr size_t kOffGam = kOffKT + DK * CH * 2;    // float[64]     exp(L_t)
-constexpr size_t kOffE = kOffGam + CH * 4;          // float[64]     exp(L_C - L_t)
+// Workspace record per (chunk, v-head).  Matrices are stored as MFMA
+// fragments: the 16 x 32 block (row block rb, column block cb) of a matrix
+// with n column blocks is 1 KB at ((rb * n + cb) * 64 + lane) * 16 bytes, lane
+// (r % 16) + 16 * ((c % 32) / 8) holding columns c .. c+7 of row r -- exactly
+// the A/B operand registers of a 16x16x32 MFMA, so a wave loads a fragment
+// with one contiguous 1 KB read.
+constexpr size_t kOffTh = 0;                        // bf16 64x64   hi((I + A)^{-1})
+constexpr size_t kOffTl = kOffTh + CH * CH * 2;     // bf16 64x64   lo
+constexpr size_t kOffPh = kOffTl + CH * CH * 2;     // bf16 64x64   hi(decayed Q K^T)
+constexpr size_t kOffPl = kOffPh + CH * CH * 2;     // bf16 64x64   lo
+// K^T, K and Q are per k-head: written into the record of its first v-head.
+constexpr size_t kOffKT = kOffPl + CH * CH * 2;     // bf16 128x64  K^T
+constexpr size_t kOffKf = kOffKT + DK * CH * 2;     // bf16 64x128  K
+constexpr size_t kOffQf = kOffKf + CH * DK * 2;     // bf16 64x128  Q
+constexpr size_t kOffGam = kOffQf + CH * DK * 2;    // float[64]    exp(L_t)
+constexpr size_t kOffE = kOffGam + CH * 4;          // float[64]    exp(L_C - L_t)
 constexpr size_t kOffBeta = kOffE + CH * 4;         // float[64]
-constexpr size_t kRecBytes = kOffBeta + CH * 4;     // 49920 (multiple of 256)
+constexpr size_t kRecBytes = kOffBeta + CH * 4;     // 82688 (multiple of 256)
+
+// Element offset of (r, c) in the fragment layout of a matrix with ncb
+// 32-column blocks.
+__host__ __device__ constexpr int frag_elem(int r, int c, int ncb) {
+  return (((r >> 4) * ncb + (c >> 5)) * 64 + (r & 15) + 16 * ((c & 31) >> 3)) * 8 + (c & 7);
+}
 static_assert(kRecBytes % 256 == 0, "workspace records must stay 256-byte aligned");
 
 struct ChunkParams {
@@ -82,13 +96,6 @@ __device__ __forceinline__ bf16x8 lds8(const uint16_t* p) {
   return *reinterpret_cast<const bf16x8*>(p);
 }
 
-// K^T in LDS is stored with its 16-byte token groups XOR-swizzled by the
-// row's dk group, so the column-wise (transposing) stores of 16 threads hit
-// different banks; readers apply the same swizzle to whole 16-byte groups.
-__device__ __forceinline__ int kt_col(int dk, int tok) {
-  return ((((tok >> 3) ^ (dk >> 3)) & 7) << 3) | (tok & 7);
-}
-
 // Component-wise "keep or zero" (a ternary on the u32x4 struct would be
 // lowered through memory).
 __device__ __forceinline__ u32x4 keep_if(bool c, const u32x4& a) {
@@ -96,20 +103,26 @@ __device__ __forceinline__ u32x4 keep_if(bool c, const u32x4& a) {
 }
 
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
-// hi = bf16(x), lo = bf16(x - hi) for 4 values, as two 8-byte LDS stores
-// (packed converts: two values per v_cvt_pk_bf16_f32).
-__device__ __forceinline__ void split4_store(f32x4 x, uint16_t* hi, uint16_t* lo) {
-  const bf16x4 h = __builtin_convertvector(x, bf16x4);
-  const f32x4 hb = __builtin_convertvector(h, f32x4);
-  const bf16x4 l = __builtin_convertvector(x - hb, bf16x4);
-  *reinterpret_cast<bf16x4*>(hi) = h;
-  *reinterpret_cast<bf16x4*>(lo) = l;
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+// Two floats -> packed bf16 pair (one v_cvt_pk_bf16_f32, round to nearest even).
+__device__ __forceinline__ uint32_t pk_bf16(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{a, b}), bf16x2));
 }
 
-__device__ __forceinline__ void pack4(uint16_t* dst, uint16_t a, uint16_t b, uint16_t c, uint16_t d) {
-  u16x4 v = {a, b, c, d};
-  *reinterpret_cast<u16x4*>(dst) = v;
+// hi = bf16(x), lo = bf16(x - hi) for 4 values, as two 8-byte LDS stores.
+// The residual takes hi back from the packed pair (shift / mask) rather than
+// converting each value a second time.
+__device__ __forceinline__ void split4_store(f32x4 x, uint16_t* hi, uint16_t* lo) {
+  const uint32_t h01 = pk_bf16(x[0], x[1]), h23 = pk_bf16(x[2], x[3]);
+  const float r0 = x[0] - __builtin_bit_cast(float, h01 << 16);
+  const float r1 = x[1] - __builtin_bit_cast(float, h01 & 0xffff0000u);
+  const float r2 = x[2] - __builtin_bit_cast(float, h23 << 16);
+  const float r3 = x[3] - __builtin_bit_cast(float, h23 & 0xffff0000u);
+  *reinterpret_cast<u32x2*>(hi) = u32x2{h01, h23};
+  *reinterpret_cast<u32x2*>(lo) = u32x2{pk_bf16(r0, r1), pk_bf16(r2, r3)};
 }
 
 struct SeqRange {
@@ -223,12 +236,18 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(const ChunkParams p) {
     reinterpret_cast<float*>(rec + kOffE)[lane] = expf(static_cast<float>(LC - L));
     reinterpret_cast<float*>(rec + kOffBeta)[lane] = bt;
   }
+  const bool first_v = hv % p.group == 0;  // writes the k-head's K^T, K and Q
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int i = tid + 256 * j;
     const int r = i / (DK / 8), cc = (i % (DK / 8)) * 8;
-    *reinterpret_cast<u32x4*>(&Ks[r][cc]) = keep_if(r < len, kr[j]);
-    *reinterpret_cast<u32x4*>(&Qs[r][cc]) = keep_if(r < len, qr[j]);
+    const u32x4 kv = keep_if(r < len, kr[j]), qv = keep_if(r < len, qr[j]);
+    *reinterpret_cast<u32x4*>(&Ks[r][cc]) = kv;
+    *reinterpret_cast<u32x4*>(&Qs[r][cc]) = qv;
+    if (first_v) {
+      *reinterpret_cast<u32x4*>(reinterpret_cast<uint16_t*>(rec + kOffKf) + frag_elem(r, cc, DK / 32)) = kv;
+      *reinterpret_cast<u32x4*>(reinterpret_cast<uint16_t*>(rec + kOffQf) + frag_elem(r, cc, DK / 32)) = qv;
+    }
   }
   for (int i = tid; i < CH * (CH + 1); i += 256) (&Ti[0][0])[i] = 0.0f;
   __syncthreads();
@@ -255,7 +274,7 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(const ChunkParams p) {
   }
   // K^T [dk][token] for the scan's state update: one 16-byte group of 8
   // tokens per store, written once per k-head (by its first v-head).
-  if (hv % p.group == 0) {
+  if (first_v) {
     uint16_t* KTg = reinterpret_cast<uint16_t*>(rec + kOffKT);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -269,7 +288,7 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(const ChunkParams p) {
       v.y = h[2] | (static_cast<uint32_t>(h[3]) << 16);
       v.z = h[4] | (static_cast<uint32_t>(h[5]) << 16);
       v.w = h[6] | (static_cast<uint32_t>(h[7]) << 16);
-      *reinterpret_cast<u32x4*>(KTg + dk * CH + tg) = v;
+      *reinterpret_cast<u32x4*>(KTg + frag_elem(dk, tg, CH / 32)) = v;
     }
   }
   uint16_t* Ph = reinterpret_cast<uint16_t*>(rec + kOffPh);
@@ -284,8 +303,8 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(const ChunkParams p) {
       As[t][col] = col < t ? Bs[t] * dec * kk[j][i] : 0.0f;
       uint16_t h, l;
       split_bf16(dec * qk[j][i], h, l);
-      Ph[t * CH + col] = h;
-      Pl[t * CH + col] = l;
+      Ph[frag_elem(t, col, CH / 32)] = h;
+      Pl[frag_elem(t, col, CH / 32)] = l;
     }
   }
   __syncthreads();
@@ -339,11 +358,15 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(const ChunkParams p) {
   }
   uint16_t* Th = reinterpret_cast<uint16_t*>(rec + kOffTh);
   uint16_t* Tl = reinterpret_cast<uint16_t*>(rec + kOffTl);
-  for (int i = tid; i < CH * CH; i += 256) {
-    uint16_t h, l;
-    split_bf16(Ti[i / CH][i % CH], h, l);
-    Th[i] = h;
-    Tl[i] = l;
+  // one 16-byte group (8 columns of a row) per thread and pass
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int i = tid + 256 * j;
+    const int r = i >> 3, c = (i & 7) * 8;
+    const f32x4 a = {Ti[r][c], Ti[r][c + 1], Ti[r][c + 2], Ti[r][c + 3]};
+    const f32x4 b = {Ti[r][c + 4], Ti[r][c + 5], Ti[r][c + 6], Ti[r][c + 7]};
+    split4_store(a, Th + frag_elem(r, c, CH / 32), Tl + frag_elem(r, c, CH / 32));
+    split4_store(b, Th + frag_elem(r, c + 4, CH / 32), Tl + frag_elem(r, c + 4, CH / 32));
   }
 }
 
@@ -353,99 +376,54 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(const ChunkParams p) {
 // that head's chunks.  Wave w produces the chunk's quantities for tokens
 // [16w, 16w+16) (X_K, X_Q, R, U, Y) and updates state columns
 // [32w, 32w+32).  Every MFMA operand that is specific to a wave -- its K, Q,
-// T and P rows, its K^T columns, its V values and gates -- is loaded from
+// T and P rows, its K^T rows, its V values and gates -- is loaded from
 // global memory straight into registers in MFMA layout, and reloaded for the
 // next chunk right after its last use, so those loads overlap the rest of
-// the chunk.  LDS only carries what the waves exchange: the state (as hi/lo
-// bf16, the B operand of X_K / X_Q) and R^T, U^T, (eU)^T; three barriers
-// per chunk.
+// the chunk.  LDS only carries what the waves exchange: the state (hi/lo
+// bf16) and R^T, U^T, (eU)^T; three barriers per chunk.
+//
+// The state update and Y are computed transposed (S^T += K^T (eU),
+// Y^T = gamma X_Q^T + U^T P^T): a lane then holds 4 consecutive state
+// columns / value channels, so the state goes to LDS and y to memory in
+// 8-byte stores.  Global operands are read through buffer descriptors
+// rebased per chunk (scalar work) with loop-invariant lane offsets; a
+// descriptor's extent ends at the chunk's last token, so the hardware returns
+// zeros for the padding rows of a short chunk and drops their y stores.
+
+typedef __amdgpu_buffer_rsrc_t BufRsrc;
+
+constexpr int kBufFlags = 0x00020000;  // raw buffer, 32-bit data format (gfx9)
+
+__device__ __forceinline__ BufRsrc buf_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(bytes), kBufFlags);
+}
+
+__device__ __forceinline__ bf16x8 buf_bf16x8(BufRsrc r, uint32_t voff, int soff) {
+  return __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+}
+
+__device__ __forceinline__ f32x4 buf_f32x4(BufRsrc r, uint32_t voff) {
+  return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, 0, 0));
+}
 
 // One wave's operands of one chunk (all in MFMA operand layouts).
 struct WaveOps {
-  bf16x8 k[4];          // K[16w + lr][32s + 8lq ..]    s = 0..3   (A of X_K)
-  bf16x8 q[4];          // Q rows, same layout                     (A of X_Q)
-  bf16x8 th[2], tl[2];  // T[16w + lr][32s + 8lq ..]    s = 0..1   (A of U)
-  bf16x8 ph[2], pl[2];  // P rows, same layout                     (A of P U)
-  bf16x8 kt[2][2];      // K^T[32w + 16j + lr][32s + 8lq ..]       (B of S update)
-  float v[4];           // V[16w + 4lq + i][dv0 + lr]
-  f32x4 g, b, e;        // gamma / beta / e of tokens 16w + 4lq + i
-  float gC;             // gamma of the chunk's last token
+  bf16x8 k[4], q[4];     // K / Q rows 16w + lr, columns 32s + 8lq ..
+  bf16x8 th[2], tl[2];   // T rows 16w + lr, columns 32s + 8lq .. (hi / lo)
+  bf16x8 ph[2], pl[2];   // P rows, same layout
+  bf16x8 kt[2][2];       // K^T rows 32w + 16j + lr, columns 32s + 8lq ..
+  uint16_t v[4];         // V[16w + 4lq + i][dv0 + lr] (bf16 bits)
+  f32x4 g, b, e;         // gamma / beta / e of tokens 16w + 4lq + i
+  float gy;              // gamma of token 16w + lr
+  float gC;              // gamma of the chunk's last token
 };
 
-struct ChunkSrc {
-  const uint16_t* kq_row;  // K row (token) of this lane, at column 8lq: add s*32
-  const uint16_t* q_row;
-  const uint16_t* v_tok;   // V of token 16w + 4lq (+ i * Hv * DV), state row dv0 + lr
-  const unsigned char* rec;
-  const unsigned char* rec_k;
-  int v_stride;            // elements between tokens of V
-  int v_rows;              // valid rows among the lane's 4 V tokens
+// A chunk's descriptors: V and Y (this v-head, from state row dv0) and all
+// v-heads' workspace records of the chunk.
+struct ChunkBufs {
+  BufRsrc v, y, rec;
+  const float* gam;      // gamma of this head's record
 };
-
-__device__ __forceinline__ ChunkSrc chunk_src(const ChunkParams& p, int64_t t0, int clen, const unsigned char* rec,
-                                             const unsigned char* rec_k, int hk, int hv, int dv0, int wave, int lr,
-                                             int lq) {
-  ChunkSrc c;
-  // rows past the chunk's end read its last row (finite; products with them
-  // are discarded or multiplied by a zero beta)
-  const int krow = min(16 * wave + lr, clen - 1);
-  c.kq_row = p.k + ((t0 + krow) * p.Hk + hk) * DK + 8 * lq;
-  c.q_row = p.q + ((t0 + krow) * p.Hk + hk) * DK + 8 * lq;
-  c.v_tok = p.v + (t0 * p.Hv + hv) * DV + dv0 + lr;
-  c.v_stride = p.Hv * DV;
-  c.v_rows = clen;
-  c.rec = rec;
-  c.rec_k = rec_k;
-  return c;
-}
-
-__device__ __forceinline__ void load_kq(WaveOps& o, const ChunkSrc& c) {
-  static_for<4>([&](auto s) {
-    o.k[s.value] = *reinterpret_cast<const bf16x8*>(c.kq_row + 32 * s.value);
-    o.q[s.value] = *reinterpret_cast<const bf16x8*>(c.q_row + 32 * s.value);
-  });
-}
-
-__device__ __forceinline__ void load_vg(WaveOps& o, const ChunkSrc& c, int wave, int lq) {
-  const int tb = 16 * wave + 4 * lq;
-  static_for<4>([&](auto i) {
-    o.v[i.value] = bf16_to_f32(c.v_tok[min(tb + i.value, c.v_rows - 1) * c.v_stride]);
-  });
-  o.g = *reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(c.rec + kOffGam) + tb);
-  o.b = *reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(c.rec + kOffBeta) + tb);
-}
-
-__device__ __forceinline__ void load_t(WaveOps& o, const ChunkSrc& c, int wave, int lr, int lq) {
-  const uint16_t* th = reinterpret_cast<const uint16_t*>(c.rec + kOffTh) + (16 * wave + lr) * CH + 8 * lq;
-  const uint16_t* tl = reinterpret_cast<const uint16_t*>(c.rec + kOffTl) + (16 * wave + lr) * CH + 8 * lq;
-  static_for<2>([&](auto s) {
-    o.th[s.value] = *reinterpret_cast<const bf16x8*>(th + 32 * s.value);
-    o.tl[s.value] = *reinterpret_cast<const bf16x8*>(tl + 32 * s.value);
-  });
-}
-
-__device__ __forceinline__ void load_e(WaveOps& o, const ChunkSrc& c, int wave, int lq) {
-  o.e = *reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(c.rec + kOffE) + 16 * wave + 4 * lq);
-}
-
-__device__ __forceinline__ void load_kt(WaveOps& o, const ChunkSrc& c, int wave, int lr, int lq) {
-  const uint16_t* kt = reinterpret_cast<const uint16_t*>(c.rec_k + kOffKT) + (32 * wave + lr) * CH + 8 * lq;
-  static_for<2>([&](auto j) {
-    static_for<2>([&](auto s) {
-      o.kt[j.value][s.value] = *reinterpret_cast<const bf16x8*>(kt + 16 * j.value * CH + 32 * s.value);
-    });
-  });
-  o.gC = reinterpret_cast<const float*>(c.rec + kOffGam)[CH - 1];
-}
-
-__device__ __forceinline__ void load_p(WaveOps& o, const ChunkSrc& c, int wave, int lr, int lq) {
-  const uint16_t* ph = reinterpret_cast<const uint16_t*>(c.rec + kOffPh) + (16 * wave + lr) * CH + 8 * lq;
-  const uint16_t* pl = reinterpret_cast<const uint16_t*>(c.rec + kOffPl) + (16 * wave + lr) * CH + 8 * lq;
-  static_for<2>([&](auto s) {
-    o.ph[s.value] = *reinterpret_cast<const bf16x8*>(ph + 32 * s.value);
-    o.pl[s.value] = *reinterpret_cast<const bf16x8*>(pl + 32 * s.value);
-  });
-}
 
 // Rank of sequence n when sequences are ordered by length, longest first
 // (ties by index); used to start the longest chains first.
@@ -480,7 +458,8 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(const ChunkParams p) {
   const int dv0 = tile * DVT;
   const int hk = hv / p.group;
   const int hv_k = hk * p.group;  // the v-head whose record holds this k-head's K^T
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lr = lane & 15, lq = lane >> 4, lg8 = lq * 8;
   const SeqRange sr = seq_range(p, seq);
   const int nch = n_chunks(sr.len);
@@ -490,95 +469,149 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(const ChunkParams p) {
   __shared__ __align__(16) uint16_t Uh[DVT][CP], Ul[DVT][CP];  // U^T
   __shared__ __align__(16) uint16_t Eh[DVT][CP], El[DVT][CP];  // (diag(e) U)^T
 
-  // This wave's 16 x 32 slice of the state: columns [32w, 32w+32) as two
-  // 16x16 accumulator tiles; lane holds rows 4*lq + i, column 16*j + lr.
-  const int64_t srow0 = (static_cast<int64_t>(seq) * p.Hv + hv) * DV + dv0;
-  f32x4 sacc[2];
+  // Loop-invariant lane offsets (bytes) into the per-chunk descriptors:
+  // fragment (rb, cb) of a record matrix is 1 KB at (rb * n_cb + cb) KB.
+  const uint32_t hv_row = static_cast<uint32_t>(p.Hv) * DV * 2;
+  const uint32_t rec_hk = static_cast<uint32_t>(hv_k) * kRecBytes;
+  const uint32_t off_kq = rec_hk + kOffKf + (4 * wave * 64 + lane) * 16;  // K (+ Q plane)
+  uint32_t off_v[4];
 #pragma unroll
-  for (int j = 0; j < 2; ++j)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int64_t idx = (srow0 + 4 * lq + i) * DK + 32 * wave + 16 * j + lr;
-      sacc[j][i] = p.state_in != nullptr ? p.state_in[idx] : 0.0f;
-    }
+  for (int i = 0; i < 4; ++i) off_v[i] = (16 * wave + 4 * lq + i) * hv_row + 2 * lr;
+  const uint32_t off_y = (16 * wave + lr) * hv_row + 8 * lq;
+  const uint32_t rec_hv = static_cast<uint32_t>(hv) * kRecBytes;
+  const uint32_t off_rows = rec_hv + (2 * wave * 64 + lane) * 16;        // T, P rows 16w + lr
+  const uint32_t off_kt = rec_hk + kOffKT + (4 * wave * 64 + lane) * 16;  // K^T rows 32w + 16j + lr
+  const uint32_t off_g4 = rec_hv + kOffGam + (16 * wave + 4 * lq) * 4;
+  const uint32_t off_g1 = rec_hv + kOffGam + (16 * wave + lr) * 4;
 
-  auto src_of = [&](int ci) {
-    const unsigned char* rec = p.ws + (static_cast<size_t>(sr.chunk0 + ci) * p.Hv + hv) * kRecBytes;
-    const unsigned char* rec_k = p.ws + (static_cast<size_t>(sr.chunk0 + ci) * p.Hv + hv_k) * kRecBytes;
-    return chunk_src(p, sr.tok0 + static_cast<int64_t>(ci) * CH, min(CH, sr.len - ci * CH), rec, rec_k, hk, hv,
-                     dv0, wave, lr, lq);
-  };
-  auto write_state = [&]() {
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        split_bf16(sacc[j][i], Sh[4 * lq + i][32 * wave + 16 * j + lr], Sl[4 * lq + i][32 * wave + 16 * j + lr]);
+  auto bufs_of = [&](int ci) {
+    const int64_t t0 = sr.tok0 + static_cast<int64_t>(ci) * CH;
+    const uint32_t last = static_cast<uint32_t>(min(CH, sr.len - ci * CH) - 1);
+    const size_t chunk = static_cast<size_t>(sr.chunk0 + ci);
+    ChunkBufs c;
+    c.v = buf_rsrc(p.v + (t0 * p.Hv + hv) * DV + dv0, last * hv_row + DV * 2);
+    c.y = buf_rsrc(p.y + (t0 * p.Hv + hv) * DV + dv0, last * hv_row + DV * 2);
+    const unsigned char* recs = p.ws + chunk * p.Hv * kRecBytes;
+    c.rec = buf_rsrc(recs, static_cast<uint32_t>(p.Hv) * kRecBytes);
+    c.gam = reinterpret_cast<const float*>(recs + rec_hv + kOffGam);
+    return c;
   };
 
   WaveOps o;
+  auto load_kq = [&](const ChunkBufs& c) {
+    static_for<4>([&](auto s) {
+      o.k[s.value] = buf_bf16x8(c.rec, off_kq + 1024 * s.value, 0);
+      o.q[s.value] = buf_bf16x8(c.rec, off_kq + 1024 * s.value, kOffQf - kOffKf);
+    });
+  };
+  auto load_vg = [&](const ChunkBufs& c) {
+    static_for<4>([&](auto i) {
+      o.v[i.value] = __builtin_amdgcn_raw_buffer_load_b16(c.v, off_v[i.value], 0, 0);
+    });
+    o.g = buf_f32x4(c.rec, off_g4);
+    o.b = buf_f32x4(c.rec, off_g4 + (kOffBeta - kOffGam));
+    o.gy = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(c.rec, off_g1, 0, 0));
+  };
+  auto load_t = [&](const ChunkBufs& c) {
+    static_for<2>([&](auto s) {
+      o.th[s.value] = buf_bf16x8(c.rec, off_rows + 1024 * s.value, kOffTh);
+      o.tl[s.value] = buf_bf16x8(c.rec, off_rows + 1024 * s.value, kOffTl);
+    });
+  };
+  auto load_e = [&](const ChunkBufs& c) { o.e = buf_f32x4(c.rec, off_g4 + (kOffE - kOffGam)); };
+  auto load_kt = [&](const ChunkBufs& c) {
+    static_for<2>([&](auto j) {
+      static_for<2>([&](auto s) {
+        o.kt[j.value][s.value] = buf_bf16x8(c.rec, off_kt + 2048 * j.value + 1024 * s.value, 0);
+      });
+    });
+    o.gC = c.gam[CH - 1];
+  };
+  auto load_p = [&](const ChunkBufs& c) {
+    static_for<2>([&](auto s) {
+      o.ph[s.value] = buf_bf16x8(c.rec, off_rows + 1024 * s.value, kOffPh);
+      o.pl[s.value] = buf_bf16x8(c.rec, off_rows + 1024 * s.value, kOffPl);
+    });
+  };
+
+  // This wave's 32 x 16 slice of S^T: state columns [32w, 32w+32) as two
+  // 16x16 accumulator tiles; lane holds S^T[32w + 16j + 4lq + i][lr], i.e.
+  // 4 consecutive columns of state row dv0 + lr.
+  const int64_t srow = (static_cast<int64_t>(seq) * p.Hv + hv) * DV + dv0 + lr;
+  f32x4 sacc[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int64_t idx = srow * DK + 32 * wave + 16 * j + 4 * lq;
+    sacc[j] = p.state_in != nullptr ? *reinterpret_cast<const f32x4*>(p.state_in + idx) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  }
+  auto write_state = [&]() {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) split4_store(sacc[j], &Sh[lr][32 * wave + 16 * j + 4 * lq], &Sl[lr][32 * wave + 16 * j + 4 * lq]);
+  };
+
   if (nch > 0) {
-    const ChunkSrc c0 = src_of(0);
-    load_kq(o, c0);
-    load_vg(o, c0, wave, lq);
-    load_t(o, c0, wave, lr, lq);
-    load_e(o, c0, wave, lq);
-    load_kt(o, c0, wave, lr, lq);
-    load_p(o, c0, wave, lr, lq);
+    const ChunkBufs c0 = bufs_of(0);
+    load_kq(c0);
+    load_vg(c0);
+    load_t(c0);
+    load_e(c0);
+    load_kt(c0);
+    load_p(c0);
   }
   write_state();
   const f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
 
+  BufRsrc y_cur = bufs_of(0).y;  // (only used when the sequence has chunks)
   for (int ci = 0; ci < nch; ++ci) {
-    const int64_t t0 = sr.tok0 + static_cast<int64_t>(ci) * CH;
-    const int clen = min(CH, sr.len - ci * CH);
     // the next chunk's operands (the last chunk reloads its own: no branches
     // around the loads, so their waits are not forced early)
-    const ChunkSrc cn = src_of(min(ci + 1, nch - 1));
+    const ChunkBufs cn = bufs_of(min(ci + 1, nch - 1));
     __syncthreads();  // state hi/lo of this chunk is in LDS
 
-    // ---- X_K = K S0^T and X_Q = Q S0^T for this wave's 16 tokens
+    // ---- X_K = K S0^T (tokens x rows) and X_Q^T = S0 Q^T (rows x tokens)
     f32x4 xk0 = z, xk1 = z, xq0 = z, xq1 = z;
     static_for<4>([&](auto s) {
       const int kc = 32 * s.value + lg8;
-      const bf16x8 bh = lds8(&Sh[lr][kc]);
-      const bf16x8 bl = lds8(&Sl[lr][kc]);
-      xk0 = mfma16(o.k[s.value], bh, xk0);
-      xk1 = mfma16(o.k[s.value], bl, xk1);
-      xq0 = mfma16(o.q[s.value], bh, xq0);
-      xq1 = mfma16(o.q[s.value], bl, xq1);
+      const bf16x8 sh = lds8(&Sh[lr][kc]);
+      const bf16x8 sl = lds8(&Sl[lr][kc]);
+      xk0 = mfma16(o.k[s.value], sh, xk0);
+      xk1 = mfma16(o.k[s.value], sl, xk1);
+      xq0 = mfma16(sh, o.q[s.value], xq0);
+      xq1 = mfma16(sl, o.q[s.value], xq1);
     });
-    load_kq(o, cn);
+    load_kq(cn);
 
     // ---- R = beta (V - gamma X_K) -> R^T
     {
       f32x4 r;
-      static_for<4>([&](auto i) { r[i.value] = o.b[i.value] * (o.v[i.value] - o.g[i.value] * (xk0[i.value] + xk1[i.value])); });
+      static_for<4>([&](auto i) {
+        r[i.value] = o.b[i.value] * (bf16_to_f32(o.v[i.value]) - o.g[i.value] * (xk0[i.value] + xk1[i.value]));
+      });
       split4_store(r, &Rh[lr][16 * wave + 4 * lq], &Rl[lr][16 * wave + 4 * lq]);
     }
-    const f32x4 gam = o.g;  // kept for Y
-    load_vg(o, cn, wave, lq);
+    const float gy = o.gy;  // kept for Y
+    load_vg(cn);
     __syncthreads();  // R^T complete
 
     // ---- U = T R for this wave's 16 tokens
     f32x4 u0 = z, u1 = z;
     static_for<2>([&](auto s) {
       const int kc = 32 * s.value + lg8;
-      const bf16x8 bh = lds8(&Rh[lr][kc]);
-      u0 = mfma16(o.th[s.value], bh, u0);
+      const bf16x8 rh = lds8(&Rh[lr][kc]);
+      u0 = mfma16(o.th[s.value], rh, u0);
       u1 = mfma16(o.th[s.value], lds8(&Rl[lr][kc]), u1);
-      u1 = mfma16(o.tl[s.value], bh, u1);
+      u1 = mfma16(o.tl[s.value], rh, u1);
     });
-    load_t(o, cn, wave, lr, lq);
+    load_t(cn);
     {
       const f32x4 uv = u0 + u1;
       split4_store(uv, &Uh[lr][16 * wave + 4 * lq], &Ul[lr][16 * wave + 4 * lq]);
       split4_store(o.e * uv, &Eh[lr][16 * wave + 4 * lq], &El[lr][16 * wave + 4 * lq]);
     }
-    load_e(o, cn, wave, lq);
+    load_e(cn);
     __syncthreads();  // U^T, (eU)^T complete
 
-    // ---- S = gamma_C S0 + (diag(e) U)^T K on this wave's 32 columns
+    // ---- S^T = gamma_C S0^T + K^T (diag(e) U) on this wave's 32 columns
 #pragma unroll
     for (int j = 0; j < 2; ++j) sacc[j] *= o.gC;
     static_for<2>([&](auto s) {
@@ -586,40 +619,34 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(const ChunkParams p) {
       const bf16x8 eh = lds8(&Eh[lr][kc]);
       const bf16x8 el = lds8(&El[lr][kc]);
       static_for<2>([&](auto j) {
-        sacc[j.value] = mfma16(eh, o.kt[j.value][s.value], sacc[j.value]);
-        sacc[j.value] = mfma16(el, o.kt[j.value][s.value], sacc[j.value]);
+        sacc[j.value] = mfma16(o.kt[j.value][s.value], eh, sacc[j.value]);
+        sacc[j.value] = mfma16(o.kt[j.value][s.value], el, sacc[j.value]);
       });
     });
-    load_kt(o, cn, wave, lr, lq);
+    load_kt(cn);
+    write_state();  // every wave read S0 before the R^T barrier
 
-    // ---- Y = gamma X_Q + P U for this wave's 16 tokens
+    // ---- Y^T = gamma X_Q^T + U^T P^T (rows x this wave's 16 tokens)
     f32x4 y0 = z, y1 = z;
     static_for<2>([&](auto s) {
       const int kc = 32 * s.value + lg8;
       const bf16x8 uh = lds8(&Uh[lr][kc]);
-      y0 = mfma16(o.ph[s.value], uh, y0);
-      y1 = mfma16(o.ph[s.value], lds8(&Ul[lr][kc]), y1);
-      y1 = mfma16(o.pl[s.value], uh, y1);
+      y0 = mfma16(uh, o.ph[s.value], y0);
+      y1 = mfma16(lds8(&Ul[lr][kc]), o.ph[s.value], y1);
+      y1 = mfma16(uh, o.pl[s.value], y1);
     });
-    load_p(o, cn, wave, lr, lq);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int t = 16 * wave + 4 * lq + i;
-      if (t < clen) {
-        const float yv = fmaf(gam[i], xq0[i] + xq1[i], y0[i] + y1[i]);
-        p.y[((t0 + t) * p.Hv + hv) * DV + dv0 + lr] = f32_to_bf16(yv);
-      }
+    load_p(cn);
+    {
+      const f32x4 yv = gy * (xq0 + xq1) + (y0 + y1);
+      const bf16x4 yb = __builtin_convertvector(yv, bf16x4);
+      __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, yb), y_cur, off_y, 0, 0);
     }
-    write_state();  // every wave read S0 before the R^T barrier
+    y_cur = cn.y;
   }
 
 #pragma unroll
   for (int j = 0; j < 2; ++j)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int64_t idx = (srow0 + 4 * lq + i) * DK + 32 * wave + 16 * j + lr;
-      p.state_out[idx] = sacc[j][i];
-    }
+    *reinterpret_cast<f32x4*>(p.state_out + srow * DK + 32 * wave + 16 * j + 4 * lq) = sacc[j];
 }
 
 int64_t max_chunks(int64_t n_seqs, int64_t n_tok, bool packed) {
