@@ -41,6 +41,7 @@ constexpr int DV = 128;     // value head dim
 constexpr int DVT = 16;     // state rows per scan workgroup
 constexpr int KP = DK + 8;  // padded LDS row (bf16) for 128-wide rows
 constexpr int CP = CH + 8;  // padded LDS row (bf16) for 64-wide rows
+constexpr double kLog2e = 1.4426950408889634;
 
 // Workspace record per (chunk, v-head).  Matrices are stored as MFMA
 // fragments: the 16 x 32 block (row block rb, column block cb) of a matrix
@@ -95,6 +96,7 @@ __device__ __forceinline__ void split_bf16(float x, uint16_t& hi, uint16_t& lo) 
 __device__ __forceinline__ bf16x8 lds8(const uint16_t* p) {
   return *reinterpret_cast<const bf16x8*>(p);
 }
+
 
 // Component-wise "keep or zero" (a ternary on the u32x4 struct would be
 // lowered through memory).
@@ -187,6 +189,14 @@ __device__ __forceinline__ bool chunk_at(const ChunkParams& p, int c, int64_t& t
 
 // ------------------------------------------------------------ chunk_prep
 
+// Orders this wave's LDS writes before its later LDS reads (no other wave
+// takes part).
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 __global__ __launch_bounds__(256) void chunk_prep_kernel(const ChunkParams p) {
   // work index = chunk * Hv + hv: both v-heads of a k-head (GQA) share an XCD
   const int w = xcd_work_index();
@@ -197,17 +207,30 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(const ChunkParams p) {
   if (!chunk_at(p, c, tok0, len)) return;
   const int hk = hv / p.group;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int lr = lane & 15, lq = lane >> 4, lg8 = lq * 8;
 
-  __shared__ __align__(16) uint16_t Ks[CH][KP];
-  __shared__ __align__(16) uint16_t Qs[CH][KP];
-  __shared__ float As[CH][CH + 1];
-  __shared__ float Ti[CH][CH + 1];
-  __shared__ float Ms[3][16][17];
+  // Two 17 KB buffers, each reused once (LDS stays under 53 KB, so three
+  // workgroups fit on a CU):  buf0 = K rows, then A;  buf1 = Q rows, then
+  // the P hi/lo planes in fragment order, then (I + A)^{-1}.
+  constexpr int kBuf = CH * KP * 2;
+  static_assert(kBuf == CH * (CH + 4) * 4, "A and T must fill the K / Q buffers exactly");
+  static_assert(kBuf >= 2 * CH * CH * 2, "P staging must fit in the Q buffer");
+  __shared__ __align__(16) unsigned char buf0[kBuf];
+  __shared__ __align__(16) unsigned char buf1[kBuf];
+  __shared__ __align__(16) float Ms[4][16][20];
   __shared__ double Ld[CH];
   __shared__ float Bs[CH];
+  auto Ks = reinterpret_cast<uint16_t(*)[KP]>(buf0);
+  auto Qs = reinterpret_cast<uint16_t(*)[KP]>(buf1);
+  auto As = reinterpret_cast<float(*)[CH + 4]>(buf0);
+  auto Ti = reinterpret_cast<float(*)[CH + 4]>(buf1);
+  uint16_t* Pst = reinterpret_cast<uint16_t*>(buf1);
 
-  // All row loads first (rows past the chunk's end read its last row and
-  // are zeroed at the LDS store), then the LDS stores.
+  // Gate loads first (wave 0), so waiting for them does not wait for the
+  // K/Q rows queued behind; then the rows (rows past the chunk's end read its
+  // last row and are zeroed at the LDS store).
+  float lg = 0.0f, bt = 0.0f;
+  if (wave == 0) load_log_gates(p.ga, (tok0 + min(lane, len - 1)) * p.Hv + hv, hv, lg, bt);
   u32x4 kr[4], qr[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
@@ -219,8 +242,6 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(const ChunkParams p) {
   }
   unsigned char* rec = p.ws + (static_cast<size_t>(c) * p.Hv + hv) * kRecBytes;
   if (wave == 0) {
-    float lg, bt;
-    load_log_gates(p.ga, (tok0 + min(lane, len - 1)) * p.Hv + hv, hv, lg, bt);
     // padding tokens: no decay, no write; g = 0 (pre-transformed) stays finite
     lg = lane < len ? fmaxf(lg, -1.0e30f) : 0.0f;
     bt = lane < len ? bt : 0.0f;
@@ -249,7 +270,6 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(const ChunkParams p) {
       *reinterpret_cast<u32x4*>(reinterpret_cast<uint16_t*>(rec + kOffQf) + frag_elem(r, cc, DK / 32)) = qv;
     }
   }
-  for (int i = tid; i < CH * (CH + 1); i += 256) (&Ti[0][0])[i] = 0.0f;
   __syncthreads();
 
   // K K^T and Q K^T: wave w computes row block w (16 rows) x 4 column blocks.
@@ -259,7 +279,18 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(const ChunkParams p) {
     kk[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     qk[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   }
-  const int lr = lane & 15, lg8 = (lane >> 4) * 8;
+  // K^T for the scan's state update, as MFMA A-fragments (rows dk, columns
+  // tokens): a product with a one-hot B turns this wave's K rows into 16x16
+  // tiles whose lane (r, q) holds K[16w + 4q .. +3][16d + r], i.e. 4
+  // consecutive tokens of one dk -- half of the 16 bytes of fragment lane
+  // r + 16 * (2 * (w % 2) + q / 2).  Written once per k-head (by its first
+  // v-head), 8 bytes per lane and tile.
+  bf16x8 eye[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) eye[h][e] = static_cast<__bf16>(lg8 + e == lr + 16 * h ? 1.0f : 0.0f);
+  unsigned char* KTg = rec + kOffKT + (wave >> 1) * 1024 + (lr + 16 * (2 * (wave & 1) + (lq >> 1))) * 16 + (lq & 1) * 8;
 #pragma unroll
   for (int s = 0; s < DK / 32; ++s) {
     const int kc = s * 32 + lg8;
@@ -271,43 +302,53 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(const ChunkParams p) {
       kk[j] = mfma16(ak, bk, kk[j]);
       qk[j] = mfma16(aq, bk, qk[j]);
     }
-  }
-  // K^T [dk][token] for the scan's state update: one 16-byte group of 8
-  // tokens per store, written once per k-head (by its first v-head).
-  if (first_v) {
-    uint16_t* KTg = reinterpret_cast<uint16_t*>(rec + kOffKT);
+    if (first_v) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int i = tid + 256 * j;            // 1024 groups: 128 dk x 8 token groups
-      const int dk = i >> 3, tg = (i & 7) * 8;
-      uint16_t h[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) h[e] = Ks[tg + e][dk];
-      u32x4 v;
-      v.x = h[0] | (static_cast<uint32_t>(h[1]) << 16);
-      v.y = h[2] | (static_cast<uint32_t>(h[3]) << 16);
-      v.z = h[4] | (static_cast<uint32_t>(h[5]) << 16);
-      v.w = h[6] | (static_cast<uint32_t>(h[7]) << 16);
-      *reinterpret_cast<u32x4*>(KTg + frag_elem(dk, tg, CH / 32)) = v;
+      for (int h = 0; h < 2; ++h) {
+        const f32x4 t = mfma16(ak, eye[h], f32x4{0.0f, 0.0f, 0.0f, 0.0f});
+        // dk block d = 2s + h: fragment (d, token column wave / 2) at 2 KB * d
+        *reinterpret_cast<u32x2*>(KTg + (2 * s + h) * 2048) = u32x2{pk_bf16(t[0], t[1]), pk_bf16(t[2], t[3])};
+      }
     }
   }
-  uint16_t* Ph = reinterpret_cast<uint16_t*>(rec + kOffPh);
-  uint16_t* Pl = reinterpret_cast<uint16_t*>(rec + kOffPl);
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
+  // every wave has its K K^T / Q K^T products in registers; K and Q in LDS
+  // are no longer read, so their buffers take A and the P planes
+  __syncthreads();
+
+  // Decays, A (to LDS, fp32) and P (hi/lo bf16, staged in fragment order).
+  {
+    double Lt[4], Lc[4];
+    float bs[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int t = 16 * wave + 4 * (lane >> 4) + i;
-      const int col = 16 * j + lr;
-      const float dec = col <= t ? expf(static_cast<float>(Ld[t] - Ld[col])) : 0.0f;
-      As[t][col] = col < t ? Bs[t] * dec * kk[j][i] : 0.0f;
-      uint16_t h, l;
-      split_bf16(dec * qk[j][i], h, l);
-      Ph[frag_elem(t, col, CH / 32)] = h;
-      Pl[frag_elem(t, col, CH / 32)] = l;
+      Lt[i] = Ld[16 * wave + 4 * lq + i];
+      bs[i] = Bs[16 * wave + 4 * lq + i];
+      Lc[i] = Ld[16 * i + lr];
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int t = 16 * wave + 4 * lq + i;
+        const int col = 16 * j + lr;
+        const float dec = col <= t ? __builtin_amdgcn_exp2f(static_cast<float>((Lt[i] - Lc[j]) * kLog2e)) : 0.0f;
+        As[t][col] = col < t ? bs[i] * dec * kk[j][i] : 0.0f;
+        uint16_t h, l;
+        split_bf16(dec * qk[j][i], h, l);
+        Pst[frag_elem(t, col, CH / 32)] = h;
+        Pst[CH * CH + frag_elem(t, col, CH / 32)] = l;
+      }
     }
   }
   __syncthreads();
+
+  // P planes out: a linear 16 KB copy (hi then lo, as in the record).
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int i = tid + 256 * j;
+    *reinterpret_cast<u32x4*>(rec + kOffPh + 16 * i) = *reinterpret_cast<const u32x4*>(Pst + 8 * i);
+  }
+  __syncthreads();  // the P planes are out: their buffer takes (I + A)^{-1}
 
   // (I + A)^{-1}, A strictly lower.  Diagonal 16x16 blocks by forward
   // substitution from registers (one lane per (block, column)).
@@ -330,43 +371,70 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(const ChunkParams p) {
     for (int t = 0; t < 16; ++t) Ti[base + t][base + j] = x[t];
   }
   __syncthreads();
-  // Off-diagonal blocks, by distance from the diagonal (blocks of one
-  // distance in parallel):  T_IJ = -T_II * sum_{K=J}^{I-1} A_IK T_KJ
+  // Off-diagonal blocks by distance d from the diagonal.  Block (I, J=I-d)
+  // belongs to wave J; a lane computes a 1x4 patch (row r, columns c4..c4+3):
+  //   M = sum_{K=J}^{I-1} A_IK T_KJ,   T_IJ = -T_II M
   {
-    const int r = (tid >> 4) & 15, cc = tid & 15;
-    for (int lvl = 1; lvl < 4; ++lvl) {
-      const int nblk = 4 - lvl;
-      for (int bi = 0; bi < nblk; ++bi) {
-        const int I = lvl + bi, J = bi;
-        float m = 0.0f;
+    const int r = lane >> 2, c4 = (lane & 3) * 4;
+    for (int d = 1; d < 4; ++d) {
+      const int J = wave, I = wave + d;
+      if (I < 4) {
+        // operands of a block product are loaded ahead of its FMAs (one LDS
+        // round trip per block instead of one per step)
+        f32x4 m0 = {0.0f, 0.0f, 0.0f, 0.0f}, m1 = m0;
         for (int Kb = J; Kb < I; ++Kb) {
+          f32x4 av[4], tb[16];
 #pragma unroll
-          for (int x = 0; x < 16; ++x) m = fmaf(As[16 * I + r][16 * Kb + x], Ti[16 * Kb + x][16 * J + cc], m);
+          for (int q = 0; q < 4; ++q) av[q] = *reinterpret_cast<const f32x4*>(&As[16 * I + r][16 * Kb + 4 * q]);
+#pragma unroll
+          for (int x = 0; x < 16; ++x) tb[x] = *reinterpret_cast<const f32x4*>(&Ti[16 * Kb + x][16 * J + c4]);
+#pragma unroll
+          for (int x = 0; x < 16; x += 2) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              m0[e] = fmaf(av[x >> 2][x & 3], tb[x][e], m0[e]);
+              m1[e] = fmaf(av[(x + 1) >> 2][(x + 1) & 3], tb[x + 1][e], m1[e]);
+            }
+          }
         }
-        Ms[bi][r][cc] = m;
-      }
-      __syncthreads();
-      for (int bi = 0; bi < nblk; ++bi) {
-        const int I = lvl + bi, J = bi;
-        float tv = 0.0f;
+        *reinterpret_cast<f32x4*>(&Ms[wave][r][c4]) = m0 + m1;
+        wave_lds_sync();  // Ms is written and read by this wave only
+        f32x4 tv0 = {0.0f, 0.0f, 0.0f, 0.0f}, tv1 = tv0;
+        {
+          f32x4 av[4], mb[16];
 #pragma unroll
-        for (int x = 0; x < 16; ++x) tv = fmaf(-Ti[16 * I + r][16 * I + x], Ms[bi][x][cc], tv);
-        Ti[16 * I + r][16 * J + cc] = tv;
+          for (int q = 0; q < 4; ++q) av[q] = *reinterpret_cast<const f32x4*>(&Ti[16 * I + r][16 * I + 4 * q]);
+#pragma unroll
+          for (int x = 0; x < 16; ++x) mb[x] = *reinterpret_cast<const f32x4*>(&Ms[wave][x][c4]);
+#pragma unroll
+          for (int x = 0; x < 16; x += 2) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              tv0[e] = fmaf(-av[x >> 2][x & 3], mb[x][e], tv0[e]);
+              tv1[e] = fmaf(-av[(x + 1) >> 2][(x + 1) & 3], mb[x + 1][e], tv1[e]);
+            }
+          }
+        }
+        const f32x4 tv = tv0 + tv1;
+        *reinterpret_cast<f32x4*>(&Ti[16 * I + r][16 * J + c4]) = tv;
       }
       __syncthreads();
     }
   }
   uint16_t* Th = reinterpret_cast<uint16_t*>(rec + kOffTh);
   uint16_t* Tl = reinterpret_cast<uint16_t*>(rec + kOffTl);
-  // one 16-byte group (8 columns of a row) per thread and pass
+  // one 16-byte group (8 columns of a row) per thread and pass; blocks
+  // above the diagonal are zero (never written in Ti)
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     const int i = tid + 256 * j;
-    const int r = i >> 3, c = (i & 7) * 8;
-    const f32x4 a = {Ti[r][c], Ti[r][c + 1], Ti[r][c + 2], Ti[r][c + 3]};
-    const f32x4 b = {Ti[r][c + 4], Ti[r][c + 5], Ti[r][c + 6], Ti[r][c + 7]};
-    split4_store(a, Th + frag_elem(r, c, CH / 32), Tl + frag_elem(r, c, CH / 32));
-    split4_store(b, Th + frag_elem(r, c + 4, CH / 32), Tl + frag_elem(r, c + 4, CH / 32));
+    const int r = i >> 3, cc = (i & 7) * 8;
+    const bool upper = (cc >> 4) > (r >> 4);
+    const f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
+    const f32x4 a = upper ? z : *reinterpret_cast<const f32x4*>(&Ti[r][cc]);
+    const f32x4 b = upper ? z : *reinterpret_cast<const f32x4*>(&Ti[r][cc + 4]);
+    split4_store(a, Th + frag_elem(r, cc, CH / 32), Tl + frag_elem(r, cc, CH / 32));
+    split4_store(b, Th + frag_elem(r, cc + 4, CH / 32), Tl + frag_elem(r, cc + 4, CH / 32));
   }
 }
 
