@@ -107,13 +107,6 @@ __device__ __forceinline__ u32x4 keep_if(bool c, const u32x4& a) {
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-
-// Two floats -> packed bf16 pair (one v_cvt_pk_bf16_f32, round to nearest even).
-__device__ __forceinline__ uint32_t pk_bf16(float a, float b) {
-  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{a, b}), bf16x2));
-}
-
 // hi = bf16(x), lo = bf16(x - hi) for 4 values, as two 8-byte LDS stores.
 // The residual takes hi back from the packed pair (shift / mask) rather than
 // converting each value a second time.

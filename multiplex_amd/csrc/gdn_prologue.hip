@@ -3,10 +3,11 @@
 // partially accepted verify.  Bound by HBM: each mixed-qkv element is read
 // once and each q/k/v element written once.
 //
-// A wavefront owns one head-wide channel group (D = Dk = Dv channels; lane
-// holds D/64 adjacent channels) and walks a run of consecutive tokens with a
-// sliding window of the previous 3 inputs in registers, so the causal conv
-// needs no re-reads.  The per-token q/k norm is a wavefront reduction.
+// A lane owns 8 adjacent channels (one 16-byte access of a bf16 row), so a
+// head of D channels spans D/8 lanes and a wavefront covers 512/D heads.  A
+// wavefront walks a run of consecutive tokens with a sliding window of the
+// previous 3 inputs in registers, so the causal conv needs no re-reads; the
+// per-token q/k norm is a DPP reduction over the head's lanes.
 #include "gdn_common.hpp"
 
 namespace {
@@ -32,30 +33,77 @@ struct ProParams {
   float eps;
 };
 
-template <int CPL, int DT>
-__device__ __forceinline__ void load_vec(const void* p, int64_t i, float (&x)[CPL]) {
-  if constexpr (CPL == 1) {
-    x[0] = IO<DT>::load1(p, i);
-  } else if constexpr (CPL == 2) {
-    const f32x2 v = IO<DT>::load2(p, i);
-    x[0] = v.x;
-    x[1] = v.y;
+constexpr int CPL = 8;  // channels per lane
+
+// Raw 8-channel slice of a row as loaded (converted at its use, so the loads
+// of a whole run can be in flight at once).
+template <int DT>
+struct Raw8 {
+  u32x4 v;  // 8 x 16-bit
+};
+template <>
+struct Raw8<GDN_DTYPE_F32> {
+  f32x4 a, b;
+};
+
+template <int DT>
+__device__ __forceinline__ Raw8<DT> load_raw8(const void* base, int64_t i) {
+  Raw8<DT> r;
+  if constexpr (DT == GDN_DTYPE_F32) {
+    r.a = *reinterpret_cast<const f32x4*>(static_cast<const float*>(base) + i);
+    r.b = *reinterpret_cast<const f32x4*>(static_cast<const float*>(base) + i + 4);
   } else {
-    const f32x4 v = IO<DT>::load4(p, i);
-    x[0] = v.x;
-    x[1] = v.y;
-    x[2] = v.z;
-    x[3] = v.w;
+    r.v = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(base) + i);
+  }
+  return r;
+}
+
+template <int DT>
+__device__ __forceinline__ void unpack8(const Raw8<DT>& r, float (&x)[CPL]) {
+  if constexpr (DT == GDN_DTYPE_F32) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      x[k] = r.a[k];
+      x[4 + k] = r.b[k];
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      if constexpr (DT == GDN_DTYPE_BF16) {
+        x[2 * k] = __uint_as_float(r.v[k] << 16);
+        x[2 * k + 1] = __uint_as_float(r.v[k] & 0xffff0000u);
+      } else {
+        x[2 * k] = f16_to_f32(static_cast<uint16_t>(r.v[k] & 0xffffu));
+        x[2 * k + 1] = f16_to_f32(static_cast<uint16_t>(r.v[k] >> 16));
+      }
+    }
   }
 }
 
-template <int CPL, int DT>
-__device__ __forceinline__ void store_vec(void* p, int64_t i, const float (&x)[CPL]) {
-  if constexpr (CPL == 1) {
-    IO<DT>::store1(p, i, x[0]);
+template <int DT>
+__device__ __forceinline__ void store8(void* base, int64_t i, const float (&x)[CPL]) {
+  if constexpr (DT == GDN_DTYPE_F32) {
+    *reinterpret_cast<f32x4*>(static_cast<float*>(base) + i) = f32x4{x[0], x[1], x[2], x[3]};
+    *reinterpret_cast<f32x4*>(static_cast<float*>(base) + i + 4) = f32x4{x[4], x[5], x[6], x[7]};
   } else {
+    u32x4 v;
 #pragma unroll
-    for (int j = 0; j < CPL; j += 2) IO<DT>::store2(p, i + j, x[j], x[j + 1]);
+    for (int k = 0; k < 4; ++k)
+      v[k] = DT == GDN_DTYPE_BF16 ? pk_bf16(x[2 * k], x[2 * k + 1]) : pk_f16(x[2 * k], x[2 * k + 1]);
+    *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(base) + i) = v;
+  }
+}
+
+// Sum over the LPH lanes of a head (aligned lane groups of 8, 16 or 32).
+template <int LPH>
+__device__ __forceinline__ float head_sum(float x) {
+  if constexpr (LPH == 8) {
+    return sum8(x);
+  } else if constexpr (LPH == 16) {
+    return sum16(x);
+  } else {
+    x = sum16(x);
+    return x + __shfl_xor(x, 16, 64);
   }
 }
 
@@ -85,18 +133,22 @@ __device__ __forceinline__ bool locate(const ProParams& p, int& seq, int64_t& st
   return false;
 }
 
-// Read-only stand-ins for absent operands (loads stay unconditional).
-__device__ const float kZeros[4] = {};
-__device__ const uint8_t kOne = 1;
+// SiLU x * sigmoid(x) = x / (1 + 2^(-x log2 e)) on the hardware exp2 and
+// reciprocal (about 1 ulp each; the result is rounded to the io dtype).  For
+// x -> -inf the denominator overflows to inf and the result is -0.
+__device__ __forceinline__ float silu(float x) {
+  return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(x * -1.4426950408889634f));
+}
 
-// W32: conv taps are fp32 (else they share the io dtype DT).
-template <int D, int DT, bool W32>
+// W32: conv taps are fp32 (else they share the io dtype DT).  MASK: a token
+// mask is given (without one no mask bytes are read or applied).
+template <int D, int DT, bool W32, bool MASK>
 __global__ __launch_bounds__(256) void prologue_kernel(const ProParams p) {
-  constexpr int CPL = D / 64;
+  constexpr int LPH = D / CPL;   // lanes per head
+  constexpr int HPW = 64 / LPH;  // heads per wavefront
   constexpr int WDT = W32 ? GDN_DTYPE_F32 : DT;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int grp = blockIdx.x;
   int seq, len, run;
   int64_t start;
   if (!locate(p, seq, start, len, run)) return;
@@ -104,74 +156,102 @@ __global__ __launch_bounds__(256) void prologue_kernel(const ProParams p) {
   if (t_begin >= len && !(len == 0 && t_begin == 0)) return;
   const int t_end = t_begin + kRun < len ? t_begin + kRun : len;
 
-  const int c0 = grp * D + lane * CPL;
+  // This lane's head (over the 2 Hk + Hv heads of the mixed row) and its 8
+  // channels; lanes past the last head work on a copy of it and store nothing.
+  const int n_heads = 2 * p.Hk + p.Hv;
+  const int head_all = blockIdx.x * HPW + lane / LPH;
+  const bool active = head_all < n_heads;
+  const int hg = active ? head_all : n_heads - 1;
+  const int c0 = hg * D + (lane % LPH) * CPL;
   const int64_t C = p.C;
 
-  // Issue every load first: the run's tokens (rows past the end re-read the
-  // last row and are never used), the window of the 3 inputs before the
-  // run, the taps.  A masked token reads as zero (mask byte as multiplier).
-  float xs[kRun][CPL];
-  float xm[kRun];
-  if (t_end > t_begin) {
-#pragma unroll
-    for (int u = 0; u < kRun; ++u) {
-      const int64_t tok = start + min(t_begin + u, t_end - 1);
-      load_vec<CPL, DT>(p.qkv, tok * C + c0, xs[u]);
-      const uint8_t* mp = p.mask != nullptr ? p.mask + tok : &kOne;
-      xm[u] = *mp != 0 ? 1.0f : 0.0f;
-    }
-  }
-  // window[i] = X[t + i], X = concat(conv_state (KT-1 rows), masked qkv)
-  float win[KT - 1][CPL];
-#pragma unroll
-  for (int i = 0; i < KT - 1; ++i) {
-    const int xi = t_begin + i;
-    const void* src;
-    float wm = 1.0f;
+  // X = concat(conv_state (KT-1 rows), masked qkv): row xi of it.
+  auto load_x = [&](int xi, float (&dst)[CPL]) {
     if (xi < KT - 1) {
-      src = p.cs_in != nullptr
-                ? static_cast<const void*>(static_cast<const char*>(p.cs_in) +
-                                           ((static_cast<int64_t>(seq) * (KT - 1) + xi) * C + c0) *
-                                               (DT == GDN_DTYPE_F32 ? 4 : 2))
-                : static_cast<const void*>(kZeros);
+      if (p.cs_in != nullptr) {
+        unpack8<DT>(load_raw8<DT>(p.cs_in, (static_cast<int64_t>(seq) * (KT - 1) + xi) * C + c0), dst);
+      } else {
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) dst[j] = 0.0f;
+      }
     } else {
       const int64_t tok = start + xi - (KT - 1);
-      src = static_cast<const char*>(p.qkv) + (tok * C + c0) * (DT == GDN_DTYPE_F32 ? 4 : 2);
-      const uint8_t* mp = p.mask != nullptr ? p.mask + tok : &kOne;
-      wm = *mp != 0 ? 1.0f : 0.0f;
+      unpack8<DT>(load_raw8<DT>(p.qkv, tok * C + c0), dst);
+      if constexpr (MASK) {
+        const float wm = p.mask[tok] != 0 ? 1.0f : 0.0f;
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) dst[j] *= wm;
+      }
     }
-    load_vec<CPL, DT>(src, 0, win[i]);
+  };
+  if (t_end == t_begin) {
+    // empty sequence: the conv state passes through
+    if (p.cs_out != nullptr && active) {
 #pragma unroll
-    for (int j = 0; j < CPL; ++j) win[i][j] *= wm;
+      for (int i = 0; i < KT - 1; ++i) {
+        float r[CPL];
+        load_x(i, r);
+        store8<DT>(p.cs_out, (static_cast<int64_t>(seq) * (KT - 1) + i) * C + c0, r);
+      }
+    }
+    return;
   }
+  // Issue every load first: the run's tokens (rows past the end re-read the
+  // last row and are never stored), the window of the 3 inputs before the
+  // run, the taps.  A masked token reads as zero (mask byte as multiplier).
+  Raw8<DT> xs[kRun];
+  float xm[kRun];
+  const int t_last = t_end - 1;
+#pragma unroll
+  for (int u = 0; u < kRun; ++u) {
+    const int64_t tok = start + min(t_begin + u, t_last);
+    xs[u] = load_raw8<DT>(p.qkv, tok * C + c0);
+    if constexpr (MASK) xm[u] = p.mask[tok] != 0 ? 1.0f : 0.0f;
+  }
+  // window[i] = X[t + i] for the run's first token t
+  float win[KT - 1][CPL];
+#pragma unroll
+  for (int i = 0; i < KT - 1; ++i) load_x(t_begin + i, win[i]);
+  // taps of the lane's 8 channels: weight[c][tap], 32 consecutive values
   float w[KT][CPL];
+  {
+    float wv[CPL * KT];
+    unpack8<WDT>(load_raw8<WDT>(p.weight, static_cast<int64_t>(c0) * KT), *reinterpret_cast<float(*)[CPL]>(&wv[0]));
+    unpack8<WDT>(load_raw8<WDT>(p.weight, static_cast<int64_t>(c0) * KT + 8), *reinterpret_cast<float(*)[CPL]>(&wv[8]));
+    unpack8<WDT>(load_raw8<WDT>(p.weight, static_cast<int64_t>(c0) * KT + 16), *reinterpret_cast<float(*)[CPL]>(&wv[16]));
+    unpack8<WDT>(load_raw8<WDT>(p.weight, static_cast<int64_t>(c0) * KT + 24), *reinterpret_cast<float(*)[CPL]>(&wv[24]));
 #pragma unroll
-  for (int j = 0; j < CPL; ++j)
+    for (int j = 0; j < CPL; ++j)
 #pragma unroll
-    for (int i = 0; i < KT; ++i) w[i][j] = IO<WDT>::load1(p.weight, (c0 + j) * KT + i);
+      for (int i = 0; i < KT; ++i) w[i][j] = wv[j * KT + i];
+  }
 
-  // Head role of this channel group: 0 = q, 1 = k, 2 = v.
-  const int role = grp < p.Hk ? 0 : (grp < 2 * p.Hk ? 1 : 2);
-  const int head = role == 0 ? grp : (role == 1 ? grp - p.Hk : grp - 2 * p.Hk);
+  // Head role: 0 = q, 1 = k, 2 = v (lanes of one head agree).
+  const int role = hg < p.Hk ? 0 : (hg < 2 * p.Hk ? 1 : 2);
+  const int head = role == 0 ? hg : (role == 1 ? hg - p.Hk : hg - 2 * p.Hk);
   void* out = role == 0 ? p.q_out : (role == 1 ? p.k_out : p.v_out);
   const int H = role == 2 ? p.Hv : p.Hk;
   const float post = role == 0 ? 1.0f / static_cast<float>(D) : rsqrtf(static_cast<float>(D));
+  // output row of the run's first token; one row = H * D elements
+  constexpr int ES = DT == GDN_DTYPE_F32 ? 4 : 2;
+  char* orow = static_cast<char*>(out) + ((start + t_begin) * H * D + static_cast<int64_t>(head) * D +
+                                          (lane % LPH) * CPL) * ES;
+  const int64_t ostep = static_cast<int64_t>(H) * D * ES;
 
+  // Every token of the run is computed (tokens past the end repeat the last
+  // row, so no control flow splits the window); only real tokens are stored.
 #pragma unroll
   for (int u = 0; u < kRun; ++u) {
-    const int t = t_begin + u;
-    if (t >= t_end) break;
-    const int64_t tok = start + t;
-    float o[CPL];
-    float x[CPL];
+    float x[CPL], o[CPL];
+    unpack8<DT>(xs[u], x);
     float ss = 0.0f;
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
-      x[j] = xs[u][j] * xm[u];
+      if constexpr (MASK) x[j] *= xm[u];
       float acc = w[KT - 1][j] * x[j];
 #pragma unroll
       for (int i = 0; i < KT - 1; ++i) acc = fmaf(w[i][j], win[i][j], acc);
-      o[j] = acc / (1.0f + expf(-acc));  // SiLU
+      o[j] = silu(acc);
       ss = fmaf(o[j], o[j], ss);
     }
 #pragma unroll
@@ -180,19 +260,24 @@ __global__ __launch_bounds__(256) void prologue_kernel(const ProParams p) {
       for (int j = 0; j < CPL; ++j) win[i][j] = win[i + 1][j];
 #pragma unroll
     for (int j = 0; j < CPL; ++j) win[KT - 2][j] = x[j];
-    if (role != 2) {
-      ss = wave_sum(ss);
-      const float sc = rsqrtf(ss / static_cast<float>(D) + p.eps) * post;
+    // every lane takes part in the reduction (DPP); v heads keep scale 1
+    ss = head_sum<LPH>(ss);
+    const float sc = role == 2 ? 1.0f : rsqrtf(ss / static_cast<float>(D) + p.eps) * post;
 #pragma unroll
-      for (int j = 0; j < CPL; ++j) o[j] *= sc;
-    }
-    store_vec<CPL, DT>(out, (tok * H + head) * D + lane * CPL, o);
+    for (int j = 0; j < CPL; ++j) o[j] *= sc;
+    if (active && t_begin + u < t_end) store8<DT>(orow, 0, o);
+    orow += ostep;
   }
 
-  if (t_end == len && p.cs_out != nullptr) {
+  // new conv state = the last KT-1 rows of X (the wave holding the
+  // sequence's last token writes it; the window itself has run past it)
+  if (t_end == len && p.cs_out != nullptr && active) {
 #pragma unroll
-    for (int i = 0; i < KT - 1; ++i)
-      store_vec<CPL, DT>(p.cs_out, (static_cast<int64_t>(seq) * (KT - 1) + i) * C + c0, win[i]);
+    for (int i = 0; i < KT - 1; ++i) {
+      float r[CPL];
+      load_x(len + i, r);
+      store8<DT>(p.cs_out, (static_cast<int64_t>(seq) * (KT - 1) + i) * C + c0, r);
+    }
   }
 }
 
@@ -244,11 +329,10 @@ extern "C" int gdn_conv_prologue(const void* qkv, int io_dtype, const void* conv
   if (conv_state_out != nullptr && conv_state_out == conv_state_in)
     return fail(GDN_ERR_INVALID, "gdn_conv_prologue: conv_state_out must not alias conv_state_in");
   if (!(eps >= 0.0f)) return fail(GDN_ERR_INVALID, "gdn_conv_prologue: eps must be >= 0");
-  const size_t al = io_dtype == GDN_DTYPE_F32 ? 16 : 8;
-  if (!gdn_host::aligned(qkv, al) || !gdn_host::aligned(q_out, al) || !gdn_host::aligned(k_out, al) ||
-      !gdn_host::aligned(v_out, al) || !gdn_host::aligned(conv_state_in, al) ||
-      !gdn_host::aligned(conv_state_out, al))
-    return fail(GDN_ERR_INVALID, "gdn_conv_prologue: misaligned pointer");
+  if (!gdn_host::aligned(qkv, 16) || !gdn_host::aligned(q_out, 16) || !gdn_host::aligned(k_out, 16) ||
+      !gdn_host::aligned(v_out, 16) || !gdn_host::aligned(conv_state_in, 16) ||
+      !gdn_host::aligned(conv_state_out, 16) || !gdn_host::aligned(weight, 16))
+    return fail(GDN_ERR_INVALID, "gdn_conv_prologue: pointers must be 16-byte aligned");
   if (B == 0) return GDN_OK;
   if (B > 65535 || S > INT32_MAX / 2)
     return fail(GDN_ERR_UNSUPPORTED, "gdn_conv_prologue: B or S too large");
@@ -274,7 +358,8 @@ extern "C" int gdn_conv_prologue(const void* qkv, int io_dtype, const void* conv
   constexpr int RW = kRun * kWaves;
   dim3 block(64 * kWaves);
   dim3 grid;
-  grid.x = static_cast<unsigned>(2 * Hk + Hv);
+  const int64_t heads_per_wave = 512 / Dk;  // a lane covers 8 channels
+  grid.x = static_cast<unsigned>((2 * Hk + Hv + heads_per_wave - 1) / heads_per_wave);
   if (cu_seqlens != nullptr) {
     grid.y = static_cast<unsigned>((S + RW - 1) / RW + B);
     grid.z = 1;
@@ -283,11 +368,17 @@ extern "C" int gdn_conv_prologue(const void* qkv, int io_dtype, const void* conv
     grid.z = static_cast<unsigned>(B);
   }
   hipStream_t st = static_cast<hipStream_t>(stream);
-#define GDN_PRO_LAUNCH(D_, DT_)                                                              \
-  if (w_dtype == GDN_DTYPE_F32)                                                             \
-    hipLaunchKernelGGL((prologue_kernel<D_, DT_, true>), grid, block, 0, st, p);          \
-  else                                                                                      \
-    hipLaunchKernelGGL((prologue_kernel<D_, DT_, false>), grid, block, 0, st, p)
+#define GDN_PRO_LAUNCH_M(D_, DT_, W_)                                                    \
+  if (mask != nullptr)                                                                  \
+    hipLaunchKernelGGL((prologue_kernel<D_, DT_, W_, true>), grid, block, 0, st, p);    \
+  else                                                                                  \
+    hipLaunchKernelGGL((prologue_kernel<D_, DT_, W_, false>), grid, block, 0, st, p)
+#define GDN_PRO_LAUNCH(D_, DT_)            \
+  if (w_dtype == GDN_DTYPE_F32) {          \
+    GDN_PRO_LAUNCH_M(D_, DT_, true);       \
+  } else {                                 \
+    GDN_PRO_LAUNCH_M(D_, DT_, false);      \
+  }
 #define GDN_PRO_DT(D_)                                             \
   switch (io_dtype) {                                             \
     case GDN_DTYPE_BF16: GDN_PRO_LAUNCH(D_, GDN_DTYPE_BF16); break; \
@@ -301,6 +392,7 @@ extern "C" int gdn_conv_prologue(const void* qkv, int io_dtype, const void* conv
   }
 #undef GDN_PRO_DT
 #undef GDN_PRO_LAUNCH
+#undef GDN_PRO_LAUNCH_M
   return gdn_host::check_launch("gdn_conv_prologue");
 }
 

@@ -77,6 +77,22 @@ def test_packed_sequences():
     check(qkv, w, cs, None, 2, 4, 128, cu=cu)
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+def test_io_dtypes_with_fp32_taps_and_partial_head_group(dtype):
+    # 2*1 + 1 = 3 heads of 128 channels: a wavefront covers 4 heads, so one
+    # lane group has no head and must store nothing
+    qkv, w, cs, mask = draw_prologue(25, 2, 40, 1, 1, 128, mask_p=0.3, dtype=dtype)
+    check(qkv, w.float(), cs, mask, 1, 1, 128)
+
+
+def test_packed_sequences_with_mask_and_trailing_empty():
+    lens = [70, 3, 0]
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    qkv, w, _, mask = draw_prologue(26, 1, int(cu[-1]), 2, 4, 64, mask_p=0.25)
+    cs = torch.tensor(np.random.default_rng(2).standard_normal((len(lens), 3, qkv.shape[-1]))).to(torch.bfloat16)
+    check(qkv, w, cs, mask, 2, 4, 64, cu=cu)
+
+
 def test_fp32_golden_fixture():
     with np.load(GOLD / "prologue_small.npz") as z:
         f = {k: z[k] for k in z.files}
