@@ -199,19 +199,22 @@ def bench_prefill(torch, mx, dev, timer, iters=10):
     A_log = (torch.rand(Hv, generator=gen) * math.log(16.0)).to(dev)
     dt_bias = (torch.rand(Hv, generator=gen) * 2 - 1).to(dev)
     ws = torch.empty(mx.chunk_workspace_bytes(1, T, Hv, Dk, Dv), dtype=torch.uint8, device=dev)
-    out = {}
+    # prepared launches (validated once, as a serving loop issues them): the
+    # prologue's q/k/v buffers are the chunked pass's inputs
+    pro = mx.prepare_conv_prologue(qkv, w, Hk, Hv, Dk, Dv, cs)
+    q, k, v, _ = pro.outputs
+    gdn = mx.prepare_chunked(q, k, v, a, b, A_log, dt_bias, None, workspace=ws)
+    out = {"S": gdn.outputs[1]}
 
     def step(i):
-        q, k, v, _ = mx.gdn_conv_prologue(qkv, w, Hk, Hv, Dk, Dv, cs)
-        out["y"], out["S"] = mx.gated_delta_update(q, k, v, a, b, A_log, dt_bias, None, chunked=True, workspace=ws)
-
-    q, k, v, _ = mx.gdn_conv_prologue(qkv, w, Hk, Hv, Dk, Dv, cs)
+        pro.launch()
+        gdn.launch()
 
     def gdn_only(i):
-        mx.gated_delta_update(q, k, v, a, b, A_log, dt_bias, None, chunked=True, workspace=ws)
+        gdn.launch()
 
     def pro_only(i):
-        mx.gdn_conv_prologue(qkv, w, Hk, Hv, Dk, Dv, cs)
+        pro.launch()
 
     for _ in range(3):
         step(0)
@@ -242,10 +245,11 @@ def bench_mixed(torch, mx, dev, timer, iters=10):
     cplan = mx.prepare_recurrent(None, ver["k"], ver["v"], ver["a"], ver["b"], ver["A_log"], ver["dt_bias"],
                                  ver["state"], y=False, commit_len=n_b, state_out=torch.empty_like(ver["state"]))
     st_out = torch.empty_like(pf_state)
+    pplan = mx.prepare_chunked(pf["q"], pf["k"], pf["v"], pf["a"], pf["b"], pf["A_log"], pf["dt_bias"], pf_state,
+                               cu_seqlens=cu, workspace=ws, state_out=st_out)
 
     def step(i):
-        mx.gated_delta_update(pf["q"], pf["k"], pf["v"], pf["a"], pf["b"], pf["A_log"], pf["dt_bias"], pf_state,
-                              cu_seqlens=cu, chunked=True, workspace=ws, state_out=st_out)
+        pplan.launch()
         dplan.launch()
         vplan.launch()
         cplan.launch()

@@ -16,9 +16,10 @@ from .gated_delta import (
     gated_delta_ops,
     gated_delta_update,
     gated_delta_verify,
+    prepare_chunked,
     prepare_recurrent,
 )
-from .conv import conv_state_commit, gdn_conv_prologue
+from .conv import conv_state_commit, gdn_conv_prologue, prepare_conv_prologue
 from .cache import ArraysCache, clone_ssm, merge_layer, restore_ssm, restore_ssm_snapshot, snapshot_ssm
 from .mixer import GatedDeltaNet, commit_verified, gated_rms_norm
 
@@ -43,5 +44,7 @@ __all__ = [
     "gated_delta_update",
     "gated_delta_verify",
     "gdn_conv_prologue",
+    "prepare_chunked",
+    "prepare_conv_prologue",
     "prepare_recurrent",
 ]

@@ -15,9 +15,10 @@ from typing import Optional
 import torch
 
 from . import _lib
-from .gated_delta import IntSeq, _contig, _cu_seqlens, _dtype_code, _int_rows, _mask_u8, _ptr, _require_device, _stream
+from .gated_delta import (IntSeq, PreparedCall, _contig, _cu_seqlens, _dtype_code, _int_rows, _mask_u8, _ptr,
+                          _require_device, _stream)
 
-__all__ = ["gdn_conv_prologue", "conv_state_commit"]
+__all__ = ["gdn_conv_prologue", "prepare_conv_prologue", "conv_state_commit"]
 
 
 def _weight_2d(conv_weight: torch.Tensor, C: int) -> torch.Tensor:
@@ -35,21 +36,8 @@ def _weight_2d(conv_weight: torch.Tensor, C: int) -> torch.Tensor:
     return w.contiguous()
 
 
-def gdn_conv_prologue(qkv: torch.Tensor, conv_weight: torch.Tensor, num_k_heads: int,
-                      num_v_heads: int, head_k_dim: int, head_v_dim: int,
-                      conv_state: Optional[torch.Tensor] = None, mask: Optional[torch.Tensor] = None,
-                      *, cu_seqlens: Optional[IntSeq] = None, eps: float = 1e-6,
-                      write_conv_state: bool = True):
-    """Returns ``(q, k, v, new_conv_state)``.
-
-    qkv ``[B,S,C]`` (C = 2*Hk*Dk + Hv*Dv, channels q | k | v), conv_weight
-    ``[C,K]`` (or ``[C,K,1]`` / ``[C,1,K]``), conv_state ``[B,K-1,C]`` or None
-    (zeros), mask ``[B,S]`` or None.  q, k are ``[B,S,Hk,Dk]``, v is
-    ``[B,S,Hv,Dv]``, all in qkv's dtype; the new conv state is the last K-1
-    rows of ``concat(conv_state, masked qkv)`` (None if not requested).
-    With ``cu_seqlens`` the rows are packed ragged sequences (``B == 1``) and
-    conv_state has one row per sequence.
-    """
+def _prologue_args(qkv, conv_weight, num_k_heads, num_v_heads, head_k_dim, head_v_dim, conv_state, mask,
+                   cu_seqlens, eps, write_conv_state):
     dev = _require_device([qkv, conv_weight, conv_state, mask], ["qkv", "conv_weight", "conv_state", "mask"])
     if qkv.dim() != 3:
         raise ValueError("qkv must be [B, S, C]")
@@ -75,11 +63,49 @@ def gdn_conv_prologue(qkv: torch.Tensor, conv_weight: torch.Tensor, num_k_heads:
     k = torch.empty(B, S, Hk, Dk, dtype=qkv.dtype, device=dev)
     v = torch.empty(B, S, Hv, Dv, dtype=qkv.dtype, device=dev)
     cs_out = torch.empty(n_rows, Kt - 1, C, dtype=qkv.dtype, device=dev) if write_conv_state else None
+    args = (_ptr(qkv), io, _ptr(conv_state), _ptr(w), wdt, _ptr(m), _ptr(cu), _ptr(q), _ptr(k), _ptr(v),
+            _ptr(cs_out), n_rows, S, Hk, Hv, Dk, Dv, Kt, float(eps), _stream(dev))
+    keep = dict(qkv=qkv, conv_state=conv_state, w=w, mask=m, cu=cu)
+    return args, keep, (q, k, v, cs_out), dev
+
+
+def gdn_conv_prologue(qkv: torch.Tensor, conv_weight: torch.Tensor, num_k_heads: int,
+                      num_v_heads: int, head_k_dim: int, head_v_dim: int,
+                      conv_state: Optional[torch.Tensor] = None, mask: Optional[torch.Tensor] = None,
+                      *, cu_seqlens: Optional[IntSeq] = None, eps: float = 1e-6,
+                      write_conv_state: bool = True):
+    """Returns ``(q, k, v, new_conv_state)``.
+
+    qkv ``[B,S,C]`` (C = 2*Hk*Dk + Hv*Dv, channels q | k | v), conv_weight
+    ``[C,K]`` (or ``[C,K,1]`` / ``[C,1,K]``), conv_state ``[B,K-1,C]`` or None
+    (zeros), mask ``[B,S]`` or None.  q, k are ``[B,S,Hk,Dk]``, v is
+    ``[B,S,Hv,Dv]``, all in qkv's dtype; the new conv state is the last K-1
+    rows of ``concat(conv_state, masked qkv)`` (None if not requested).
+    With ``cu_seqlens`` the rows are packed ragged sequences (``B == 1``) and
+    conv_state has one row per sequence.
+    """
+    args, _keep, outs, dev = _prologue_args(qkv, conv_weight, num_k_heads, num_v_heads, head_k_dim, head_v_dim,
+                                            conv_state, mask, cu_seqlens, eps, write_conv_state)
     with torch.cuda.device(dev):
-        _lib.call("gdn_conv_prologue", _ptr(qkv), io, _ptr(conv_state), _ptr(w), wdt, _ptr(m), _ptr(cu),
-                  _ptr(q), _ptr(k), _ptr(v), _ptr(cs_out), n_rows, S, Hk, Hv, Dk, Dv, Kt, float(eps),
-                  _stream(dev))
-    return q, k, v, cs_out
+        _lib.call("gdn_conv_prologue", *args)
+    return outs
+
+
+def prepare_conv_prologue(qkv: torch.Tensor, conv_weight: torch.Tensor, num_k_heads: int,
+                          num_v_heads: int, head_k_dim: int, head_v_dim: int,
+                          conv_state: Optional[torch.Tensor] = None, mask: Optional[torch.Tensor] = None,
+                          *, cu_seqlens: Optional[IntSeq] = None, eps: float = 1e-6,
+                          write_conv_state: bool = True) -> PreparedCall:
+    """Validates the prologue once; ``launch()`` re-issues it (``outputs`` = ``(q, k, v, conv_state)``).
+
+    qkv must be contiguous (it is bound by address, so refill it in place).
+    """
+    if not qkv.is_contiguous():
+        raise ValueError("qkv must be contiguous for a prepared launch")
+    args, keep, outs, dev = _prologue_args(qkv, conv_weight, num_k_heads, num_v_heads, head_k_dim,
+                                           head_v_dim, conv_state, mask, cu_seqlens, eps, write_conv_state)
+    keep.update(q=outs[0], k=outs[1], v=outs[2], cs_out=outs[3])
+    return PreparedCall("gdn_conv_prologue", args, keep, outs, dev)
 
 
 def conv_state_commit(conv_state: Optional[torch.Tensor], qkv: torch.Tensor, n_commit: IntSeq,

@@ -207,60 +207,98 @@ __global__ __launch_bounds__(256) void recurrent_kernel(const RecParams p) {
   }
 }
 
-// Multi-token body (verify, commit, packed rows): the workgroup stages a
-// tile of kTile tokens -- k and q as fp32, the transformed gates, the mask
-// and the v values of its rows -- in LDS, then every wave walks the tile
-// from LDS.  All of a tile's global loads are in flight together.
+// Multi-token body (verify, commit, packed rows): the workgroup (always 4
+// waves, 32 state rows) stages a tile of kTile tokens -- k and q as fp32, the
+// transformed gates, the mask and the v values of its rows -- in LDS, then
+// every wave walks the tile from LDS.  The first tile's global loads are
+// issued before the state stream: loads complete in issue order, so the tile
+// reaches LDS while the state is still arriving.
 constexpr int kTile = 16;
-constexpr int kMaxRowsPerWg = 32;
+constexpr int kTileThreads = 256;
+constexpr int kTileRows = kTileThreads / kLanesPerRow;  // 32
 
 template <int DK, int DT, int GF>
-__global__ __launch_bounds__(256) void recurrent_tile_kernel(const RecParams p) {
+__global__ __launch_bounds__(kTileThreads) void recurrent_tile_kernel(const RecParams p) {
   constexpr int EPL = DK / kLanesPerRow;
   constexpr int NV = EPL / 4;
+  constexpr int KV4 = kTile * DK / 4 / kTileThreads;  // float4 of k (and q) per thread
+  constexpr int VV = kTile * kTileRows / kTileThreads;  // v values per thread
+  static_assert(KV4 >= 1 && VV >= 1, "tile must cover the workgroup");
   const RowCtx c = row_ctx<DK>(p);
   const int tid = threadIdx.x;
-  const int rows_wg = blockDim.x / kLanesPerRow;
-  const int dv0 = blockIdx.x * rows_wg;
+  const int dv0 = blockIdx.x * kTileRows;
 
   __shared__ __align__(16) float Kt[kTile][DK];
   __shared__ __align__(16) float Qt[kTile][DK];
-  __shared__ float Vt[kTile][kMaxRowsPerWg];
+  __shared__ float Vt[kTile][kTileRows];
   __shared__ float Gt[kTile], Bt[kTile];
   __shared__ uint8_t Mt[kTile];
 
   float ea, db;
   param_load<GF, DT>(p.ga, c.hv, ea, db);
+
+  f32x4 kr[KV4], qr[KV4];
+  float vr[VV];
+  float gx = 0.0f, gy = 0.0f;
+  uint8_t mm = 1;
+  // rows past the tile's n tokens re-read its last token (never used)
+  auto issue_tile = [&](int t0, int n) {
+#pragma unroll
+    for (int it = 0; it < KV4; ++it) {
+      const int i = tid + kTileThreads * it;
+      const int j = i / (DK / 4), e = (i % (DK / 4)) * 4;
+      const int64_t off = ((c.tok0 + t0 + min(j, n - 1)) * p.Hk + c.hk) * DK + e;
+      kr[it] = IO<DT>::load4(p.k, off);
+      if (c.want_y) qr[it] = IO<DT>::load4(p.q, off);
+    }
+#pragma unroll
+    for (int it = 0; it < VV; ++it) {
+      const int i = tid + kTileThreads * it;
+      const int j = i / kTileRows, r = i % kTileRows;
+      const int64_t tok = c.tok0 + t0 + min(j, n - 1);
+      vr[it] = IO<DT>::load1(p.v, (tok * p.Hv + c.hv) * p.Dv + min(dv0 + r, p.Dv - 1));
+    }
+    if (tid < kTile) {
+      const int64_t tok = c.tok0 + t0 + min(tid, n - 1);
+      gate_load<GF, DT>(p.ga, tok * p.Hv + c.hv, gx, gy);
+      const uint8_t* mp = p.mask != nullptr ? p.mask + tok : &kActive;
+      mm = *mp;
+    }
+  };
+  auto store_tile = [&]() {
+#pragma unroll
+    for (int it = 0; it < KV4; ++it) {
+      const int i = tid + kTileThreads * it;
+      const int j = i / (DK / 4), e = (i % (DK / 4)) * 4;
+      *reinterpret_cast<f32x4*>(&Kt[j][e]) = kr[it];
+      if (c.want_y) *reinterpret_cast<f32x4*>(&Qt[j][e]) = qr[it];
+    }
+#pragma unroll
+    for (int it = 0; it < VV; ++it) {
+      const int i = tid + kTileThreads * it;
+      Vt[i / kTileRows][i % kTileRows] = vr[it];
+    }
+    if (tid < kTile) {
+      float g, beta;
+      gate_transform<GF>(p.ga.mode, gx, gy, ea, db, g, beta);
+      Gt[tid] = g;
+      Bt[tid] = beta;
+      Mt[tid] = mm;
+    }
+  };
+
+  if (c.steps > 0) issue_tile(0, min(kTile, c.steps));
   float s[EPL];
   load_state<DK>(p, c, s);
   if (c.write_state && c.commit == 0 && c.row_ok) store_row<EPL>(p.state_out + c.srow, c.sub, s);
 
   for (int t0 = 0; t0 < c.steps; t0 += kTile) {
     const int n = min(kTile, c.steps - t0);
-    __syncthreads();  // the previous tile is consumed
-    // k and q: n tokens x DK, 4 elements per thread per pass
-    for (int i = tid; i < kTile * DK / 4; i += blockDim.x) {
-      const int j = i / (DK / 4), e = (i % (DK / 4)) * 4;
-      const int64_t tok = c.tok0 + t0 + min(j, n - 1);
-      const int64_t off = (tok * p.Hk + c.hk) * DK + e;
-      *reinterpret_cast<f32x4*>(&Kt[j][e]) = IO<DT>::load4(p.k, off);
-      if (c.want_y) *reinterpret_cast<f32x4*>(&Qt[j][e]) = IO<DT>::load4(p.q, off);
+    if (t0 > 0) {
+      __syncthreads();  // the previous tile is consumed
+      issue_tile(t0, n);
     }
-    for (int i = tid; i < kTile * rows_wg; i += blockDim.x) {
-      const int j = i / rows_wg, r = i % rows_wg;
-      const int64_t tok = c.tok0 + t0 + min(j, n - 1);
-      Vt[j][r] = IO<DT>::load1(p.v, (tok * p.Hv + c.hv) * p.Dv + min(dv0 + r, p.Dv - 1));
-    }
-    if (tid < kTile) {
-      const int64_t tok = c.tok0 + t0 + min(tid, n - 1);
-      const uint8_t* mp = p.mask != nullptr ? p.mask + tok : &kActive;
-      float x, y, g, beta;
-      gate_load<GF, DT>(p.ga, tok * p.Hv + c.hv, x, y);
-      gate_transform<GF>(p.ga.mode, x, y, ea, db, g, beta);
-      Gt[tid] = g;
-      Bt[tid] = beta;
-      Mt[tid] = *mp;
-    }
+    store_tile();
     __syncthreads();
 
     const int rloc = threadIdx.x / kLanesPerRow;
@@ -399,8 +437,11 @@ int run_recurrent(const gdn_recurrent_args* a) {
 
   // Waves per workgroup: the largest of 4/2/1 that still gives >= 1024
   // workgroups (4 per CU), so small batches spread over the 256 CUs.
-  int waves = 1;
-  for (int w = 4; w >= 1; w >>= 1) {
+  // Tokens per row > 1 (or packed rows): stage token tiles in LDS, with
+  // workgroups of 4 waves.
+  const bool pf = a->T > 1 || a->cu_seqlens != nullptr;
+  int waves = pf ? 4 : 1;
+  for (int w = 4; w >= 1 && !pf; w >>= 1) {
     const int64_t rows_per_wg = 8 * w;
     const int64_t wgs = a->B * a->Hv * ((a->Dv + rows_per_wg - 1) / rows_per_wg);
     if (wgs >= 1024 || w == 1) {
@@ -413,8 +454,6 @@ int run_recurrent(const gdn_recurrent_args* a) {
   dim3 grid(static_cast<unsigned>((a->Dv + rows_per_wg - 1) / rows_per_wg),
             static_cast<unsigned>(a->Hv), static_cast<unsigned>(a->B));
   hipStream_t st = static_cast<hipStream_t>(a->stream);
-  // Tokens per row > 1 (or packed rows): stage token tiles in LDS.
-  const bool pf = a->T > 1 || a->cu_seqlens != nullptr;
   switch (a->Dk) {
     case 64:
       return launch_dt<64>(a->qkv_dtype, gf, pf, grid, block, st, p);

@@ -35,7 +35,9 @@ __all__ = [
     "gated_delta_commit",
     "chunk_workspace_bytes",
     "prepare_recurrent",
+    "prepare_chunked",
     "PreparedRecurrent",
+    "PreparedCall",
     "CHUNK_MIN_TOKENS",
 ]
 
@@ -351,8 +353,31 @@ def chunk_workspace_bytes(n_seqs: int, n_tok: int, Hv: int, Dk: int, Dv: int, ch
     return int(_lib.load().gdn_chunk_workspace_bytes(n_seqs, n_tok, Hv, Dk, Dv, chunk))
 
 
-def _chunked(q, k, v, gx, gy, gate_mode, A_log, dt_bias, state, *, cu_seqlens=None,
-             state_out=None, workspace=None):
+class PreparedCall:
+    """A validated ``libgdn`` call that can be re-issued without re-validation.
+
+    Holds the argument tuple and keeps every tensor it points to alive; each
+    ``launch()`` enqueues the same work on the stream current at ``prepare``
+    time (what a serving loop repeats every step).  ``outputs`` are the
+    tensors the call writes.
+    """
+
+    def __init__(self, fn: str, args: tuple, keep: dict, outputs: tuple, dev):
+        self._fn_name = fn
+        self._args = args
+        self._keep = keep
+        self.outputs = outputs
+        self.device = dev
+        self._fn = getattr(_lib.load(), fn)
+
+    def launch(self):
+        st = self._fn(*self._args)
+        if st != _lib.OK:
+            _lib.check(self._fn_name, st)
+
+
+def _chunk_args(q, k, v, gx, gy, gate_mode, A_log, dt_bias, state, *, cu_seqlens=None,
+                state_out=None, workspace=None):
     names = ["q", "k", "v", "a/g", "b/beta", "A_log", "dt_bias", "state", "state_out"]
     dev = _require_device([q, k, v, gx, gy, A_log, dt_bias, state, state_out], names)
     packed = cu_seqlens is not None
@@ -375,14 +400,41 @@ def _chunked(q, k, v, gx, gy, gate_mode, A_log, dt_bias, state, *, cu_seqlens=No
     ws_bytes = chunk_workspace_bytes(n_seqs, n_tok, sh.Hv, sh.Dk, sh.Dv, CHUNK)
     if workspace is None or workspace.numel() * workspace.element_size() < ws_bytes:
         workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    args = (_ptr(q), _ptr(k), _ptr(v), qkv_code, gate_mode, _ptr(gx), _ptr(gy), gate_code, _ptr(A_log),
+            _ptr(dt_bias), param_code, _ptr(state), _ptr(y_t), _ptr(out_state), _ptr(cu), n_seqs, n_tok,
+            sh.Hk, sh.Hv, sh.Dk, sh.Dv, CHUNK, _ptr(workspace), ws_bytes, _stream(dev))
+    keep = dict(q=q, k=k, v=v, gx=gx, gy=gy, A_log=A_log, dt_bias=dt_bias, state=state, cu=cu,
+                workspace=workspace)
+    return args, keep, y_t, out_state, dev
+
+
+def _chunked(q, k, v, gx, gy, gate_mode, A_log, dt_bias, state, *, cu_seqlens=None,
+             state_out=None, workspace=None):
+    args, _keep, y_t, out_state, dev = _chunk_args(q, k, v, gx, gy, gate_mode, A_log, dt_bias, state,
+                                                   cu_seqlens=cu_seqlens, state_out=state_out,
+                                                   workspace=workspace)
     with torch.cuda.device(dev):
-        _lib.call(
-            "gdn_chunk_fwd", _ptr(q), _ptr(k), _ptr(v), qkv_code, gate_mode, _ptr(gx), _ptr(gy),
-            gate_code, _ptr(A_log), _ptr(dt_bias), param_code, _ptr(state), _ptr(y_t),
-            _ptr(out_state), _ptr(cu), n_seqs, n_tok, sh.Hk, sh.Hv, sh.Dk, sh.Dv, CHUNK,
-            _ptr(workspace), ws_bytes, _stream(dev),
-        )
+        _lib.call("gdn_chunk_fwd", *args)
     return y_t, out_state
+
+
+def prepare_chunked(q, k, v, a, b, A_log, dt_bias, state=None, *, cu_seqlens=None, state_out=None,
+                    workspace=None, gates_precomputed=False) -> PreparedCall:
+    """Validates a chunked prefill once; ``launch()`` re-issues it.
+
+    Same arguments as :func:`gated_delta_update` with ``chunked=True``;
+    ``outputs`` is ``(y, new_state)``.  The inputs are bound by address, so a
+    serving loop refills them in place between launches.
+    """
+    mode = _lib.GATES_PRE if gates_precomputed else _lib.GATES_RAW
+    args, keep, y_t, out_state, dev = _chunk_args(q, k, v, a, b, mode, A_log, dt_bias, state,
+                                                  cu_seqlens=cu_seqlens, state_out=state_out,
+                                                  workspace=workspace)
+    for name in ("q", "k", "v", "gx", "gy"):
+        if keep[name].data_ptr() != {"q": q, "k": k, "v": v, "gx": a, "gy": b}[name].data_ptr():
+            raise ValueError(f"{name} must be contiguous for a prepared launch")
+    keep.update(y=y_t, state_out=out_state)
+    return PreparedCall("gdn_chunk_fwd", args, keep, (y_t, out_state), dev)
 
 
 def _use_chunked(chunked, k, mask, cu_seqlens, T):

@@ -113,3 +113,18 @@ def test_in_place_state():
                                    state_out=st, chunked=True)
     assert S2.data_ptr() == st.data_ptr()
     assert torch.equal(S2, S1) and torch.equal(y2, y1)
+
+
+def test_prepared_launch_equals_call():
+    d = draw(308, 1, 300, 2, 4, 128, 128)
+    t, _ = to_torch(d, DEV)
+    cu = torch.tensor([0, 70, 70, 300], dtype=torch.int32)
+    st = torch.tensor(np.random.default_rng(9).normal(0.0, 0.02, (3, 4, 128, 128)), dtype=torch.float32,
+                      device=DEV)
+    y_ref, S_ref = chunked(t, st, cu=cu)
+    plan = mx.prepare_chunked(t["q"], t["k"], t["v"], t["a"], t["b"], t["A_log"], t["dt_bias"], st,
+                              cu_seqlens=cu)
+    for _ in range(2):  # re-issued launches recompute the same outputs
+        plan.launch()
+        y, S = plan.outputs
+        assert torch.equal(y, y_ref) and torch.equal(S, S_ref)

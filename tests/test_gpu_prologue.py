@@ -127,3 +127,14 @@ def test_conv_state_commit():
                                        cs.double().numpy(), mask.numpy())
     ref = gdn.conv_state_commit(ci, n, 4)
     np.testing.assert_array_equal(out.float().cpu().numpy(), ref)
+
+
+def test_prepared_launch_equals_call():
+    qkv, w, cs, mask = draw_prologue(27, 2, 50, 2, 4, 128, mask_p=0.2)
+    dev = [x.to(DEV) for x in (qkv, w, cs, mask)]
+    ref = mx.gdn_conv_prologue(*dev[:2], 2, 4, 128, 128, dev[2], dev[3])
+    plan = mx.prepare_conv_prologue(*dev[:2], 2, 4, 128, 128, dev[2], dev[3])
+    for _ in range(2):
+        plan.launch()
+        for got, want in zip(plan.outputs, ref):
+            assert torch.equal(got, want)
