@@ -316,6 +316,10 @@ def main():
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 256 MiB device-to-device copy (counter calibration) and exit")
     ap.add_argument("--prefill-only", action="store_true", help="only the T=4096 prefill workload")
+    ap.add_argument("--hbm-ceiling", action="store_true",
+                    help="only time in-place streaming updates (read + write) of 128 MiB and 1 GiB fp32 "
+                         "with a library elementwise kernel, the practical HBM ceiling the decode kernel is "
+                         "compared against, and exit")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -348,6 +352,17 @@ def main():
             torch.mul(src, 2.0, out=dst)
         torch.cuda.synchronize()
         print(json.dumps({"copy_bytes_per_launch": 2 * src.numel() * 4, "launches": args.steps}), flush=True)
+        return
+    if args.hbm_ceiling:
+        res = {}
+        for mib in (128, 1024):
+            x = torch.zeros(mib * 1024 * 1024 // 4, device=dev)
+            for _ in range(5):
+                x.mul_(0.5)
+            t = timer.total_ms(lambda i: x.mul_(0.5), 50) / 50
+            res[f"{mib}MiB"] = {"ms": round(t, 5), "GB/s": round(2 * x.numel() * 4 / (t * 1e-3) / 1e9, 1)}
+            del x
+        print(json.dumps({"inplace_stream": res, "peak_GB/s": HBM_PEAK_GBS}), flush=True)
         return
     if args.prefill_only:
         p = bench_prefill(torch, mx, dev, timer, iters=args.steps)
