@@ -558,7 +558,7 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(const ChunkParams p) {
     return c;
   };
 
-  WaveOps o;
+  WaveOps o = {};
   auto load_kq = [&](const ChunkBufs& c) {
     static_for<4>([&](auto s) {
       o.k[s.value] = buf_bf16x8(c.rec, off_kq + 1024 * s.value, 0);
@@ -573,10 +573,16 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(const ChunkParams p) {
     o.b = buf_f32x4(c.rec, off_g4 + (kOffBeta - kOffGam));
     o.gy = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(c.rec, off_g1, 0, 0));
   };
+  // T and P are lower triangular: the rows of waves 0 and 1 (tokens < 32)
+  // have no entries in the second 32-column block, whose loads and products
+  // those waves skip (wave-uniform branches).
+  const bool full_rows = wave >= 2;
   auto load_t = [&](const ChunkBufs& c) {
     static_for<2>([&](auto s) {
-      o.th[s.value] = buf_bf16x8(c.rec, off_rows + 1024 * s.value, kOffTh);
-      o.tl[s.value] = buf_bf16x8(c.rec, off_rows + 1024 * s.value, kOffTl);
+      if (s.value == 0 || full_rows) {
+        o.th[s.value] = buf_bf16x8(c.rec, off_rows + 1024 * s.value, kOffTh);
+        o.tl[s.value] = buf_bf16x8(c.rec, off_rows + 1024 * s.value, kOffTl);
+      }
     });
   };
   auto load_e = [&](const ChunkBufs& c) { o.e = buf_f32x4(c.rec, off_g4 + (kOffE - kOffGam)); };
@@ -590,8 +596,10 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(const ChunkParams p) {
   };
   auto load_p = [&](const ChunkBufs& c) {
     static_for<2>([&](auto s) {
-      o.ph[s.value] = buf_bf16x8(c.rec, off_rows + 1024 * s.value, kOffPh);
-      o.pl[s.value] = buf_bf16x8(c.rec, off_rows + 1024 * s.value, kOffPl);
+      if (s.value == 0 || full_rows) {
+        o.ph[s.value] = buf_bf16x8(c.rec, off_rows + 1024 * s.value, kOffPh);
+        o.pl[s.value] = buf_bf16x8(c.rec, off_rows + 1024 * s.value, kOffPl);
+      }
     });
   };
 
@@ -657,6 +665,7 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(const ChunkParams p) {
     // ---- U = T R for this wave's 16 tokens
     f32x4 u0 = z, u1 = z;
     static_for<2>([&](auto s) {
+      if (s.value == 1 && !full_rows) return;
       const int kc = 32 * s.value + lg8;
       const bf16x8 rh = lds8(&Rh[lr][kc]);
       u0 = mfma16(o.th[s.value], rh, u0);
@@ -690,6 +699,7 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(const ChunkParams p) {
     // ---- Y^T = gamma X_Q^T + U^T P^T (rows x this wave's 16 tokens)
     f32x4 y0 = z, y1 = z;
     static_for<2>([&](auto s) {
+      if (s.value == 1 && !full_rows) return;
       const int kc = 32 * s.value + lg8;
       const bf16x8 uh = lds8(&Uh[lr][kc]);
       y0 = mfma16(uh, o.ph[s.value], y0);
