@@ -228,6 +228,10 @@ def bench_prefill(torch, mx, dev, timer, iters=10):
 
 
 def bench_mixed(torch, mx, dev, timer, iters=10):
+    """One continuous-batching step: the packed prefills run on the current
+    stream while the decode, verify and commit launches (independent rows
+    and states) run beside them on a second stream; the step ends when both
+    are done."""
     gen = torch.Generator().manual_seed(1004)
     lens = [1024, 2560, 7168]
     n_tok = sum(lens)
@@ -238,21 +242,26 @@ def bench_mixed(torch, mx, dev, timer, iters=10):
     ver = draw(gen, 16, 4, torch, dev)
     n_b = torch.randint(1, 5, (16,), generator=gen, dtype=torch.int32).to(dev)
     ws = torch.empty(mx.chunk_workspace_bytes(3, n_tok, Hv, Dk, Dv), dtype=torch.uint8, device=dev)
-    dplan = mx.prepare_recurrent(dec["q"], dec["k"], dec["v"], dec["a"], dec["b"], dec["A_log"], dec["dt_bias"],
-                                 dec["state"], state_out=dec["state"])
-    vplan = mx.prepare_recurrent(ver["q"], ver["k"], ver["v"], ver["a"], ver["b"], ver["A_log"], ver["dt_bias"],
-                                 ver["state"], write_state=False)
-    cplan = mx.prepare_recurrent(None, ver["k"], ver["v"], ver["a"], ver["b"], ver["A_log"], ver["dt_bias"],
-                                 ver["state"], y=False, commit_len=n_b, state_out=torch.empty_like(ver["state"]))
+    main = torch.cuda.current_stream(dev)
+    side = torch.cuda.Stream(dev)  # default priority
+    with torch.cuda.stream(side):
+        dplan = mx.prepare_recurrent(dec["q"], dec["k"], dec["v"], dec["a"], dec["b"], dec["A_log"],
+                                     dec["dt_bias"], dec["state"], state_out=dec["state"])
+        vplan = mx.prepare_recurrent(ver["q"], ver["k"], ver["v"], ver["a"], ver["b"], ver["A_log"],
+                                     ver["dt_bias"], ver["state"], write_state=False)
+        cplan = mx.prepare_recurrent(None, ver["k"], ver["v"], ver["a"], ver["b"], ver["A_log"], ver["dt_bias"],
+                                     ver["state"], y=False, commit_len=n_b, state_out=torch.empty_like(ver["state"]))
     st_out = torch.empty_like(pf_state)
     pplan = mx.prepare_chunked(pf["q"], pf["k"], pf["v"], pf["a"], pf["b"], pf["A_log"], pf["dt_bias"], pf_state,
                                cu_seqlens=cu, workspace=ws, state_out=st_out)
 
     def step(i):
+        side.wait_stream(main)
         pplan.launch()
         dplan.launch()
         vplan.launch()
         cplan.launch()
+        main.wait_stream(side)
 
     for _ in range(3):
         step(0)
@@ -260,7 +269,8 @@ def bench_mixed(torch, mx, dev, timer, iters=10):
     flops = prefill_flops(lens)
     hbm = decode_bytes(48) + 2 * state_bytes(16) + io_bytes(16, 4)
     toks = n_tok + 48 + 64
-    return dict(ms=t, tokens_per_s=toks / (t * 1e-3), prefill_gflop=flops / 1e9, decode_verify_bytes=hbm)
+    return dict(ms=t, tokens_per_s=toks / (t * 1e-3), prefill_gflop=flops / 1e9, decode_verify_bytes=hbm,
+                streams=2)
 
 
 # ------------------------------------------------------------ CPU baseline
