@@ -273,6 +273,38 @@ def bench_mixed(torch, mx, dev, timer, iters=10):
                 streams=2)
 
 
+def bench_epilogue(torch, mx, dev, timer, iters=50):
+    """The mixer epilogue's gated RMSNorm at the decode (B=64) and prefill
+    (T=4096) row counts: the fused HIP kernel, and for comparison the same
+    formula as separate torch ops (what the epilogue cost before fusion)."""
+    gen = torch.Generator().manual_seed(1005)
+    res = {}
+    for name, rows in (("decode_b64", 64 * Hv), ("prefill_t4096", 4096 * Hv)):
+        x = torch.randn(rows, Dv, generator=gen).to(torch.bfloat16).to(dev)
+        z = torch.randn(rows, Dv, generator=gen).to(torch.bfloat16).to(dev)
+        w = (1 + 0.1 * torch.randn(Dv, generator=gen)).to(torch.bfloat16).to(dev)
+        plan = mx.prepare_gated_rms_norm(x, z, w, 1e-6)
+
+        def fused(i):
+            plan.launch()
+
+        def unfused(i):
+            xf = x.float()
+            n = (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + 1e-6)).to(torch.bfloat16)
+            (w * n * torch.nn.functional.silu(z.float())).to(torch.bfloat16)
+
+        for _ in range(5):
+            fused(0)
+            unfused(0)
+        t = timer.total_ms(fused, iters) / iters
+        t_ref = timer.total_ms(unfused, iters) / iters
+        nbytes = 3 * rows * Dv * 2
+        res[name] = dict(rows=rows, us=round(1e3 * t, 3), bytes=nbytes, gbs=round(nbytes / (t * 1e-3) / 1e9, 1),
+                         hbm_frac=round(nbytes / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                         unfused_torch_us=round(1e3 * t_ref, 3))
+    return res
+
+
 # ------------------------------------------------------------ CPU baseline
 
 def cpu_baseline(torch, budget_s=12.0):
@@ -326,6 +358,7 @@ def main():
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 256 MiB device-to-device copy (counter calibration) and exit")
     ap.add_argument("--prefill-only", action="store_true", help="only the T=4096 prefill workload")
+    ap.add_argument("--epilogue-only", action="store_true", help="only the gated RMSNorm epilogue workloads")
     ap.add_argument("--hbm-ceiling", action="store_true",
                     help="only time in-place streaming updates (read + write) of 128 MiB and 1 GiB fp32 "
                          "with a library elementwise kernel, the practical HBM ceiling the decode kernel is "
@@ -374,6 +407,10 @@ def main():
             del x
         print(json.dumps({"inplace_stream": res, "peak_GB/s": HBM_PEAK_GBS}), flush=True)
         return
+    if args.epilogue_only:
+        print(json.dumps({"epilogue_gated_rmsnorm": bench_epilogue(torch, mx, dev, timer, iters=args.steps)}),
+              flush=True)
+        return
     if args.prefill_only:
         p = bench_prefill(torch, mx, dev, timer, iters=args.steps)
         print(json.dumps({"prefill_t4096": p}), flush=True)
@@ -391,6 +428,7 @@ def main():
         configs["verify_b32_t4"] = bench_verify(torch, mx, dev, timer)
         configs["prefill_t4096"] = bench_prefill(torch, mx, dev, timer)
         configs["mixed"] = bench_mixed(torch, mx, dev, timer)
+        configs["epilogue_gated_rmsnorm"] = bench_epilogue(torch, mx, dev, timer)
     base = None if args.no_cpu else cpu_baseline(torch)
 
     line = {

@@ -180,6 +180,21 @@ int gdn_conv_state_commit(const void* conv_state_in, const void* qkv, int io_dty
                           void* conv_state_out, int64_t B, int64_t T, int64_t C,
                           int64_t Kt, void* stream);
 
+/*
+ * Gated RMSNorm of the mixer epilogue, self_layer.norm(out, z) at
+ * dflash.py:377 (mlx-lm's gated norm; restated by transformers'
+ * Qwen3NextRMSNormGated, models/qwen3_next/modeling_qwen3_next.py:57-74).
+ * Per row of D channels:
+ *   n = x / sqrt(mean(x^2) + eps)       rounded to io_dtype
+ *   m = weight * n                      rounded to io_dtype if w_dtype == io_dtype
+ *   out = m * silu(gate)                (fp32 product, rounded once)
+ *   x, gate, out  [rows, D] io_dtype;  weight [D] w_dtype, or NULL for ones
+ * out may alias x or gate.  Requires D in {64, 128, 256}.
+ */
+int gdn_gated_rmsnorm(const void* x, const void* gate, int io_dtype,
+                      const void* weight, int w_dtype, void* out,
+                      int64_t rows, int64_t D, float eps, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -38,6 +38,7 @@ EXPORTS = (
     "gdn_chunk_fwd",
     "gdn_conv_prologue",
     "gdn_conv_state_commit",
+    "gdn_gated_rmsnorm",
 )
 
 
@@ -115,6 +116,10 @@ _SIGNATURES = {
     "gdn_conv_state_commit": (
         c_int,
         [_P, _P, c_int, _P, _P, _P, _I64, _I64, _I64, _I64, _P],
+    ),
+    "gdn_gated_rmsnorm": (
+        c_int,
+        [_P, _P, c_int, _P, c_int, _P, _I64, _I64, c_float, _P],
     ),
 }
 

@@ -276,6 +276,89 @@ __device__ __forceinline__ float wave_sum(float x) {
   return x;
 }
 
+// ------------------------------------------- 8-element row slices
+
+constexpr int CPL = 8;  // channels per lane
+
+// Raw 8-channel slice of a row as loaded (converted at its use, so the loads
+// of a whole run can be in flight at once).
+template <int DT>
+struct Raw8 {
+  u32x4 v;  // 8 x 16-bit
+};
+template <>
+struct Raw8<GDN_DTYPE_F32> {
+  f32x4 a, b;
+};
+
+template <int DT>
+__device__ __forceinline__ Raw8<DT> load_raw8(const void* base, int64_t i) {
+  Raw8<DT> r;
+  if constexpr (DT == GDN_DTYPE_F32) {
+    r.a = *reinterpret_cast<const f32x4*>(static_cast<const float*>(base) + i);
+    r.b = *reinterpret_cast<const f32x4*>(static_cast<const float*>(base) + i + 4);
+  } else {
+    r.v = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(base) + i);
+  }
+  return r;
+}
+
+template <int DT>
+__device__ __forceinline__ void unpack8(const Raw8<DT>& r, float (&x)[CPL]) {
+  if constexpr (DT == GDN_DTYPE_F32) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      x[k] = r.a[k];
+      x[4 + k] = r.b[k];
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      if constexpr (DT == GDN_DTYPE_BF16) {
+        x[2 * k] = __uint_as_float(r.v[k] << 16);
+        x[2 * k + 1] = __uint_as_float(r.v[k] & 0xffff0000u);
+      } else {
+        x[2 * k] = f16_to_f32(static_cast<uint16_t>(r.v[k] & 0xffffu));
+        x[2 * k + 1] = f16_to_f32(static_cast<uint16_t>(r.v[k] >> 16));
+      }
+    }
+  }
+}
+
+template <int DT>
+__device__ __forceinline__ void store8(void* base, int64_t i, const float (&x)[CPL]) {
+  if constexpr (DT == GDN_DTYPE_F32) {
+    *reinterpret_cast<f32x4*>(static_cast<float*>(base) + i) = f32x4{x[0], x[1], x[2], x[3]};
+    *reinterpret_cast<f32x4*>(static_cast<float*>(base) + i + 4) = f32x4{x[4], x[5], x[6], x[7]};
+  } else {
+    u32x4 v;
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      v[k] = DT == GDN_DTYPE_BF16 ? pk_bf16(x[2 * k], x[2 * k + 1]) : pk_f16(x[2 * k], x[2 * k + 1]);
+    *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(base) + i) = v;
+  }
+}
+
+// Sum over the LPH lanes of a row (aligned lane groups of 8, 16 or 32).
+template <int LPH>
+__device__ __forceinline__ float head_sum(float x) {
+  if constexpr (LPH == 8) {
+    return sum8(x);
+  } else if constexpr (LPH == 16) {
+    return sum16(x);
+  } else {
+    x = sum16(x);
+    return x + __shfl_xor(x, 16, 64);
+  }
+}
+
+// SiLU x * sigmoid(x) = x / (1 + 2^(-x log2 e)) on the hardware exp2 and
+// reciprocal (about 1 ulp each; the result is rounded to the io dtype).  For
+// x -> -inf the denominator overflows to inf and the result is -0.
+__device__ __forceinline__ float silu(float x) {
+  return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(x * -1.4426950408889634f));
+}
+
 }  // namespace gdn
 
 // ----------------------------------------------------- host-side status

@@ -11,7 +11,8 @@ Data path per call:
   in_proj_qkv / z / b / a      library GEMMs (hipBLASLt through torch)
   gdn_conv_prologue            fused conv1d + SiLU + q/k norm (HIP)
   gated_delta_update           recurrent or chunked kernel (HIP)
-  gated RMSNorm + out_proj     torch ops (the epilogue)
+  gated_rms_norm               fused gated RMSNorm (HIP)
+  out_proj                     library GEMM (hipBLASLt through torch)
 
 Speculative rounds: ``mixer(inputs, mask, cache, verify=True)`` computes the
 outputs of all T draft tokens without touching ``cache`` and remembers what
@@ -29,20 +30,13 @@ from dataclasses import dataclass
 from typing import Optional, Sequence
 
 import torch
-import torch.nn.functional as F
 
 from .cache import ArraysCache
 from .conv import conv_state_commit, gdn_conv_prologue
+from .epilogue import gated_rms_norm
 from .gated_delta import IntSeq, gated_delta_commit, gated_delta_update, gated_delta_verify
 
 __all__ = ["GatedDeltaNet", "gated_rms_norm", "commit_verified"]
-
-
-def gated_rms_norm(x: torch.Tensor, gate: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
-    """``rms_norm(x) * weight * silu(gate)`` over the last dim, in float32, cast back to x's dtype."""
-    xf = x.float()
-    xf = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)
-    return (xf * weight.float() * F.silu(gate.float())).to(x.dtype)
 
 
 @dataclass
@@ -107,7 +101,8 @@ class GatedDeltaNet(torch.nn.Module):
 
     def _epilogue(self, y, z):
         B, S = y.shape[:2]
-        out = gated_rms_norm(y, z, self.norm_weight, self.rms_norm_eps)
+        # y is this call's own buffer: normalise it in place
+        out = gated_rms_norm(y, z, self.norm_weight, self.rms_norm_eps, out=y)
         return self.out_proj(out.reshape(B, S, -1))
 
     def forward(self, inputs: torch.Tensor, mask: Optional[torch.Tensor] = None,

@@ -18,6 +18,7 @@ third-party ``mlx-lm`` package that multiplex imports, which is absent here):
 * the mixer prologue: mask zeroing, conv-state concat, depthwise causal
   conv1d (K taps, no bias) + SiLU, q/k RMS-norm with ``1/Dk`` and
   ``1/sqrt(Dk)`` scales, conv-state update (``dflash.py:351-370``).
+* the mixer epilogue's gated RMSNorm ``norm(out, z)`` (``dflash.py:377``).
 * the commit rule of a partially accepted verify: state after the first
   ``n`` tokens, ``conv_state = conv_input[:, n : n + K - 1]``
   (``dflash.py:403-426``; ``engine.py:337-359`` replays the same prefix).
@@ -36,6 +37,9 @@ other than a retyping of its own formula):
 * ``conv_prologue``: torch.nn.functional.conv1d(groups=C) and
   torch.nn.functional.rms_norm.
 * ``commit``: equality with ``recurrent`` run on the accepted prefix alone.
+* ``gated_rms_norm``: transformers' ``Qwen3NextRMSNormGated`` module run on
+  the CPU (library cross-check), closed forms (constant rows, zero gate) and
+  scale invariance.
 
 Rounding points inside mlx-lm's Metal kernel (bf16 vs fp32 gates, reduction
 order) cannot be pinned without importing mlx-lm; the tolerances
@@ -61,6 +65,7 @@ __all__ = [
     "conv_prologue",
     "conv_state_commit",
     "bf16_round",
+    "gated_rms_norm",
     "mixer_forward",
 ]
 
@@ -340,6 +345,26 @@ def conv_state_commit(conv_input, n_commit, Kt):
     return out
 
 
+def gated_rms_norm(x, gate, weight=None, eps=1e-6, round_fn=None, weight_rounds=True):
+    """Gated RMSNorm of the mixer epilogue, ``norm(out, z)`` at ``dflash.py:377``.
+
+    Per row of the last dim: ``n = x / sqrt(mean(x^2) + eps)``,
+    ``m = weight * n``, ``out = m * silu(gate)``.  ``round_fn`` (e.g.
+    ``bf16_round``) rounds where a half-precision model materialises values,
+    at the points of transformers' ``Qwen3NextRMSNormGated``
+    (``models/qwen3_next/modeling_qwen3_next.py:57-74``): after the
+    normalisation, after the weight product when the weight has the io dtype
+    (``weight_rounds``), and at the output.
+    """
+    r = round_fn if round_fn is not None else (lambda t: np.asarray(t, dtype=np.float64))
+    x = _f64(x)
+    n = r(x / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + eps))
+    m = n if weight is None else _f64(weight) * n
+    if weight is not None and weight_rounds:
+        m = r(m)
+    return r(m * _silu(_f64(gate)))
+
+
 def mixer_forward(params, inputs, Hk, Hv, Dk, Dv, conv_state=None, state=None, mask=None,
                   eps=1e-6, round_bf16=True):
     """GatedDeltaNet mixer (``multiplex/kernel/dflash.py:343-381``), float64.
@@ -362,7 +387,6 @@ def mixer_forward(params, inputs, Hk, Hv, Dk, Dv, conv_state=None, state=None, m
     q, k, v = r(q), r(k), r(v)
     y, new_state = gated_delta_update(q, k, v, a, b, params["A_log"], params["dt_bias"], state, mask)
     y = r(y)
-    yn = y / np.sqrt(np.mean(y * y, axis=-1, keepdims=True) + eps) * _f64(params["norm"])
-    yn = r(yn * _silu(z))
+    yn = gated_rms_norm(y, z, params["norm"], eps, round_fn=r if round_bf16 else None)
     out = r(yn.reshape(B, S, -1) @ _f64(params["out_proj"]).T)
     return out, new_cs, new_state

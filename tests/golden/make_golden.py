@@ -11,10 +11,13 @@ therefore computed by implementations independent of ``oracle/gdn.py``:
   internally and compute in float32;
 * the gate transforms: ``torch.nn.functional.softplus`` / ``torch.sigmoid``;
 * the prologue: ``torch.nn.functional.conv1d(groups=C)``, ``silu`` and
-  ``rms_norm`` in float64.
+  ``rms_norm`` in float64;
+* the epilogue's gated RMSNorm: transformers' ``Qwen3NextRMSNormGated``
+  module, run in bfloat16 (bf16 and fp32 weight) and in float32.
 
 Inputs are drawn from ``numpy.random.default_rng`` with fixed seeds.
-Run: ``python tests/golden/make_golden.py`` (needs transformers).
+Run: ``python tests/golden/make_golden.py [case ...]`` (needs transformers;
+no argument writes every case).
 """
 
 from __future__ import annotations
@@ -116,13 +119,47 @@ def prologue_case(name, seed, B, S, Hk, Hv, D, Kt=4, eps=1e-6):
     )
 
 
+def gated_norm_case(name, seed, rows, D, eps=1e-6):
+    from transformers.models.qwen3_next.modeling_qwen3_next import Qwen3NextRMSNormGated
+
+    rng = np.random.default_rng(seed)
+    scale = 10.0 ** rng.uniform(-3, 3, (rows, 1))
+    x = torch.tensor(rng.standard_normal((rows, D)) * scale, dtype=torch.float32).to(torch.bfloat16)
+    gate = torch.tensor(rng.normal(0.0, 2.0, (rows, D)), dtype=torch.float32).to(torch.bfloat16)
+    w = torch.tensor(rng.normal(1.0, 0.25, D), dtype=torch.float32).to(torch.bfloat16)
+    x[0] = 0.75           # a constant row
+    gate[1] = 0.0         # a zero gate
+    outs = {}
+    with torch.no_grad():
+        m = Qwen3NextRMSNormGated(D, eps=eps).to(torch.bfloat16)
+        m.weight.copy_(w)
+        outs["out_bf16_wbf16"] = m(x, gate)
+        m = Qwen3NextRMSNormGated(D, eps=eps).to(torch.float32)
+        m.weight.copy_(w.float())
+        outs["out_bf16_wf32"] = m(x, gate)
+        outs["out_f32"] = m(x.float(), gate.float())
+    np.savez_compressed(
+        HERE / f"{name}.npz",
+        x=x.float().numpy(), gate=gate.float().numpy(), weight=w.float().numpy(), eps=np.array(eps),
+        **{k: v.float().numpy() for k, v in outs.items()},
+    )
+
+
+CASES = {
+    "recurrent_small": lambda: recurrent_case("recurrent_small", 11, B=2, T=6, Hk=2, Hv=4, Dk=16, Dv=8),
+    "recurrent_hd128": lambda: recurrent_case("recurrent_hd128", 12, B=1, T=3, Hk=2, Hv=4, Dk=128, Dv=128),
+    "chunked_t100": lambda: chunked_case("chunked_t100", 13, B=1, T=100, Hk=1, Hv=2, Dk=32, Dv=16, chunk=64),
+    "prologue_small": lambda: prologue_case("prologue_small", 14, B=2, S=7, Hk=2, Hv=4, D=16),
+    "gated_norm_small": lambda: gated_norm_case("gated_norm_small", 15, rows=48, D=128),
+}
+
+
 def main():
-    torch.set_default_dtype(torch.float64)
-    recurrent_case("recurrent_small", 11, B=2, T=6, Hk=2, Hv=4, Dk=16, Dv=8)
-    recurrent_case("recurrent_hd128", 12, B=1, T=3, Hk=2, Hv=4, Dk=128, Dv=128)
-    chunked_case("chunked_t100", 13, B=1, T=100, Hk=1, Hv=2, Dk=32, Dv=16, chunk=64)
-    prologue_case("prologue_small", 14, B=2, S=7, Hk=2, Hv=4, D=16)
-    print("wrote", sorted(p.name for p in HERE.glob("*.npz")), file=sys.stderr)
+    names = sys.argv[1:] or list(CASES)
+    for n in names:
+        torch.set_default_dtype(torch.float64)
+        CASES[n]()
+    print("wrote", names, file=sys.stderr)
 
 
 if __name__ == "__main__":

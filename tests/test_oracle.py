@@ -140,6 +140,43 @@ def test_bf16_round_matches_torch():
     np.testing.assert_array_equal(gdn.bf16_round(x), ref)
 
 
+def test_gated_norm_matches_library_fixture():
+    d = load("gated_norm_small")
+    eps = float(d["eps"])
+    cases = [(gdn.bf16_round, True, "out_bf16_wbf16"), (gdn.bf16_round, False, "out_bf16_wf32"),
+             (None, False, "out_f32")]
+    for rnd, w_rounds, key in cases:
+        got = gdn.gated_rms_norm(d["x"], d["gate"], d["weight"], eps, round_fn=rnd, weight_rounds=w_rounds)
+        exp = d[key]
+        if rnd is None:
+            assert rel_err(got, exp) < 1e-6, key
+        else:
+            # float64 vs the module's float32 arithmetic: the same bf16 value
+            # except where an intermediate lies next to a rounding boundary
+            same = np.mean(got == exp)
+            assert same > 0.999 and rel_err(got, exp) < 2e-3, (key, same)
+    # a plausible mistake: the weight product left unrounded for a bf16 weight
+    wrong = gdn.gated_rms_norm(d["x"], d["gate"], d["weight"], eps, round_fn=gdn.bf16_round, weight_rounds=False)
+    assert np.mean(wrong == d["out_bf16_wbf16"]) < 0.95
+
+
+def test_gated_norm_closed_forms():
+    D = 64
+    x = np.full((3, D), -2.5)
+    gate = np.stack([np.zeros(D), np.full(D, 40.0), np.linspace(-3, 3, D)])
+    w = np.linspace(0.5, 1.5, D)
+    out = gdn.gated_rms_norm(x, gate, w, eps=0.0)
+    np.testing.assert_allclose(out[0], 0.0, atol=0)                  # silu(0) = 0
+    np.testing.assert_allclose(out[1], -w * 40.0, rtol=1e-15)        # rms of a constant row is |c|
+    np.testing.assert_allclose(out[2], -w * gate[2] / (1 + np.exp(-gate[2])), rtol=1e-14)
+    rng = np.random.default_rng(5)
+    xr, gr = rng.standard_normal((4, D)), rng.standard_normal((4, D))
+    np.testing.assert_allclose(gdn.gated_rms_norm(1e3 * xr, gr, w, eps=0.0), gdn.gated_rms_norm(xr, gr, w, eps=0.0),
+                               rtol=1e-13)
+    np.testing.assert_allclose(gdn.gated_rms_norm(xr, gr, None, eps=0.0), gdn.gated_rms_norm(xr, gr, np.ones(D), eps=0.0),
+                               rtol=0)
+
+
 # -------------------------------------------------------------- invariants
 
 def test_split_T_carries_state():
