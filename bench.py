@@ -305,6 +305,50 @@ def bench_epilogue(torch, mx, dev, timer, iters=50):
     return res
 
 
+def bench_pool(torch, mx, dev, timer, iters=20):
+    """Pooled states: a batch-membership change (64 rows -> keep 48 -> add 16
+    fresh rows) done densely (index_select + cat of the fp32 states, as the
+    engine's filter / merge do) and through a StatePool (slot lists only);
+    and B=64 decode steps reading and writing pool slots."""
+    gen = torch.Generator().manual_seed(1006)
+    B = 64
+    keep = sorted(torch.randperm(B, generator=gen)[:48].tolist())
+    dense = (torch.randn(B, Hv, Dv, Dk, generator=gen) * 0.02).to(dev)
+    keep_t = torch.tensor(keep, device=dev)
+
+    def dense_change(i):
+        s = dense.index_select(0, keep_t)
+        torch.cat([s, torch.zeros(16, Hv, Dv, Dk, device=dev)])
+
+    pool = mx.StatePool(2 * B, Hv, Dv, Dk, device=dev)
+
+    def pooled_change(i):
+        batch = mx.PooledBatch(pool, pool.alloc(B, zero=False))
+        batch.filter(keep)
+        batch = mx.PooledBatch.merge([batch, mx.PooledBatch.new(pool, 16)])
+        batch.index  # the int32 slot table the next launch reads
+        batch.release()
+
+    for _ in range(3):
+        dense_change(0)
+        pooled_change(0)
+    t_dense = timer.total_ms(dense_change, iters) / iters
+    t_pool = timer.total_ms(pooled_change, iters) / iters
+
+    d = draw(gen, B, 1, torch, dev, state=False)
+    slots = pool.alloc(B, zero=False)
+    pool.states.copy_((torch.randn(pool.states.shape, generator=gen) * 0.02).to(dev))
+    plan = mx.prepare_recurrent(d["q"], d["k"], d["v"], d["a"], d["b"], d["A_log"], d["dt_bias"], pool.states,
+                                state_index=pool.index(slots), state_out=pool.states)
+    for _ in range(10):
+        plan.launch()
+    t_dec = timer.total_ms(lambda i: plan.launch(), 100) / 100
+    return dict(change_dense_us=round(1e3 * t_dense, 2), change_pooled_us=round(1e3 * t_pool, 2),
+                dense_bytes_moved=(48 + 48 + 64) * state_bytes(1),
+                decode_b64_pooled_ms=round(t_dec, 5),
+                decode_b64_pooled_gbs=round(decode_bytes(B) / (t_dec * 1e-3) / 1e9, 1))
+
+
 # ------------------------------------------------------------ CPU baseline
 
 def cpu_baseline(torch, budget_s=12.0):
@@ -359,6 +403,7 @@ def main():
                     help="only run a plain 256 MiB device-to-device copy (counter calibration) and exit")
     ap.add_argument("--prefill-only", action="store_true", help="only the T=4096 prefill workload")
     ap.add_argument("--epilogue-only", action="store_true", help="only the gated RMSNorm epilogue workloads")
+    ap.add_argument("--pool-only", action="store_true", help="only the pooled-state workloads")
     ap.add_argument("--hbm-ceiling", action="store_true",
                     help="only time in-place streaming updates (read + write) of 128 MiB and 1 GiB fp32 "
                          "with a library elementwise kernel, the practical HBM ceiling the decode kernel is "
@@ -407,6 +452,9 @@ def main():
             del x
         print(json.dumps({"inplace_stream": res, "peak_GB/s": HBM_PEAK_GBS}), flush=True)
         return
+    if args.pool_only:
+        print(json.dumps({"state_pool": bench_pool(torch, mx, dev, timer)}), flush=True)
+        return
     if args.epilogue_only:
         print(json.dumps({"epilogue_gated_rmsnorm": bench_epilogue(torch, mx, dev, timer, iters=args.steps)}),
               flush=True)
@@ -429,6 +477,7 @@ def main():
         configs["prefill_t4096"] = bench_prefill(torch, mx, dev, timer)
         configs["mixed"] = bench_mixed(torch, mx, dev, timer)
         configs["epilogue_gated_rmsnorm"] = bench_epilogue(torch, mx, dev, timer)
+        configs["state_pool"] = bench_pool(torch, mx, dev, timer)
     base = None if args.no_cpu else cpu_baseline(torch)
 
     line = {

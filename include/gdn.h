@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define GDN_ABI_VERSION 1
+#define GDN_ABI_VERSION 2
 
 /* dtype codes for the void* operands */
 #define GDN_DTYPE_F32 0
@@ -98,6 +98,16 @@ int gdn_gated_delta_kernel(const void* q, const void* k, const void* v, int qkv_
  *   commit_len [B] int32: row b writes the state after its first
  *              commit_len[b] tokens (0 = initial state, < 0 = no write,
  *              > length = clamped); NULL = after all tokens.
+ *   state_index [B] int32 or NULL: pooled states.  state_in and state_out
+ *              are then pools of n_slots states [n_slots,Hv,Dv,Dk], and row
+ *              b reads and writes slot state_index[b] (state_in NULL = a
+ *              zero initial state; state_out == state_in updates the pool
+ *              in place).  Batch membership changes (join, leave, filter,
+ *              merge of the scheduler, engine.py:383-432) then move int32
+ *              indices, not 2 MiB states.  A row whose index is outside
+ *              [0, n_slots) is not processed: its y and its slot are left
+ *              as they are.  Rows that write state must use distinct slots.
+ *              No counterpart in the reference, which concatenates states.
  * Rows run independently; a launch never reads another row's state.
  */
 typedef struct gdn_recurrent_args {
@@ -119,8 +129,10 @@ typedef struct gdn_recurrent_args {
   const uint8_t* mask;
   const int32_t* cu_seqlens; /* [B+1] or NULL */
   const int32_t* commit_len; /* [B] or NULL */
+  const int32_t* state_index; /* [B] or NULL: slots of pooled states */
   int64_t B, T;              /* T = tokens per row, or N_tok when packed */
   int64_t Hk, Hv, Dk, Dv;
+  int64_t n_slots;           /* pool size when state_index != NULL */
   void* stream;
 } gdn_recurrent_args;
 
@@ -133,7 +145,10 @@ int gdn_recurrent(const gdn_recurrent_args* args);
  * scheduler.py:331-333 -> engine.py:261-269).  q/k/v must be bf16.
  * cu_seqlens [n_seqs+1] (NULL: n_seqs rows of n_tok/n_seqs tokens each,
  * [B,T,...] layout).  state_in [n_seqs,Hv,Dv,Dk] fp32 or NULL (zeros),
- * state_out may alias state_in.  No mask.  chunk must be 64.
+ * state_out may alias state_in.  state_index [n_seqs] int32 or NULL:
+ * pooled states as in gdn_recurrent_args (state_in / state_out are pools of
+ * n_slots states; sequence n uses slot state_index[n]; out-of-range slots
+ * are skipped).  No mask.  chunk must be 64.
  * workspace must hold gdn_chunk_workspace_bytes(...) bytes (256-B aligned).
  */
 size_t gdn_chunk_workspace_bytes(int64_t n_seqs, int64_t n_tok, int64_t Hv,
@@ -143,6 +158,7 @@ int gdn_chunk_fwd(const void* q, const void* k, const void* v, int qkv_dtype,
                   int gate_mode, const void* gx, const void* gy, int gate_dtype,
                   const void* A_log, const void* dt_bias, int param_dtype,
                   const float* state_in, void* y, float* state_out,
+                  const int32_t* state_index, int64_t n_slots,
                   const int32_t* cu_seqlens, int64_t n_seqs, int64_t n_tok,
                   int64_t Hk, int64_t Hv, int64_t Dk, int64_t Dv, int64_t chunk,
                   void* workspace, size_t workspace_bytes, void* stream);

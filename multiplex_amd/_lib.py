@@ -13,7 +13,7 @@ from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libgdn.so"
 
-GDN_ABI_VERSION = 1
+GDN_ABI_VERSION = 2
 
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
@@ -64,12 +64,14 @@ class RecurrentArgs(Structure):
         ("mask", c_void_p),
         ("cu_seqlens", c_void_p),
         ("commit_len", c_void_p),
+        ("state_index", c_void_p),
         ("B", c_int64),
         ("T", c_int64),
         ("Hk", c_int64),
         ("Hv", c_int64),
         ("Dk", c_int64),
         ("Dv", c_int64),
+        ("n_slots", c_int64),
         ("stream", c_void_p),
     ]
 
@@ -105,7 +107,7 @@ _SIGNATURES = {
     "gdn_chunk_workspace_bytes": (c_size_t, [_I64, _I64, _I64, _I64, _I64, _I64]),
     "gdn_chunk_fwd": (
         c_int,
-        [_P, _P, _P, c_int, c_int, _P, _P, c_int, _P, _P, c_int, _P, _P, _P, _P,
+        [_P, _P, _P, c_int, c_int, _P, _P, c_int, _P, _P, c_int, _P, _P, _P, _P, _I64, _P,
          _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P, c_size_t, _P],
     ),
     "gdn_conv_prologue": (

@@ -77,6 +77,8 @@ struct ChunkParams {
   const float* state_in;
   uint16_t* y;
   float* state_out;
+  const int32_t* state_index;  // slot of each sequence in pooled states, or null
+  int n_slots;
   const int32_t* cu;  // [n_seqs + 1] or null
   int n_seqs;
   int T;              // tokens per sequence when cu == null
@@ -515,6 +517,11 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(const ChunkParams p) {
   const int head_rank = (r8 / kTiles) * kXcds + xcd;
   if (head_rank >= p.n_seqs * p.Hv) return;
   const int seq = seq_by_rank(p, head_rank / p.Hv);
+  int slot = seq;
+  if (p.state_index != nullptr) {
+    slot = p.state_index[seq];
+    if (slot < 0 || slot >= p.n_slots) return;  // uniform, before any barrier
+  }
   const int hv = head_rank % p.Hv;
   const int dv0 = tile * DVT;
   const int hk = hv / p.group;
@@ -606,7 +613,7 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(const ChunkParams p) {
   // This wave's 32 x 16 slice of S^T: state columns [32w, 32w+32) as two
   // 16x16 accumulator tiles; lane holds S^T[32w + 16j + 4lq + i][lr], i.e.
   // 4 consecutive columns of state row dv0 + lr.
-  const int64_t srow = (static_cast<int64_t>(seq) * p.Hv + hv) * DV + dv0 + lr;
+  const int64_t srow = (static_cast<int64_t>(slot) * p.Hv + hv) * DV + dv0 + lr;
   f32x4 sacc[2];
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
@@ -741,6 +748,7 @@ extern "C" int gdn_chunk_fwd(const void* q, const void* k, const void* v, int qk
                              int gate_mode, const void* gx, const void* gy, int gate_dtype,
                              const void* A_log, const void* dt_bias, int param_dtype,
                              const float* state_in, void* y, float* state_out,
+                             const int32_t* state_index, int64_t n_slots,
                              const int32_t* cu_seqlens, int64_t n_seqs, int64_t n_tok, int64_t Hk,
                              int64_t Hv, int64_t Dk, int64_t Dv, int64_t chunk, void* workspace,
                              size_t workspace_bytes, void* stream) {
@@ -764,6 +772,8 @@ extern "C" int gdn_chunk_fwd(const void* q, const void* k, const void* v, int qk
   if (n_tok > 0 && (!q || !k || !v || !gx || !gy || !y))
     return fail(GDN_ERR_INVALID, "gdn_chunk_fwd: q, k, v, gates and y are required");
   if (!state_out) return fail(GDN_ERR_INVALID, "gdn_chunk_fwd: state_out is required");
+  if (state_index != nullptr && (n_slots < 0 || n_slots > INT32_MAX))
+    return fail(GDN_ERR_INVALID, "gdn_chunk_fwd: n_slots=%lld out of range", (long long)n_slots);
   if (n_seqs == 0) return GDN_OK;
   const size_t need = gdn_chunk_workspace_bytes(n_seqs, n_tok, Hv, Dk, Dv, chunk);
   if (workspace == nullptr || workspace_bytes < need)
@@ -790,6 +800,8 @@ extern "C" int gdn_chunk_fwd(const void* q, const void* k, const void* v, int qk
   p.state_in = state_in;
   p.y = static_cast<uint16_t*>(y);
   p.state_out = state_out;
+  p.state_index = state_index;
+  p.n_slots = state_index != nullptr ? static_cast<int>(n_slots) : 0;
   p.cu = cu_seqlens;
   p.n_seqs = static_cast<int>(n_seqs);
   p.T = packed ? 0 : static_cast<int>(n_tok / n_seqs);

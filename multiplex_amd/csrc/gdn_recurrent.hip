@@ -42,6 +42,8 @@ struct RecParams {
   const uint8_t* mask;
   const int32_t* cu_seqlens;
   const int32_t* commit_len;
+  const int32_t* state_index;  // slot of each row in pooled states, or NULL
+  int n_slots;
   int T, Hk, Hv, Dv, group;  // group = Hv / Hk
 };
 
@@ -95,6 +97,7 @@ __device__ __forceinline__ void load_token(const RecParams& p, int64_t tok, int 
 struct RowCtx {
   int sub, dv, dv_c, hv, hk, row, L, commit, steps;
   bool row_ok, write_state, want_y;
+  bool skip;  // pooled row with a slot outside the pool: not processed
   int64_t tok0, srow, srow_c;
 };
 
@@ -125,8 +128,14 @@ __device__ __forceinline__ RowCtx row_ctx(const RecParams& p) {
   c.want_y = p.y != nullptr;
   const bool need_all = c.want_y || (p.snapshots != nullptr);
   c.steps = need_all ? c.L : (c.write_state ? c.commit : 0);
-  c.srow = ((static_cast<int64_t>(c.row) * p.Hv + c.hv) * p.Dv + c.dv) * DK;
-  c.srow_c = ((static_cast<int64_t>(c.row) * p.Hv + c.hv) * p.Dv + c.dv_c) * DK;
+  int slot = c.row;
+  c.skip = false;
+  if (p.state_index != nullptr) {
+    slot = p.state_index[c.row];
+    c.skip = slot < 0 || slot >= p.n_slots;
+  }
+  c.srow = ((static_cast<int64_t>(slot) * p.Hv + c.hv) * p.Dv + c.dv) * DK;
+  c.srow_c = ((static_cast<int64_t>(slot) * p.Hv + c.hv) * p.Dv + c.dv_c) * DK;
   return c;
 }
 
@@ -168,6 +177,7 @@ __global__ __launch_bounds__(256) void recurrent_kernel(const RecParams p) {
   constexpr int EPL = DK / kLanesPerRow;  // fp32 state elements per lane
   constexpr int NV = EPL / 4;             // float4 per lane
   const RowCtx c = row_ctx<DK>(p);
+  if (c.skip) return;  // uniform: a workgroup serves one row
 
   TokenIn<EPL> cur;
   if (c.steps > 0) load_token<DK, DT, GF, false>(p, c.tok0, c.hv, c.hk, c.dv_c, c.sub, cur);
@@ -225,6 +235,7 @@ __global__ __launch_bounds__(kTileThreads) void recurrent_tile_kernel(const RecP
   constexpr int VV = kTile * kTileRows / kTileThreads;  // v values per thread
   static_assert(KV4 >= 1 && VV >= 1, "tile must cover the workgroup");
   const RowCtx c = row_ctx<DK>(p);
+  if (c.skip) return;  // uniform: a workgroup serves one row, before any barrier
   const int tid = threadIdx.x;
   const int dv0 = blockIdx.x * kTileRows;
 
@@ -402,6 +413,8 @@ int run_recurrent(const gdn_recurrent_args* a) {
       !gdn_host::aligned(a->state_in, 16) || !gdn_host::aligned(a->state_out, 16) ||
       !gdn_host::aligned(a->snapshots, 16))
     return fail(GDN_ERR_INVALID, "gdn_recurrent: q/k or state pointers are misaligned");
+  if (a->state_index != nullptr && (a->n_slots < 0 || a->n_slots > INT32_MAX))
+    return fail(GDN_ERR_INVALID, "gdn_recurrent: n_slots=%lld out of range", (long long)a->n_slots);
   if (a->B == 0) return GDN_OK;
   if (a->T > INT32_MAX) return fail(GDN_ERR_UNSUPPORTED, "gdn_recurrent: T too large");
 
@@ -423,6 +436,8 @@ int run_recurrent(const gdn_recurrent_args* a) {
   p.mask = a->mask;
   p.cu_seqlens = a->cu_seqlens;
   p.commit_len = a->commit_len;
+  p.state_index = a->state_index;
+  p.n_slots = a->state_index != nullptr ? static_cast<int>(a->n_slots) : 0;
   p.T = static_cast<int>(a->T);
   p.Hk = static_cast<int>(a->Hk);
   p.Hv = static_cast<int>(a->Hv);

@@ -122,6 +122,33 @@ def _out_state(state_out, shape, dev, what="state_out"):
     return state_out
 
 
+def _state_operands(state, state_out, write_state, n_rows, Hv, Dv, Dk, dev, state_index):
+    """``(state_in, state_out, index, n_slots)`` of a launch.
+
+    Dense: ``[rows, Hv, Dv, Dk]`` states, one per row.  Pooled (``state_index``
+    given): ``state`` / ``state_out`` are pools ``[n_slots, Hv, Dv, Dk]`` and
+    row b uses slot ``state_index[b]``; the new states go to ``state_out``, or
+    into the pool itself when it is None.
+    """
+    if state_index is None:
+        st_shape = (n_rows, Hv, Dv, Dk)
+        state = _check_state(state, st_shape)
+        out_state = _out_state(state_out, st_shape, dev) if write_state else None
+        return state, out_state, None, 0
+    pool = state if state is not None else state_out
+    if pool is None:
+        raise ValueError("pooled states (state_index) need the pool as state or state_out")
+    st_shape = (pool.shape[0], Hv, Dv, Dk)
+    if state is not None and not state.is_contiguous():
+        raise ValueError("the state pool must be contiguous")
+    state = _check_state(state, st_shape, "state pool")
+    out_state = None
+    if write_state:
+        out_state = _out_state(state_out if state_out is not None else state, st_shape, dev, "state_out pool")
+    idx = _int_rows(state_index, n_rows, dev, "state_index")
+    return state, out_state, idx, st_shape[0]
+
+
 def _cu_seqlens(cu: Optional[IntSeq], n_tok: int, dev) -> Optional[torch.Tensor]:
     """Validates packed-sequence offsets on the host and returns them on ``dev``.
 
@@ -245,7 +272,7 @@ def gated_delta_ops(q, k, v, g, beta, state=None, mask=None):
 
 def _recurrent(q, k, v, gx, gy, gate_mode, A_log, dt_bias, state, mask, *,
                y=True, state_out=None, write_state=True, snapshots=False,
-               cu_seqlens=None, commit_len=None):
+               cu_seqlens=None, commit_len=None, state_index=None):
     names = ["q", "k", "v", "a/g", "b/beta", "A_log", "dt_bias", "state", "mask", "state_out"]
     dev = _require_device([q, k, v, gx, gy, A_log, dt_bias, state, mask, state_out], names)
     packed = cu_seqlens is not None
@@ -262,10 +289,9 @@ def _recurrent(q, k, v, gx, gy, gate_mode, A_log, dt_bias, state, mask, *,
         param_code = _lib.DTYPE_F32
     cu = _cu_seqlens(cu_seqlens, sh.T, dev)
     n_rows = (cu.numel() - 1) if packed else sh.B
-    st_shape = (n_rows, sh.Hv, sh.Dv, sh.Dk)
-    state = _check_state(state, st_shape)
+    state, out_state, idx, n_slots = _state_operands(state, state_out, write_state, n_rows, sh.Hv, sh.Dv, sh.Dk,
+                                                     dev, state_index)
     mask_u8 = _mask_u8(mask, (sh.B, sh.T))
-    out_state = _out_state(state_out, st_shape, dev) if write_state else None
     y_t = torch.empty(sh.B, sh.T, sh.Hv, sh.Dv, dtype=k.dtype, device=dev) if y else None
     snaps = (torch.empty(sh.B, sh.T, sh.Hv, sh.Dv, sh.Dk, dtype=torch.float32, device=dev)
              if snapshots else None)
@@ -275,8 +301,8 @@ def _recurrent(q, k, v, gx, gy, gate_mode, A_log, dt_bias, state, mask, *,
         gx=_ptr(gx), gy=_ptr(gy), gate_dtype=gate_code, param_dtype=param_code,
         A_log=_ptr(A_log), dt_bias=_ptr(dt_bias), state_in=_ptr(state),
         state_out=_ptr(out_state), snapshots=_ptr(snaps), y=_ptr(y_t), mask=_ptr(mask_u8),
-        cu_seqlens=_ptr(cu), commit_len=_ptr(commit), B=n_rows, T=sh.T, Hk=sh.Hk, Hv=sh.Hv,
-        Dk=sh.Dk, Dv=sh.Dv, stream=_stream(dev),
+        cu_seqlens=_ptr(cu), commit_len=_ptr(commit), state_index=_ptr(idx), B=n_rows, T=sh.T, Hk=sh.Hk,
+        Hv=sh.Hv, Dk=sh.Dk, Dv=sh.Dv, n_slots=n_slots, stream=_stream(dev),
     )
     with torch.cuda.device(dev):
         _lib.call("gdn_recurrent", _lib.ctypes.byref(args))
@@ -310,7 +336,7 @@ class PreparedRecurrent:
 
 def prepare_recurrent(q, k, v, a, b, A_log, dt_bias, state, mask=None, *, y=True, state_out=None,
                       write_state=True, snapshots=False, commit_len=None, cu_seqlens=None,
-                      gates_precomputed=False) -> PreparedRecurrent:
+                      gates_precomputed=False, state_index=None) -> PreparedRecurrent:
     """Validates once and returns a :class:`PreparedRecurrent` (same arguments as the entry points)."""
     mode = _lib.GATES_PRE if gates_precomputed else _lib.GATES_RAW
     names = ["q", "k", "v", "a/g", "b/beta", "A_log", "dt_bias", "state", "mask", "state_out"]
@@ -325,12 +351,11 @@ def prepare_recurrent(q, k, v, a, b, A_log, dt_bias, state, mask=None, *, y=True
     param_code = _param_codes(A_log, dt_bias, sh.Hv) if mode == _lib.GATES_RAW else _lib.DTYPE_F32
     cu = _cu_seqlens(cu_seqlens, sh.T, dev)
     n_rows = (cu.numel() - 1) if packed else sh.B
-    st_shape = (n_rows, sh.Hv, sh.Dv, sh.Dk)
     if state is not None and (not state.is_contiguous()):
         raise ValueError("state must be contiguous for a prepared launch")
-    state = _check_state(state, st_shape)
+    state, out_state, idx, n_slots = _state_operands(state, state_out, write_state, n_rows, sh.Hv, sh.Dv, sh.Dk,
+                                                     dev, state_index)
     mask_u8 = _mask_u8(mask, (sh.B, sh.T))
-    out_state = _out_state(state_out, st_shape, dev) if write_state else None
     y_t = torch.empty(sh.B, sh.T, sh.Hv, sh.Dv, dtype=k.dtype, device=dev) if y else None
     snaps = (torch.empty(sh.B, sh.T, sh.Hv, sh.Dv, sh.Dk, dtype=torch.float32, device=dev)
              if snapshots else None)
@@ -341,11 +366,11 @@ def prepare_recurrent(q, k, v, a, b, A_log, dt_bias, state, mask=None, *, y=True
         A_log=_ptr(A_log) if mode == _lib.GATES_RAW else None,
         dt_bias=_ptr(dt_bias) if mode == _lib.GATES_RAW else None, state_in=_ptr(state),
         state_out=_ptr(out_state), snapshots=_ptr(snaps), y=_ptr(y_t), mask=_ptr(mask_u8),
-        cu_seqlens=_ptr(cu), commit_len=_ptr(commit), B=n_rows, T=sh.T, Hk=sh.Hk, Hv=sh.Hv,
-        Dk=sh.Dk, Dv=sh.Dv, stream=_stream(dev),
+        cu_seqlens=_ptr(cu), commit_len=_ptr(commit), state_index=_ptr(idx), B=n_rows, T=sh.T, Hk=sh.Hk,
+        Hv=sh.Hv, Dk=sh.Dk, Dv=sh.Dv, n_slots=n_slots, stream=_stream(dev),
     )
     keep = dict(q=q, k=k, v=v, a=a, b=b, A_log=A_log, dt_bias=dt_bias, state=state, mask=mask_u8,
-                cu=cu, commit=commit, y=y_t, state_out=out_state, snapshots=snaps)
+                cu=cu, commit=commit, y=y_t, state_out=out_state, snapshots=snaps, state_index=idx)
     return PreparedRecurrent(args, keep, dev)
 
 
@@ -377,7 +402,7 @@ class PreparedCall:
 
 
 def _chunk_args(q, k, v, gx, gy, gate_mode, A_log, dt_bias, state, *, cu_seqlens=None,
-                state_out=None, workspace=None):
+                state_out=None, workspace=None, state_index=None):
     names = ["q", "k", "v", "a/g", "b/beta", "A_log", "dt_bias", "state", "state_out"]
     dev = _require_device([q, k, v, gx, gy, A_log, dt_bias, state, state_out], names)
     packed = cu_seqlens is not None
@@ -393,33 +418,32 @@ def _chunk_args(q, k, v, gx, gy, gate_mode, A_log, dt_bias, state, *, cu_seqlens
     cu = _cu_seqlens(cu_seqlens, sh.T, dev)
     n_seqs = (cu.numel() - 1) if packed else sh.B
     n_tok = sh.B * sh.T
-    st_shape = (n_seqs, sh.Hv, sh.Dv, sh.Dk)
-    state = _check_state(state, st_shape)
-    out_state = _out_state(state_out, st_shape, dev)
+    state, out_state, idx, n_slots = _state_operands(state, state_out, True, n_seqs, sh.Hv, sh.Dv, sh.Dk, dev,
+                                                     state_index)
     y_t = torch.empty(sh.B, sh.T, sh.Hv, sh.Dv, dtype=k.dtype, device=dev)
     ws_bytes = chunk_workspace_bytes(n_seqs, n_tok, sh.Hv, sh.Dk, sh.Dv, CHUNK)
     if workspace is None or workspace.numel() * workspace.element_size() < ws_bytes:
         workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
     args = (_ptr(q), _ptr(k), _ptr(v), qkv_code, gate_mode, _ptr(gx), _ptr(gy), gate_code, _ptr(A_log),
-            _ptr(dt_bias), param_code, _ptr(state), _ptr(y_t), _ptr(out_state), _ptr(cu), n_seqs, n_tok,
-            sh.Hk, sh.Hv, sh.Dk, sh.Dv, CHUNK, _ptr(workspace), ws_bytes, _stream(dev))
+            _ptr(dt_bias), param_code, _ptr(state), _ptr(y_t), _ptr(out_state), _ptr(idx), n_slots, _ptr(cu),
+            n_seqs, n_tok, sh.Hk, sh.Hv, sh.Dk, sh.Dv, CHUNK, _ptr(workspace), ws_bytes, _stream(dev))
     keep = dict(q=q, k=k, v=v, gx=gx, gy=gy, A_log=A_log, dt_bias=dt_bias, state=state, cu=cu,
-                workspace=workspace)
+                workspace=workspace, state_index=idx)
     return args, keep, y_t, out_state, dev
 
 
 def _chunked(q, k, v, gx, gy, gate_mode, A_log, dt_bias, state, *, cu_seqlens=None,
-             state_out=None, workspace=None):
+             state_out=None, workspace=None, state_index=None):
     args, _keep, y_t, out_state, dev = _chunk_args(q, k, v, gx, gy, gate_mode, A_log, dt_bias, state,
                                                    cu_seqlens=cu_seqlens, state_out=state_out,
-                                                   workspace=workspace)
+                                                   workspace=workspace, state_index=state_index)
     with torch.cuda.device(dev):
         _lib.call("gdn_chunk_fwd", *args)
     return y_t, out_state
 
 
 def prepare_chunked(q, k, v, a, b, A_log, dt_bias, state=None, *, cu_seqlens=None, state_out=None,
-                    workspace=None, gates_precomputed=False) -> PreparedCall:
+                    workspace=None, gates_precomputed=False, state_index=None) -> PreparedCall:
     """Validates a chunked prefill once; ``launch()`` re-issues it.
 
     Same arguments as :func:`gated_delta_update` with ``chunked=True``;
@@ -429,7 +453,7 @@ def prepare_chunked(q, k, v, a, b, A_log, dt_bias, state=None, *, cu_seqlens=Non
     mode = _lib.GATES_PRE if gates_precomputed else _lib.GATES_RAW
     args, keep, y_t, out_state, dev = _chunk_args(q, k, v, a, b, mode, A_log, dt_bias, state,
                                                   cu_seqlens=cu_seqlens, state_out=state_out,
-                                                  workspace=workspace)
+                                                  workspace=workspace, state_index=state_index)
     for name in ("q", "k", "v", "gx", "gy"):
         if keep[name].data_ptr() != {"q": q, "k": k, "v": v, "gx": a, "gy": b}[name].data_ptr():
             raise ValueError(f"{name} must be contiguous for a prepared launch")
@@ -447,19 +471,20 @@ def _use_chunked(chunked, k, mask, cu_seqlens, T):
 
 # ------------------------------------------------------------ entry points
 
-def gated_delta_kernel(q, k, v, g, beta, state, mask=None, *, state_out=None):
+def gated_delta_kernel(q, k, v, g, beta, state, mask=None, *, state_out=None, state_index=None):
     """mlx-lm ``gated_delta_kernel``: the fused recurrence with g and beta given.
 
-    Returns ``(y, new_state)``.
+    Returns ``(y, new_state)``.  ``state_index``: pooled states, as in
+    :func:`gated_delta_update`.
     """
     y, s, _ = _recurrent(q, k, v, g, beta, _lib.GATES_PRE, None, None, state, mask,
-                         state_out=state_out)
+                         state_out=state_out, state_index=state_index)
     return y, s
 
 
 def gated_delta_update(q, k, v, a, b, A_log, dt_bias, state=None, mask=None, use_kernel=True, *,
                        cu_seqlens: Optional[IntSeq] = None, state_out=None,
-                       chunked: Optional[bool] = None, workspace=None):
+                       chunked: Optional[bool] = None, workspace=None, state_index=None):
     """mlx-lm ``gated_delta_update`` on MI355X.
 
     Args (as mlx-lm): q, k ``[B,T,Hk,Dk]``; v ``[B,T,Hv,Dv]``; a, b ``[B,T,Hv]``;
@@ -472,12 +497,16 @@ def gated_delta_update(q, k, v, a, b, A_log, dt_bias, state=None, mask=None, use
     ``state_out`` receives the new state (may be ``state``); ``chunked``
     forces the chunked MFMA prefill kernel on/off (default: long unmasked
     bf16 rows with Dk = 128); ``workspace`` is a reusable uint8 buffer for it.
+    ``state_index`` (int32 ``[rows]``) switches to pooled states: ``state``
+    (and ``state_out``) are then pools ``[n_slots, Hv, Dv, Dk]``, row b reads
+    and writes slot ``state_index[b]``, and without ``state_out`` the pool is
+    updated in place (see :class:`multiplex_amd.StatePool`).
 
     Returns ``(y [B,T,Hv,Dv] in q's dtype, new_state [rows,Hv,Dv,Dk] float32)``.
     """
     if not use_kernel:
-        if cu_seqlens is not None:
-            raise ValueError("the ops path does not take cu_seqlens")
+        if cu_seqlens is not None or state_index is not None:
+            raise ValueError("the ops path does not take cu_seqlens or state_index")
         y, s = gated_delta_ops(q, k, v, compute_g(A_log, a, dt_bias), compute_beta(b), state, mask)
         if state_out is not None:
             state_out.copy_(s)
@@ -491,14 +520,15 @@ def gated_delta_update(q, k, v, a, b, A_log, dt_bias, state=None, mask=None, use
         if mask is not None:
             raise ValueError("the chunked kernel does not take a mask")
         return _chunked(q, k, v, a, b, _lib.GATES_RAW, A_log, dt_bias, state,
-                        cu_seqlens=cu_seqlens, state_out=state_out, workspace=workspace)
+                        cu_seqlens=cu_seqlens, state_out=state_out, workspace=workspace,
+                        state_index=state_index)
     y, s, _ = _recurrent(q, k, v, a, b, _lib.GATES_RAW, A_log, dt_bias, state, mask,
-                         state_out=state_out, cu_seqlens=cu_seqlens)
+                         state_out=state_out, cu_seqlens=cu_seqlens, state_index=state_index)
     return y, s
 
 
 def gated_delta_verify(q, k, v, a, b, A_log, dt_bias, state, mask=None, *, snapshots=False,
-                       cu_seqlens: Optional[IntSeq] = None):
+                       cu_seqlens: Optional[IntSeq] = None, state_index=None):
     """Speculative verify: y for all T draft tokens without writing the state.
 
     With ``snapshots=True`` also returns the float32 state after every token
@@ -508,12 +538,13 @@ def gated_delta_verify(q, k, v, a, b, A_log, dt_bias, state, mask=None, *, snaps
     Returns ``(y, snapshots or None)``.
     """
     y, _, snaps = _recurrent(q, k, v, a, b, _lib.GATES_RAW, A_log, dt_bias, state, mask,
-                             write_state=False, snapshots=snapshots, cu_seqlens=cu_seqlens)
+                             write_state=False, snapshots=snapshots, cu_seqlens=cu_seqlens,
+                             state_index=state_index)
     return y, snaps
 
 
 def gated_delta_commit(k, v, a, b, A_log, dt_bias, state, n_commit: IntSeq, mask=None, *,
-                       state_out=None, cu_seqlens: Optional[IntSeq] = None):
+                       state_out=None, cu_seqlens: Optional[IntSeq] = None, state_index=None):
     """Commit the accepted prefix of a verify: the state after ``n_commit[b]`` tokens.
 
     Equivalent to the reference rollback, which re-runs ``gated_delta_update``
@@ -527,5 +558,6 @@ def gated_delta_commit(k, v, a, b, A_log, dt_bias, state, n_commit: IntSeq, mask
     dev = _require_device([k], ["k"])
     commit = _int_rows(n_commit, n_rows, dev, "n_commit")
     _, s, _ = _recurrent(None, k, v, a, b, _lib.GATES_RAW, A_log, dt_bias, state, mask,
-                         y=False, state_out=state_out, cu_seqlens=cu_seqlens, commit_len=commit)
+                         y=False, state_out=state_out, cu_seqlens=cu_seqlens, commit_len=commit,
+                         state_index=state_index)
     return s

@@ -37,12 +37,14 @@ def test_exports_match_header(lib):
 
 
 def test_abi_version(lib):
-    assert lib.gdn_abi_version() == _lib.GDN_ABI_VERSION == 1
+    assert lib.gdn_abi_version() == _lib.GDN_ABI_VERSION == 2
 
 
 def test_struct_layout_matches_header():
-    # gdn_recurrent_args: 25 fields; pointers 8 B, int32 fields packed in pairs.
-    assert ctypes.sizeof(_lib.RecurrentArgs) == 8 * 3 + 4 * 2 + 8 * 2 + 4 * 2 + 8 * 9 + 8 * 6 + 8
+    # gdn_recurrent_args: 27 fields; pointers 8 B, int32 fields packed in pairs.
+    assert ctypes.sizeof(_lib.RecurrentArgs) == 8 * 3 + 4 * 2 + 8 * 2 + 4 * 2 + 8 * 10 + 8 * 6 + 8 + 8
+    assert _lib.RecurrentArgs.state_index.offset == _lib.RecurrentArgs.commit_len.offset + 8
+    assert _lib.RecurrentArgs.n_slots.offset == _lib.RecurrentArgs.Dv.offset + 8
 
 
 def _update(lib, **kw):
@@ -118,7 +120,7 @@ def test_chunk_rejects_bad_arguments(lib):
     def call(**kw):
         args = dict(q=FAKE, k=FAKE, v=FAKE, qkv=_lib.DTYPE_BF16, mode=_lib.GATES_RAW, gx=FAKE, gy=FAKE,
                     gdt=_lib.DTYPE_BF16, A_log=FAKE, dt_bias=FAKE, pdt=_lib.DTYPE_F32, s_in=None, y=FAKE,
-                    s_out=FAKE, cu=None, n_seqs=1, n_tok=4096, Hk=16, Hv=32, Dk=128, Dv=128, chunk=64,
+                    s_out=FAKE, index=None, n_slots=0, cu=None, n_seqs=1, n_tok=4096, Hk=16, Hv=32, Dk=128, Dv=128, chunk=64,
                     ws=FAKE, ws_bytes=1 << 40)
         args.update(kw)
         return lib.gdn_chunk_fwd(*args.values(), None)
@@ -130,6 +132,14 @@ def test_chunk_rejects_bad_arguments(lib):
     assert call(y=None) == _lib.ERR_INVALID
     assert call(n_seqs=2, n_tok=4095) == _lib.ERR_INVALID  # not n_seqs rows of equal length
     assert call(n_seqs=0, n_tok=0) == _lib.OK
+    assert call(index=FAKE, n_slots=-1) == _lib.ERR_INVALID
+
+
+def test_recurrent_rejects_bad_pool_size(lib):
+    a = _lib.RecurrentArgs(q=FAKE, k=FAKE, v=FAKE, gx=FAKE, gy=FAKE, gate_mode=_lib.GATES_PRE, y=FAKE,
+                           state_out=FAKE, state_index=FAKE, n_slots=-3, B=1, T=1, Hk=1, Hv=1, Dk=128, Dv=128)
+    assert lib.gdn_recurrent(ctypes.byref(a)) == _lib.ERR_INVALID
+    assert "n_slots" in _lib.last_error()
 
 
 def test_workspace_size_is_monotone(lib):

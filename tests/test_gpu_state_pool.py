@@ -1,0 +1,165 @@
+"""GPU checks of pooled states (``state_index``): every kernel path gives
+bit-identical results whether a row's state sits in a dense batch tensor or
+in a pool slot, slots of other rows are untouched, rows whose slot lies
+outside the pool are skipped, and a batch lifecycle (steps, filter, merge)
+through the pool equals the dense ArraysCache lifecycle."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import multiplex_amd as mx
+from gdn_cases import STATE_TOL, Y_TOL, draw, head_errs_state, row_errs_y, to_torch
+from oracle import gdn
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+Hk, Hv, D = 2, 4, 128
+
+
+def pool_with(seed, n_slots):
+    g = torch.Generator().manual_seed(seed)
+    pool = mx.StatePool(n_slots, Hv, D, D, device=DEV)
+    pool.states.copy_(torch.randn(pool.states.shape, generator=g) * 0.02)
+    return pool
+
+
+def inputs(seed, B, T):
+    t, _ = to_torch(draw(seed, B, T, Hk, Hv, D, D, state=False), DEV)
+    return t
+
+
+def gdn_args(t):
+    return t["q"], t["k"], t["v"], t["a"], t["b"], t["A_log"], t["dt_bias"]
+
+
+def others_unchanged(pool, before, slots):
+    rest = [s for s in range(pool.n_slots) if s not in set(slots)]
+    assert torch.equal(pool.states[rest], before[rest])
+
+
+def test_decode_pooled_equals_dense():
+    pool = pool_with(1, 11)
+    slots = [7, 2, 9, 0, 5, 3]
+    t = inputs(2, len(slots), 1)
+    before = pool.states.clone()
+    dense = before[slots].clone()
+    y_d, S_d = mx.gated_delta_update(*gdn_args(t), dense)
+    idx = pool.index(slots)
+    y_p, out = mx.gated_delta_update(*gdn_args(t), pool.states, state_index=idx)
+    torch.cuda.synchronize()
+    assert out.data_ptr() == pool.states.data_ptr()      # in place on the pool
+    assert torch.equal(y_p, y_d)
+    assert torch.equal(pool.states[slots], S_d)
+    others_unchanged(pool, before, slots)
+
+
+def test_verify_and_commit_pooled_equal_dense():
+    pool = pool_with(3, 9)
+    slots = [8, 1, 4, 6]
+    T = 4
+    t = inputs(4, len(slots), T)
+    n = torch.tensor([1, 4, 0, 3], dtype=torch.int32)
+    before = pool.states.clone()
+    dense = before[slots].clone()
+    y_d, _ = mx.gated_delta_verify(*gdn_args(t), dense)
+    S_d = mx.gated_delta_commit(*gdn_args(t)[1:], dense, n)
+    idx = pool.index(slots)
+    y_p, _ = mx.gated_delta_verify(*gdn_args(t), pool.states, state_index=idx)
+    torch.cuda.synchronize()
+    assert torch.equal(pool.states, before)               # verify writes nothing
+    mx.gated_delta_commit(*gdn_args(t)[1:], pool.states, n, state_index=idx)
+    torch.cuda.synchronize()
+    assert torch.equal(y_p, y_d)
+    assert torch.equal(pool.states[slots], S_d)
+    others_unchanged(pool, before, slots)
+
+
+@pytest.mark.parametrize("fresh", [False, True])
+def test_chunked_prefill_pooled_equals_dense(fresh):
+    pool = pool_with(5, 7)
+    slots = [5, 0, 3]
+    lens = [100, 64, 200]
+    cu = [0, 100, 164, 364]
+    t = inputs(6, 1, sum(lens))
+    before = pool.states.clone()
+    dense = None if fresh else before[slots].clone()
+    y_d, S_d = mx.gated_delta_update(*gdn_args(t), dense, cu_seqlens=cu, chunked=True)
+    idx = pool.index(slots)
+    if fresh:
+        y_p, _ = mx.gated_delta_update(*gdn_args(t), None, cu_seqlens=cu, chunked=True, state_index=idx,
+                                       state_out=pool.states)
+    else:
+        y_p, _ = mx.gated_delta_update(*gdn_args(t), pool.states, cu_seqlens=cu, chunked=True, state_index=idx)
+    torch.cuda.synchronize()
+    assert torch.equal(y_p, y_d)
+    assert torch.equal(pool.states[slots], S_d)
+    others_unchanged(pool, before, slots)
+
+
+def test_rows_with_out_of_range_slots_are_skipped():
+    pool = pool_with(7, 6)
+    slots = [1, -1, 6, 4]                                  # rows 1 and 2 have no valid slot
+    t = inputs(8, len(slots), 3)
+    before = pool.states.clone()
+    dense = torch.zeros(len(slots), Hv, D, D, device=DEV)
+    dense[0], dense[3] = before[1], before[4]
+    y_d, S_d = mx.gated_delta_update(*gdn_args(t), dense)
+    y_p, _ = mx.gated_delta_update(*gdn_args(t), pool.states, state_index=torch.tensor(slots, dtype=torch.int32,
+                                                                                        device=DEV))
+    torch.cuda.synchronize()
+    for b, s in ((0, 1), (3, 4)):
+        assert torch.equal(y_p[b], y_d[b])
+        assert torch.equal(pool.states[s], S_d[b])
+    others_unchanged(pool, before, [1, 4])
+
+
+def test_batch_lifecycle_through_the_pool_equals_dense():
+    """Three decode steps on 4 rows, drop rows 1 and 3, add a fresh row,
+    two more steps: pooled (indices only) vs dense (index_select + cat),
+    and both against the float64 oracle."""
+    pool = pool_with(9, 8)
+    batch = mx.PooledBatch(pool, pool.alloc(4, zero=False))
+    dense = pool.gather(batch.slots)
+    ref_state = dense.double().cpu().numpy()
+
+    def step(seed, dense, ref_state):
+        t, r = to_torch(draw(seed, len(batch), 1, Hk, Hv, D, D, state=False), DEV)
+        y_d, dense = mx.gated_delta_update(*gdn_args(t), dense)
+        y_p, _ = mx.gated_delta_update(*gdn_args(t), pool.states, state_index=batch.index)
+        torch.cuda.synchronize()
+        assert torch.equal(y_p, y_d)
+        assert torch.equal(pool.gather(batch.slots), dense)
+        y_r, ref_state = gdn.gated_delta_update(r["q"], r["k"], r["v"], r["a"], r["b"], r["A_log"], r["dt_bias"],
+                                                ref_state)
+        assert row_errs_y(y_p.float().cpu().numpy(), y_r).max() <= Y_TOL
+        assert head_errs_state(dense.cpu().numpy(), ref_state).max() <= STATE_TOL
+        return dense, ref_state
+
+    for s in range(3):
+        dense, ref_state = step(20 + s, dense, ref_state)
+    batch.filter([0, 2])
+    dense = dense.index_select(0, torch.tensor([0, 2], device=DEV))
+    ref_state = ref_state[[0, 2]]
+    new = mx.PooledBatch.new(pool, 1)
+    batch = mx.PooledBatch.merge([batch, new])
+    dense = torch.cat([dense, torch.zeros(1, Hv, D, D, device=DEV)])
+    ref_state = np.concatenate([ref_state, np.zeros((1, Hv, D, D))])
+    for s in range(2):
+        dense, ref_state = step(30 + s, dense, ref_state)
+
+
+def test_prepared_pooled_decode_equals_call():
+    pool = pool_with(11, 5)
+    slots = [4, 1]
+    t = inputs(12, 2, 1)
+    ref_pool = pool.states.clone()
+    idx = pool.index(slots)
+    y_c, _ = mx.gated_delta_update(*gdn_args(t), ref_pool, state_index=idx)
+    plan = mx.prepare_recurrent(*gdn_args(t), pool.states, state_index=idx, state_out=pool.states)
+    plan.launch()
+    torch.cuda.synchronize()
+    assert torch.equal(plan.outputs[0], y_c)
+    assert torch.equal(pool.states, ref_pool)
