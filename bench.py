@@ -349,6 +349,35 @@ def bench_pool(torch, mx, dev, timer, iters=20):
                 decode_b64_pooled_gbs=round(decode_bytes(B) / (t_dec * 1e-3) / 1e9, 1))
 
 
+def bench_prefix_state(torch, mx, dev, layers=24):
+    """Prefix-cache state records: a snapshot of ``layers`` GDN layers (conv
+    state [1,3,8192] bf16 + recurrent state [1,32,128,128] fp32 each) staged
+    device -> pinned host asynchronously, encoded (SHA-256 content keys) and
+    uploaded back."""
+    from multiplex_amd import prefix_state as ps
+
+    gen = torch.Generator().manual_seed(1007)
+    snap = [[torch.randn(1, KT - 1, C_DIM, generator=gen).to(torch.bfloat16).to(dev),
+             (torch.randn(1, Hv, Dv, Dk, generator=gen) * 0.02).to(dev)] for _ in range(layers)]
+    nbytes = sum(t.numel() * t.element_size() for layer in snap for t in layer)
+    side = torch.cuda.Stream(dev)
+    ps.stage_to_host(snap, side).wait()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    host = ps.stage_to_host(snap, side).wait()
+    t_d2h = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    spec, blobs = ps.encode_tree(host)
+    t_enc = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    back = ps.load_tree(spec, blobs.__getitem__, dev)
+    torch.cuda.synchronize()
+    t_h2d = time.perf_counter() - t0
+    ok = all(torch.equal(a, b) for la, lb in zip(snap, back) for a, b in zip(la, lb))
+    return dict(layers=layers, bytes=nbytes, d2h_ms=round(1e3 * t_d2h, 3), d2h_gbs=round(nbytes / t_d2h / 1e9, 1),
+                encode_ms=round(1e3 * t_enc, 1), decode_upload_ms=round(1e3 * t_h2d, 1), round_trip_equal=ok)
+
+
 # ------------------------------------------------------------ CPU baseline
 
 def cpu_baseline(torch, budget_s=12.0):
@@ -403,7 +432,8 @@ def main():
                     help="only run a plain 256 MiB device-to-device copy (counter calibration) and exit")
     ap.add_argument("--prefill-only", action="store_true", help="only the T=4096 prefill workload")
     ap.add_argument("--epilogue-only", action="store_true", help="only the gated RMSNorm epilogue workloads")
-    ap.add_argument("--pool-only", action="store_true", help="only the pooled-state workloads")
+    ap.add_argument("--pool-only", action="store_true",
+                    help="only the pooled-state and prefix-cache state-record workloads")
     ap.add_argument("--hbm-ceiling", action="store_true",
                     help="only time in-place streaming updates (read + write) of 128 MiB and 1 GiB fp32 "
                          "with a library elementwise kernel, the practical HBM ceiling the decode kernel is "
@@ -453,7 +483,8 @@ def main():
         print(json.dumps({"inplace_stream": res, "peak_GB/s": HBM_PEAK_GBS}), flush=True)
         return
     if args.pool_only:
-        print(json.dumps({"state_pool": bench_pool(torch, mx, dev, timer)}), flush=True)
+        print(json.dumps({"state_pool": bench_pool(torch, mx, dev, timer),
+                          "prefix_state": bench_prefix_state(torch, mx, dev)}), flush=True)
         return
     if args.epilogue_only:
         print(json.dumps({"epilogue_gated_rmsnorm": bench_epilogue(torch, mx, dev, timer, iters=args.steps)}),
@@ -478,6 +509,7 @@ def main():
         configs["mixed"] = bench_mixed(torch, mx, dev, timer)
         configs["epilogue_gated_rmsnorm"] = bench_epilogue(torch, mx, dev, timer)
         configs["state_pool"] = bench_pool(torch, mx, dev, timer)
+        configs["prefix_state"] = bench_prefix_state(torch, mx, dev)
     base = None if args.no_cpu else cpu_baseline(torch)
 
     line = {

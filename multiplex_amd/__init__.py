@@ -22,6 +22,7 @@ from .gated_delta import (
 from .conv import conv_state_commit, gdn_conv_prologue, prepare_conv_prologue
 from .cache import ArraysCache, clone_ssm, merge_layer, restore_ssm, restore_ssm_snapshot, snapshot_ssm
 from .state_pool import PooledBatch, StatePool
+from . import prefix_state
 from .epilogue import gated_rms_norm, prepare_gated_rms_norm
 from .mixer import GatedDeltaNet, commit_verified
 
