@@ -350,15 +350,177 @@ __global__ __launch_bounds__(kTileThreads) void recurrent_tile_kernel(const RecP
   }
 }
 
+// Speculative verify of T <= 8 draft tokens that writes no state.  With
+// a_t = S0 k_t and b_t = S0 q_t per state row (2T dot products) and
+// r(t,s) = g_{s+1} ... g_t (r(t,t) = 1), gamma_t = g_1 ... g_t, the
+// recurrence unrolls to scalars per row:
+//   delta_t = beta_t (v_t - gamma_t a_t - sum_{s<t} r(t,s) (k_s.k_t) delta_s)
+//   y_t     = gamma_t b_t + sum_{s<=t} r(t,s) (k_s.q_t) delta_s
+// so no intermediate state is formed: about half the VALU work of stepping
+// the state through every token.  The per-head coefficients r(t,s) k_s.k_t
+// and r(t,s) k_s.q_t come from products of g (no logarithms, so a decay that
+// underflows to 0 stays exact) and are formed once per workgroup in LDS.  A
+// masked token has g = 1, beta = 0 and y = 0.
+constexpr int kVerifyMaxT = 8;
+
 template <int DK, int DT, int GF>
-int launch_pf(bool tiled, dim3 grid, dim3 block, hipStream_t st, const RecParams& p) {
-  if (tiled) hipLaunchKernelGGL((recurrent_tile_kernel<DK, DT, GF>), grid, block, 0, st, p);
+__global__ __launch_bounds__(kTileThreads) void verify_wy_kernel(const RecParams p) {
+  constexpr int EPL = DK / kLanesPerRow;
+  constexpr int NV = EPL / 4;
+  constexpr int TM = kVerifyMaxT;
+  const RowCtx c = row_ctx<DK>(p);
+  if (c.skip) return;  // uniform: a workgroup serves one row, before any barrier
+  const int tid = threadIdx.x;
+  const int dv0 = blockIdx.x * kTileRows;
+  const int T = c.L;  // 1 <= T <= kVerifyMaxT on this path
+
+  __shared__ __align__(16) float Ks[TM][DK];
+  __shared__ __align__(16) float Qs[TM][DK];
+  __shared__ float Vs[TM][kTileRows];
+  __shared__ float Gs[TM], Bs[TM];          // g_t, beta_t (1 and 0 when masked)
+  __shared__ float Gam[TM];                 // gamma_t
+  __shared__ float Ckk[TM][TM], Ckq[TM][TM];
+  __shared__ uint8_t Ms[TM];
+
+  float ea, db;
+  param_load<GF, DT>(p.ga, c.hv, ea, db);
+
+  // token loads first (memory returns in issue order), then the state row
+  constexpr int NK4 = TM * DK / 4;  // float4 of k (and of q) in the tile
+  constexpr int KV4 = (NK4 + kTileThreads - 1) / kTileThreads;
+  f32x4 kr[KV4], qr[KV4];
+  static_for<KV4>([&](auto it) {
+    const int i = min(tid + kTileThreads * it.value, NK4 - 1);
+    const int j = i / (DK / 4), e = (i % (DK / 4)) * 4;
+    const int64_t off = ((c.tok0 + min(j, T - 1)) * p.Hk + c.hk) * DK + e;
+    kr[it.value] = IO<DT>::load4(p.k, off);
+    qr[it.value] = IO<DT>::load4(p.q, off);
+  });
+  float vr = 0.0f, gx = 0.0f, gy = 0.0f;
+  uint8_t mm = 1;
+  {
+    const int j = tid / kTileRows, r = tid % kTileRows;  // TM * kTileRows == kTileThreads
+    const int64_t tok = c.tok0 + min(j, T - 1);
+    vr = IO<DT>::load1(p.v, (tok * p.Hv + c.hv) * p.Dv + min(dv0 + r, p.Dv - 1));
+  }
+  if (tid < TM) {
+    const int64_t tok = c.tok0 + min(tid, T - 1);
+    gate_load<GF, DT>(p.ga, tok * p.Hv + c.hv, gx, gy);
+    const uint8_t* mp = p.mask != nullptr ? p.mask + tok : &kActive;
+    mm = *mp;
+  }
+  float s[EPL];
+  load_state<DK>(p, c, s);
+
+  static_for<KV4>([&](auto it) {
+    const int i = tid + kTileThreads * it.value;
+    if (i < NK4) {
+      const int j = i / (DK / 4), e = (i % (DK / 4)) * 4;
+      *reinterpret_cast<f32x4*>(&Ks[j][e]) = kr[it.value];
+      *reinterpret_cast<f32x4*>(&Qs[j][e]) = qr[it.value];
+    }
+  });
+  Vs[tid / kTileRows][tid % kTileRows] = vr;
+  if (tid < TM) {
+    float g, beta;
+    gate_transform<GF>(p.ga.mode, gx, gy, ea, db, g, beta);
+    const bool on = mm != 0 && tid < T;
+    Gs[tid] = on ? g : 1.0f;
+    Bs[tid] = on ? beta : 0.0f;
+    Ms[tid] = on ? 1 : 0;
+  }
+  __syncthreads();
+
+  // Coefficients: 4 lanes per pair s <= t < T, numbered densely (pair p of
+  // row t is t(t+1)/2 + s, so T = 4 needs one wave), DK/4 channels a lane.
+  {
+    const int pair = tid >> 2, part = tid & 3;
+    int t = 0;
+    while (t + 1 < TM && (t + 1) * (t + 2) / 2 <= pair) ++t;
+    const int sidx = pair - t * (t + 1) / 2;
+    float kk = 0.0f, kq = 0.0f;
+    if (t < T && sidx <= t) {
+#pragma unroll
+      for (int e = part * (DK / 4); e < (part + 1) * (DK / 4); e += 4) {
+        const f32x4 ks = *reinterpret_cast<const f32x4*>(&Ks[sidx][e]);
+        const f32x4 kt = *reinterpret_cast<const f32x4*>(&Ks[t][e]);
+        const f32x4 qt = *reinterpret_cast<const f32x4*>(&Qs[t][e]);
+        kk = fmaf(ks.x, kt.x, fmaf(ks.y, kt.y, fmaf(ks.z, kt.z, fmaf(ks.w, kt.w, kk))));
+        kq = fmaf(ks.x, qt.x, fmaf(ks.y, qt.y, fmaf(ks.z, qt.z, fmaf(ks.w, qt.w, kq))));
+      }
+    }
+    kk += dpp_f<GDN_DPP_QUAD_XOR1>(kk);
+    kk += dpp_f<GDN_DPP_QUAD_XOR2>(kk);
+    kq += dpp_f<GDN_DPP_QUAD_XOR1>(kq);
+    kq += dpp_f<GDN_DPP_QUAD_XOR2>(kq);
+    if (part == 0 && t < T && sidx <= t) {
+      float r = 1.0f;
+      for (int u = sidx + 1; u <= t; ++u) r *= Gs[u];
+      Ckk[t][sidx] = sidx < t ? r * kk : 0.0f;
+      Ckq[t][sidx] = r * kq;
+    }
+    if (tid < TM) {
+      float gm = 1.0f;
+      for (int u = 0; u <= tid; ++u) gm *= Gs[u];
+      Gam[tid] = gm;
+    }
+  }
+  __syncthreads();
+
+  // Per state row: 2T dot products, then the scalar recurrence.
+  float a[TM], b[TM];
+  static_for<TM>([&](auto tt) {
+    constexpr int t = tt.value;
+    a[t] = 0.0f;
+    b[t] = 0.0f;
+    if (t < T) {
+      float pa = 0.0f, pb = 0.0f;
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        const f32x4 kx = *reinterpret_cast<const f32x4*>(&Ks[t][i * 32 + c.sub * 4]);
+        const f32x4 qx = *reinterpret_cast<const f32x4*>(&Qs[t][i * 32 + c.sub * 4]);
+        pa = fmaf(s[4 * i], kx.x, pa);
+        pa = fmaf(s[4 * i + 1], kx.y, pa);
+        pa = fmaf(s[4 * i + 2], kx.z, pa);
+        pa = fmaf(s[4 * i + 3], kx.w, pa);
+        pb = fmaf(s[4 * i], qx.x, pb);
+        pb = fmaf(s[4 * i + 1], qx.y, pb);
+        pb = fmaf(s[4 * i + 2], qx.z, pb);
+        pb = fmaf(s[4 * i + 3], qx.w, pb);
+      }
+      a[t] = sum8(pa);
+      b[t] = sum8(pb);
+    }
+  });
+  const int rloc = tid / kLanesPerRow;
+  float dl[TM];
+  static_for<TM>([&](auto tt) {
+    constexpr int t = tt.value;
+    dl[t] = 0.0f;
+    if (t < T) {
+      float u = Vs[t][rloc] - Gam[t] * a[t];
+      float yv = Gam[t] * b[t];
+      static_for<t>([&](auto ss) { u = fmaf(-Ckk[t][ss.value], dl[ss.value], u); });
+      dl[t] = Bs[t] * u;
+      static_for<t + 1>([&](auto ss) { yv = fmaf(Ckq[t][ss.value], dl[ss.value], yv); });
+      if (Ms[t] == 0) yv = 0.0f;
+      if (c.row_ok && c.sub == 0) IO<DT>::store1(p.y, ((c.tok0 + t) * p.Hv + c.hv) * p.Dv + c.dv, yv);
+    }
+  });
+}
+
+enum KernelKind { K_DECODE = 0, K_TILE = 1, K_VERIFY = 2 };
+
+template <int DK, int DT, int GF>
+int launch_pf(int kind, dim3 grid, dim3 block, hipStream_t st, const RecParams& p) {
+  if (kind == K_VERIFY) hipLaunchKernelGGL((verify_wy_kernel<DK, DT, GF>), grid, block, 0, st, p);
+  else if (kind == K_TILE) hipLaunchKernelGGL((recurrent_tile_kernel<DK, DT, GF>), grid, block, 0, st, p);
   else hipLaunchKernelGGL((recurrent_kernel<DK, DT, GF>), grid, block, 0, st, p);
   return gdn_host::check_launch("gdn_recurrent");
 }
 
 template <int DK, int DT>
-int launch_gf(int gf, bool pf, dim3 grid, dim3 block, hipStream_t st, const RecParams& p) {
+int launch_gf(int gf, int pf, dim3 grid, dim3 block, hipStream_t st, const RecParams& p) {
   // Typed gate formats are built for the Dk = 128 kernels; other head
   // sizes read gates through the runtime-dtype path.
   if constexpr (DK == 128) {
@@ -369,7 +531,7 @@ int launch_gf(int gf, bool pf, dim3 grid, dim3 block, hipStream_t st, const RecP
 }
 
 template <int DK>
-int launch_dt(int dt, int gf, bool pf, dim3 grid, dim3 block, hipStream_t st, const RecParams& p) {
+int launch_dt(int dt, int gf, int pf, dim3 grid, dim3 block, hipStream_t st, const RecParams& p) {
   switch (dt) {
     case GDN_DTYPE_BF16:
       return launch_gf<DK, GDN_DTYPE_BF16>(gf, pf, grid, block, st, p);
@@ -454,9 +616,17 @@ int run_recurrent(const gdn_recurrent_args* a) {
   // workgroups (4 per CU), so small batches spread over the 256 CUs.
   // Tokens per row > 1 (or packed rows): stage token tiles in LDS, with
   // workgroups of 4 waves.
+  // A verify of a few tokens without state writes or snapshots: the
+  // unrolled form (verify_wy_kernel), same 32-row workgroups.
+  const bool verify = a->state_out == nullptr && a->snapshots == nullptr && a->y != nullptr &&
+                      a->cu_seqlens == nullptr && a->commit_len == nullptr && a->T >= 1 &&
+                      a->T <= kVerifyMaxT;
   const bool pf = a->T > 1 || a->cu_seqlens != nullptr;
-  int waves = pf ? 4 : 1;
-  for (int w = 4; w >= 1 && !pf; w >>= 1) {
+  const int kind = verify ? K_VERIFY : (pf ? K_TILE : K_DECODE);
+  // the tile and verify kernels assume workgroups of 4 waves (32 rows)
+  const bool four = kind != K_DECODE;
+  int waves = four ? 4 : 1;
+  for (int w = 4; w >= 1 && !four; w >>= 1) {
     const int64_t rows_per_wg = 8 * w;
     const int64_t wgs = a->B * a->Hv * ((a->Dv + rows_per_wg - 1) / rows_per_wg);
     if (wgs >= 1024 || w == 1) {
@@ -471,11 +641,11 @@ int run_recurrent(const gdn_recurrent_args* a) {
   hipStream_t st = static_cast<hipStream_t>(a->stream);
   switch (a->Dk) {
     case 64:
-      return launch_dt<64>(a->qkv_dtype, gf, pf, grid, block, st, p);
+      return launch_dt<64>(a->qkv_dtype, gf, kind, grid, block, st, p);
     case 128:
-      return launch_dt<128>(a->qkv_dtype, gf, pf, grid, block, st, p);
+      return launch_dt<128>(a->qkv_dtype, gf, kind, grid, block, st, p);
     default:
-      return launch_dt<256>(a->qkv_dtype, gf, pf, grid, block, st, p);
+      return launch_dt<256>(a->qkv_dtype, gf, kind, grid, block, st, p);
   }
 }
 

@@ -74,7 +74,9 @@ def test_verify_then_commit_equals_accepted_prefix():
     assert all(torch.equal(a, b) for a, b in zip(cache.cache, before))
     ref_all = base.clone()
     out_f = m(xv, None, ref_all)
-    assert torch.equal(out_v, out_f)
+    # verify runs the unrolled verify kernel, the forward steps the state:
+    # the same outputs up to fp32 rounding order, then bf16 and the GEMM
+    assert rel_err(out_v.float().cpu().numpy(), out_f.float().cpu().numpy()) <= 2e-3
     # commit the ragged accepted prefixes in one pass
     m.commit(cache, torch.tensor(n, dtype=torch.int32))
     for b in range(B):

@@ -183,6 +183,45 @@ def test_verify_snapshots_and_commit():
     assert torch.equal(st[2:], S_c[2:])
 
 
+@pytest.mark.parametrize("T", [1, 2, 3, 4, 5, 8])
+@pytest.mark.parametrize("dtype,Dk,Dv", [("bf16", 128, 128), ("f16", 64, 64), ("f32", 256, 256), ("bf16", 128, 96)])
+def test_verify_without_state_write_matches_oracle(T, dtype, Dk, Dv):
+    """Verify of T <= 8 tokens with no state write or snapshots runs the
+    unrolled kernel; y against the oracle and against the stepping kernel
+    (snapshot mode), masks included."""
+    d = draw(300 + T + Dk + Dv, 3, T, 2, 4, Dk, Dv, mask_p=0.25 if T > 2 else None)
+    t, r = to_torch(d, DEV, dtype=dtype, gate_dtype=dtype)
+    before = t["state"].clone()
+    y, none = mx.gated_delta_verify(t["q"], t["k"], t["v"], t["a"], t["b"], t["A_log"], t["dt_bias"],
+                                    t["state"], t["mask"])
+    assert none is None and torch.equal(t["state"], before)
+    y_ref, _ = oracle_update(r)
+    assert row_errs_y(y.float().cpu().numpy(), y_ref).max() <= Y_TOL
+    y_step, _ = mx.gated_delta_verify(t["q"], t["k"], t["v"], t["a"], t["b"], t["A_log"], t["dt_bias"],
+                                      t["state"], t["mask"], snapshots=True)
+    assert row_errs_y(y.float().cpu().numpy(), y_step.float().cpu().numpy()).max() <= Y_TOL
+    if t["mask"] is not None:
+        off = ~t["mask"].cpu()
+        assert torch.all(y.cpu()[off] == 0)
+
+
+def test_verify_with_underflowing_decay_and_precomputed_gates():
+    d = draw(77, 2, 4, 2, 4, 128, 128)
+    d["A_log"][:] = 12.0          # exp(A_log) softplus(.) >> 100: g underflows to 0
+    t, r = to_torch(d, DEV)
+    y, _ = mx.gated_delta_verify(t["q"], t["k"], t["v"], t["a"], t["b"], t["A_log"], t["dt_bias"], t["state"])
+    y_ref, _ = oracle_update(r)
+    assert torch.isfinite(y.float()).all()
+    assert row_errs_y(y.float().cpu().numpy(), y_ref).max() <= Y_TOL
+    g = mx.compute_g(t["A_log"], t["a"], t["dt_bias"])
+    beta = mx.compute_beta(t["b"])
+    plan = mx.prepare_recurrent(t["q"], t["k"], t["v"], g, beta, None, None, t["state"], write_state=False,
+                                gates_precomputed=True)
+    plan.launch()
+    torch.cuda.synchronize()
+    assert row_errs_y(plan.outputs[0].float().cpu().numpy(), y_ref).max() <= Y_TOL
+
+
 def test_packed_ragged_rows():
     lens = [1, 4, 0, 3, 1, 7]
     cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
