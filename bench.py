@@ -432,6 +432,7 @@ def main():
                     help="only run a plain 256 MiB device-to-device copy (counter calibration) and exit")
     ap.add_argument("--prefill-only", action="store_true", help="only the T=4096 prefill workload")
     ap.add_argument("--epilogue-only", action="store_true", help="only the gated RMSNorm epilogue workloads")
+    ap.add_argument("--verify-only", action="store_true", help="only the B=32, T=4 verify + commit workload")
     ap.add_argument("--pool-only", action="store_true",
                     help="only the pooled-state and prefix-cache state-record workloads")
     ap.add_argument("--hbm-ceiling", action="store_true",
@@ -481,6 +482,9 @@ def main():
             res[f"{mib}MiB"] = {"ms": round(t, 5), "GB/s": round(2 * x.numel() * 4 / (t * 1e-3) / 1e9, 1)}
             del x
         print(json.dumps({"inplace_stream": res, "peak_GB/s": HBM_PEAK_GBS}), flush=True)
+        return
+    if args.verify_only:
+        print(json.dumps({"verify_b32_t4": bench_verify(torch, mx, dev, timer, iters=args.steps)}), flush=True)
         return
     if args.pool_only:
         print(json.dumps({"state_pool": bench_pool(torch, mx, dev, timer),
