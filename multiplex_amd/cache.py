@@ -14,6 +14,10 @@ The verbs are the engine's (``engine.py:300-320`` snapshot/restore,
 cache's (``prefixcache/state.py:65-78`` clone, ``:122-140`` restore).  They
 move whole rows of device tensors; a copy is always a fresh tensor, so later
 in-place kernel writes never reach a snapshot (the reference's ``v + 0``).
+
+``cache[1]`` may also be a :class:`~multiplex_amd.state_pool.PooledBatch`
+(pool slots instead of a dense array): filter and merge then move slot
+indices only, and the copies (extract, clone, snapshot) copy slots.
 """
 
 from __future__ import annotations
@@ -21,6 +25,8 @@ from __future__ import annotations
 from typing import List, Optional, Sequence
 
 import torch
+
+from .state_pool import PooledBatch
 
 __all__ = [
     "ArraysCache",
@@ -32,8 +38,13 @@ __all__ = [
 ]
 
 
-def _copy(v: Optional[torch.Tensor]) -> Optional[torch.Tensor]:
-    return None if v is None else v.clone()
+def _copy(v):
+    """An independent copy: a fresh tensor, or fresh pool slots."""
+    if v is None:
+        return None
+    if isinstance(v, PooledBatch):
+        return v.snapshot()
+    return v.clone()
 
 
 class ArraysCache:
@@ -71,19 +82,28 @@ class ArraysCache:
 
     @property
     def nbytes(self) -> int:
-        return sum(v.numel() * v.element_size() for v in self.cache if v is not None)
+        total = 0
+        for v in self.cache:
+            if isinstance(v, PooledBatch):
+                total += len(v) * v.pool.states[0].numel() * v.pool.states.element_size()
+            elif v is not None:
+                total += v.numel() * v.element_size()
+        return total
 
     def filter(self, batch_indices) -> None:
         """Keep only rows ``batch_indices`` (in that order), in place (``engine.py:383-387``)."""
         for i, v in enumerate(self.cache):
-            if v is not None:
+            if isinstance(v, PooledBatch):
+                v.filter([int(j) for j in batch_indices])
+            elif v is not None:
                 idx = torch.as_tensor(batch_indices, dtype=torch.long, device=v.device)
                 self.cache[i] = v.index_select(0, idx)
 
     def extract(self, idx: int) -> "ArraysCache":
         """Row ``idx`` as its own single-row cache, leaving this one unchanged (``engine.py:389-393``)."""
         out = ArraysCache(len(self.cache))
-        out.cache = [None if v is None else v[idx : idx + 1].clone() for v in self.cache]
+        out.cache = [None if v is None else (v.extract(idx) if isinstance(v, PooledBatch) else v[idx:idx + 1].clone())
+                     for v in self.cache]
         return out
 
     def clone(self) -> "ArraysCache":
@@ -109,12 +129,22 @@ def restore_ssm(caches: Sequence[object], snap: Sequence[Optional[list]]) -> Non
 
 
 def merge_layer(caches: Sequence[ArraysCache]) -> ArraysCache:
-    """Stacks single- or multi-row caches along the batch axis (``engine.py:424-432``)."""
+    """Stacks single- or multi-row caches along the batch axis (``engine.py:424-432``).
+
+    Pooled entries are joined without moving states (the merged cache takes
+    over the parts' slots).
+    """
     out = ArraysCache(len(caches[0].cache))
-    out.cache = [
-        torch.cat([c.cache[i] for c in caches], dim=0) if caches[0].cache[i] is not None else None
-        for i in range(len(caches[0].cache))
-    ]
+
+    def join(i):
+        first = caches[0].cache[i]
+        if first is None:
+            return None
+        if isinstance(first, PooledBatch):
+            return PooledBatch.merge([c.cache[i] for c in caches])
+        return torch.cat([c.cache[i] for c in caches], dim=0)
+
+    out.cache = [join(i) for i in range(len(caches[0].cache))]
     return out
 
 

@@ -5,7 +5,9 @@ and the engine calls it as ``mixer(inputs, mask=None, cache=None)`` through
 ``_GDNMixerProxy`` (``engine.py:151-170``), finding it by class name
 ``GatedDeltaNet`` on ``layer.linear_attn`` (``engine.py:330-335``).  This
 module keeps that class name and call signature, with ``cache[0]`` the conv
-state and ``cache[1]`` the recurrent state.
+state and ``cache[1]`` the recurrent state -- a dense ``[B, Hv, Dv, Dk]``
+array, or a :class:`~multiplex_amd.state_pool.PooledBatch` whose slots the
+kernels update in place.
 
 Data path per call:
   in_proj_qkv / z / b / a      library GEMMs (hipBLASLt through torch)
@@ -34,6 +36,7 @@ import torch
 from .cache import ArraysCache
 from .conv import conv_state_commit, gdn_conv_prologue
 from .epilogue import gated_rms_norm
+from .state_pool import PooledBatch
 from .gated_delta import IntSeq, gated_delta_commit, gated_delta_update, gated_delta_verify
 
 __all__ = ["GatedDeltaNet", "gated_rms_norm", "commit_verified"]
@@ -116,11 +119,21 @@ class GatedDeltaNet(torch.nn.Module):
         q, k, v, new_cs = gdn_conv_prologue(
             qkv, self.conv1d_weight, self.num_k_heads, self.num_v_heads, self.head_k_dim, self.head_v_dim,
             conv_state, mask, eps=self.rms_norm_eps, write_conv_state=not verify)
+        pooled = isinstance(state, PooledBatch)
         if verify:
             if cache is None:
                 raise ValueError("verify needs the cache the round will be committed into")
-            y, _ = gated_delta_verify(q, k, v, a, b, self.A_log, self.dt_bias, state, mask)
+            if pooled:
+                y, _ = gated_delta_verify(q, k, v, a, b, self.A_log, self.dt_bias, state.pool.states, mask,
+                                          state_index=state.index)
+            else:
+                y, _ = gated_delta_verify(q, k, v, a, b, self.A_log, self.dt_bias, state, mask)
             self._pending = _Pending(qkv, k, v, a, b, mask, conv_state, cache)
+        elif pooled:
+            # the rows' states advance in their pool slots
+            y, _ = gated_delta_update(q, k, v, a, b, self.A_log, self.dt_bias, state.pool.states, mask,
+                                      state_index=state.index)
+            cache[0] = new_cs
         else:
             y, new_state = gated_delta_update(q, k, v, a, b, self.A_log, self.dt_bias, state, mask)
             if cache is not None:
@@ -138,7 +151,11 @@ class GatedDeltaNet(torch.nn.Module):
         if p is None or p.cache is not cache:
             raise ValueError("commit() must follow verify on the same cache")
         state = cache[1]
-        if state is None:
+        if isinstance(state, PooledBatch):
+            gated_delta_commit(p.k, p.v, p.a, p.b, self.A_log, self.dt_bias, state.pool.states, n_commit, p.mask,
+                               state_index=state.index)
+            new_state = state
+        elif state is None:
             new_state = gated_delta_commit(p.k, p.v, p.a, p.b, self.A_log, self.dt_bias, None, n_commit, p.mask)
         else:
             new_state = gated_delta_commit(p.k, p.v, p.a, p.b, self.A_log, self.dt_bias, state, n_commit, p.mask,

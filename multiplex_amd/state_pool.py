@@ -12,11 +12,11 @@ Here the states of all rows live in one pool ``[n_slots, Hv, Dv, Dk]`` per
 layer, and a batch is a list of slots.  The kernels read and write
 ``pool[slot[b]]`` through the ``state_index`` argument of
 :func:`gated_delta_update`, :func:`gated_delta_verify`,
-:func:`gated_delta_commit` and the chunked prefill, so filter, extract and
-merge change only the slot list (an int32 tensor of B entries).  Copies
-remain where the reference semantics need an independent state: a
-prefix-cache snapshot (:meth:`PooledBatch.snapshot`) and export to a dense
-array (:meth:`StatePool.gather`).
+:func:`gated_delta_commit` and the chunked prefill, so filter and merge
+change only the slot list (an int32 tensor of B entries).  Copies remain
+where the reference semantics need an independent state: extracting a row,
+a snapshot (:meth:`PooledBatch.snapshot`) and export to a dense array
+(:meth:`StatePool.gather`).
 
 Slots are managed on the host (one engine thread drives the scheduler,
 ``multiplex/kernel/hub.py:7-13``), so the index tensors are valid by
@@ -112,14 +112,36 @@ class PooledBatch:
     """The rows of one running batch as pool slots (row b -> ``slots[b]``).
 
     The pooled counterpart of ``cache[1]`` of multiplex's per-layer
-    ArraysCache; pass ``pool.states`` as the state and :attr:`index` as
+    ArraysCache (an ArraysCache and the GatedDeltaNet mixer accept one in
+    that place); pass ``pool.states`` as the state and :attr:`index` as
     ``state_index``.
+
+    A batch owns its slots: they return to the pool when the batch is
+    released or garbage-collected (as the reference's arrays are freed).
+    ``merge`` hands the parts' slots to the merged batch; ``extract``,
+    ``snapshot`` and ``clone`` copy into fresh slots, as the reference's
+    ``extract`` and ``v + 0`` copies do.
     """
 
     def __init__(self, pool: StatePool, slots: Sequence[int]):
         self.pool = pool
         self.slots = [int(s) for s in slots]
+        if len(set(self.slots)) != len(self.slots):
+            raise ValueError("a batch cannot hold one slot twice")
         self._index: Optional[torch.Tensor] = None
+
+    def __del__(self):
+        try:
+            if self.slots:
+                self.pool.release(self.slots)
+                self.slots = []
+        except Exception:  # interpreter shutdown or an already-released slot
+            pass
+
+    @property
+    def shape(self):
+        """``[rows, Hv, Dv, Dk]``, like the dense state it stands for."""
+        return (len(self.slots),) + tuple(self.pool.states.shape[1:])
 
     @classmethod
     def new(cls, pool: StatePool, rows: int) -> "PooledBatch":
@@ -139,32 +161,44 @@ class PooledBatch:
         self.slots = slots
         self._index = None
 
-    def filter(self, keep: Sequence[int], *, release: bool = True) -> None:
+    def filter(self, keep: Sequence[int]) -> None:
         """Keeps rows ``keep`` in that order (``engine.py:383-387``); dropped rows' slots are released."""
         keep = [int(i) for i in keep]
+        if len(set(keep)) != len(keep):
+            raise ValueError("filter cannot keep a row twice (two rows would share one state)")
         kept = [self.slots[i] for i in keep]
-        if release:
-            dropped = set(self.slots) - set(kept)
-            self.pool.release(sorted(dropped))
+        dropped = set(self.slots) - set(kept)
+        self.pool.release(sorted(dropped))
         self._set(kept)
 
     def extract(self, b: int) -> "PooledBatch":
-        """Row ``b`` as its own batch sharing the same slot (``engine.py:389-393``; no copy)."""
-        return PooledBatch(self.pool, [self.slots[b]])
+        """A copy of row ``b`` as its own batch, this one unchanged (``engine.py:389-393``)."""
+        dst = self.pool.alloc(1, zero=False)
+        self.pool.copy_slots([self.slots[b]], dst)
+        return PooledBatch(self.pool, dst)
 
     @staticmethod
     def merge(batches: Sequence["PooledBatch"]) -> "PooledBatch":
-        """Concatenates batches of one pool along the rows (``engine.py:424-432``; no copy)."""
+        """Concatenates batches of one pool along the rows (``engine.py:424-432``).
+
+        No state moves: the merged batch takes over the parts' slots and the
+        parts are left empty.
+        """
         pool = batches[0].pool
         if any(b.pool is not pool for b in batches):
             raise ValueError("batches of different pools cannot be merged")
-        return PooledBatch(pool, [s for b in batches for s in b.slots])
+        slots = [s for b in batches for s in b.slots]
+        for b in batches:
+            b._set([])
+        return PooledBatch(pool, slots)
 
     def snapshot(self) -> "PooledBatch":
         """Independent copies of every row's state in fresh slots (``prefixcache/state.py:65-78``)."""
         dst = self.pool.alloc(len(self.slots), zero=False)
         self.pool.copy_slots(self.slots, dst)
         return PooledBatch(self.pool, dst)
+
+    clone = snapshot
 
     def restore(self, snap: "PooledBatch") -> None:
         """Writes ``snap``'s states back into this batch's slots (``engine.py:316-320``)."""

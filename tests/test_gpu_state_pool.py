@@ -163,3 +163,50 @@ def test_prepared_pooled_decode_equals_call():
     torch.cuda.synchronize()
     assert torch.equal(plan.outputs[0], y_c)
     assert torch.equal(pool.states, ref_pool)
+
+
+@torch.no_grad()
+def test_mixer_on_pooled_states_equals_dense():
+    """The GatedDeltaNet mixer with ``cache[1]`` a PooledBatch: prefill,
+    decode, verify + commit, filter and merge give bit-identical outputs and
+    states to the dense ArraysCache path."""
+    hid = 256
+    m = mx.GatedDeltaNet(hid, Hk, Hv, D, D, device=DEV)
+    m.reset_parameters(torch.Generator().manual_seed(31))
+    pool = mx.StatePool(12, Hv, D, D, device=DEV)
+    g = torch.Generator().manual_seed(32)
+
+    def x(B, S):
+        return torch.randn(B, S, hid, generator=g).to(torch.bfloat16).to(DEV)
+
+    def same(dense, pooled):
+        assert torch.equal(dense[0], pooled[0])
+        assert torch.equal(dense[1], pool.gather(pooled[1].slots))
+
+    dense, pooled = mx.ArraysCache(), mx.ArraysCache()
+    pooled[1] = mx.PooledBatch.new(pool, 3)
+    x0 = x(3, 7)
+    assert torch.equal(m(x0, None, dense), m(x0, None, pooled))
+    same(dense, pooled)
+    x1 = x(3, 1)
+    assert torch.equal(m(x1, None, dense), m(x1, None, pooled))
+    same(dense, pooled)
+    xv, n = x(3, 4), torch.tensor([1, 4, 2], dtype=torch.int32)
+    o_d = m(xv, None, dense, verify=True)
+    m.commit(dense, n)
+    o_p = m(xv, None, pooled, verify=True)
+    m.commit(pooled, n)
+    assert torch.equal(o_d, o_p)
+    same(dense, pooled)
+    dense.filter([2, 0])
+    pooled.filter([2, 0])
+    fresh_d, fresh_p = mx.ArraysCache(), mx.ArraysCache()
+    fresh_p[1] = mx.PooledBatch.new(pool, 1)
+    xf = x(1, 5)
+    assert torch.equal(m(xf, None, fresh_d), m(xf, None, fresh_p))
+    dense = mx.merge_layer([dense, fresh_d])
+    pooled = mx.merge_layer([pooled, fresh_p])
+    x2 = x(3, 1)
+    assert torch.equal(m(x2, None, dense), m(x2, None, pooled))
+    same(dense, pooled)
+    assert pool.n_free == 12 - 3

@@ -35,7 +35,7 @@ def test_alloc_zeroes_reused_slots():
     assert p.alloc(1) == s and torch.count_nonzero(p.states[s[0]]) == 0
 
 
-def test_filter_extract_merge_move_indices_only():
+def test_filter_and_merge_move_indices_only():
     p = make(8)
     batch = PooledBatch.new(p, 4)
     for i, s in enumerate(batch.slots):
@@ -44,13 +44,54 @@ def test_filter_extract_merge_move_indices_only():
     batch.filter([3, 1])
     assert batch.slots == [3, 1] and p.n_free == 6
     assert batch.index.tolist() == [3, 1] and batch.index.dtype == torch.int32
-    one = batch.extract(0)
-    assert one.slots == [3]
+    with pytest.raises(ValueError):
+        batch.filter([0, 0])            # two rows on one state
     new = PooledBatch.new(p, 1)
+    n0 = new.slots[0]
     merged = PooledBatch.merge([batch, new])
-    assert merged.slots == [3, 1, new.slots[0]]
+    assert merged.slots == [3, 1, n0] and batch.slots == [] and new.slots == []
+    assert p.n_free == 5
     # no state moved
     assert torch.equal(p.states[[3, 1]], before[[3, 1]])
+
+
+def test_extract_copies_and_batches_own_their_slots():
+    p = make(6)
+    batch = PooledBatch.new(p, 2)
+    p.states[batch.slots[1]] = 5.0
+    row = batch.extract(1)
+    assert row.slots[0] not in batch.slots
+    assert torch.all(p.states[row.slots[0]] == 5.0)
+    p.states[batch.slots[1]] = 6.0                 # the extracted copy is independent
+    assert torch.all(p.states[row.slots[0]] == 5.0)
+    free = p.n_free
+    del row                                        # garbage collection returns the slot
+    assert p.n_free == free + 1
+    batch.release()
+    assert p.n_free == 6 and batch.slots == []
+
+
+def test_arrays_cache_verbs_on_a_pooled_state():
+    from multiplex_amd import ArraysCache, merge_layer, restore_ssm, snapshot_ssm
+
+    p = make(10)
+    c = ArraysCache()
+    c[0] = torch.arange(3 * 2 * 5, dtype=torch.float32).reshape(3, 2, 5)
+    c[1] = PooledBatch.new(p, 3)
+    for i, s in enumerate(c[1].slots):
+        p.states[s] = float(i)
+    assert c.batch_size == 3 and c.nbytes == c[0].numel() * 4 + 3 * 2 * 4 * 8 * 4
+    snap = snapshot_ssm([c, None])
+    assert isinstance(snap[0][1], PooledBatch) and set(snap[0][1].slots).isdisjoint(c[1].slots)
+    c.filter([2, 0])
+    assert torch.equal(c[0][:, 0, 0], torch.tensor([20.0, 0.0]))
+    assert [float(p.states[s][0, 0, 0]) for s in c[1].slots] == [2.0, 0.0]
+    row = c.extract(1)
+    assert float(p.states[row[1].slots[0]][0, 0, 0]) == 0.0 and row[1].slots[0] not in c[1].slots
+    m = merge_layer([c, row])
+    assert m.batch_size == 3 and m[1].slots[:2] != [] and c[1].slots == []
+    restore_ssm([c], [snap[0]])
+    assert [float(p.states[s][0, 0, 0]) for s in c[1].slots] == [0.0, 1.0, 2.0]
 
 
 def test_snapshot_restore_and_dense_round_trip():
