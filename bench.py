@@ -378,6 +378,45 @@ def bench_prefix_state(torch, mx, dev, layers=24):
                 encode_ms=round(1e3 * t_enc, 1), decode_upload_ms=round(1e3 * t_h2d, 1), round_trip_equal=ok)
 
 
+def bench_mixer_layer(torch, mx, dev, timer, iters=20, hidden=2048):
+    """One whole GatedDeltaNet mixer layer at the benchmark head layout with
+    hidden size 2048 (in_proj GEMMs, fused prologue, GDN kernel, fused gated
+    RMSNorm, out_proj GEMM), eager from Python: decode B=64 (one token per
+    row, states in a StatePool updated in place) and prefill T=4096."""
+    gen = torch.Generator().manual_seed(1008)
+    m = mx.GatedDeltaNet(hidden, Hk, Hv, Dk, Dv, device=dev)
+    m.reset_parameters(gen)
+    res = {"hidden": hidden}
+    with torch.no_grad():
+        pool = mx.StatePool(64, Hv, Dv, Dk, device=dev)
+        cache = mx.ArraysCache()
+        cache[1] = mx.PooledBatch.new(pool, 64)
+        x = torch.randn(64, 1, hidden, generator=gen).to(torch.bfloat16).to(dev)
+        for _ in range(3):
+            m(x, None, cache)
+        t = timer.total_ms(lambda i: m(x, None, cache), iters) / iters
+        res["decode_b64_us"] = round(1e3 * t, 2)
+        # the same step captured once in a HIP graph and replayed (the conv
+        # state is handed back to the buffer the captured step reads)
+        cs_in = cache[0]
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            m(x, None, cache)
+            cs_in.copy_(cache[0])
+        cache[0] = cs_in
+        for _ in range(3):
+            graph.replay()
+        t = timer.total_ms(lambda i: graph.replay(), iters) / iters
+        res["decode_b64_graph_us"] = round(1e3 * t, 2)
+        xp = torch.randn(1, 4096, hidden, generator=gen).to(torch.bfloat16).to(dev)
+        for _ in range(2):
+            m(xp, None, mx.ArraysCache())
+        t = timer.total_ms(lambda i: m(xp, None, mx.ArraysCache()), max(3, iters // 4)) / max(3, iters // 4)
+        res["prefill_t4096_ms"] = round(t, 4)
+        res["prefill_t4096_tokens_per_s"] = round(4096 / (t * 1e-3), 1)
+    return res
+
+
 # ------------------------------------------------------------ CPU baseline
 
 def cpu_baseline(torch, budget_s=12.0):
@@ -433,6 +472,7 @@ def main():
     ap.add_argument("--prefill-only", action="store_true", help="only the T=4096 prefill workload")
     ap.add_argument("--epilogue-only", action="store_true", help="only the gated RMSNorm epilogue workloads")
     ap.add_argument("--verify-only", action="store_true", help="only the B=32, T=4 verify + commit workload")
+    ap.add_argument("--mixer-only", action="store_true", help="only the whole-mixer-layer workloads")
     ap.add_argument("--pool-only", action="store_true",
                     help="only the pooled-state and prefix-cache state-record workloads")
     ap.add_argument("--hbm-ceiling", action="store_true",
@@ -483,6 +523,9 @@ def main():
             del x
         print(json.dumps({"inplace_stream": res, "peak_GB/s": HBM_PEAK_GBS}), flush=True)
         return
+    if args.mixer_only:
+        print(json.dumps({"mixer_layer": bench_mixer_layer(torch, mx, dev, timer, iters=args.steps)}), flush=True)
+        return
     if args.verify_only:
         print(json.dumps({"verify_b32_t4": bench_verify(torch, mx, dev, timer, iters=args.steps)}), flush=True)
         return
@@ -514,6 +557,7 @@ def main():
         configs["epilogue_gated_rmsnorm"] = bench_epilogue(torch, mx, dev, timer)
         configs["state_pool"] = bench_pool(torch, mx, dev, timer)
         configs["prefix_state"] = bench_prefix_state(torch, mx, dev)
+        configs["mixer_layer"] = bench_mixer_layer(torch, mx, dev, timer)
     base = None if args.no_cpu else cpu_baseline(torch)
 
     line = {

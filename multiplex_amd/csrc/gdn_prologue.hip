@@ -14,7 +14,7 @@ namespace {
 
 using namespace gdn;
 
-constexpr int kRun = 16;   // tokens per wavefront
+constexpr int kRun = 16;   // tokens per wavefront (prefill)
 constexpr int kWaves = 4;  // wavefronts per workgroup (consecutive runs)
 constexpr int KT = 4;      // conv taps
 
@@ -34,10 +34,11 @@ struct ProParams {
 };
 
 // Locates (sequence, first token, length, run) of this workgroup.  Packed
-// mode walks cu_seqlens: sequence n owns max(1, ceil(len/64)) run slots.
+// mode walks cu_seqlens: sequence n owns max(1, ceil(len/(R*4))) run slots.
+template <int R>
 __device__ __forceinline__ bool locate(const ProParams& p, int& seq, int64_t& start, int& len,
                                        int& run) {
-  constexpr int RW = kRun * kWaves;
+  constexpr int RW = R * kWaves;
   run = blockIdx.y;
   if (p.cu_seqlens == nullptr) {
     seq = blockIdx.z;
@@ -60,8 +61,10 @@ __device__ __forceinline__ bool locate(const ProParams& p, int& seq, int64_t& st
 }
 
 // W32: conv taps are fp32 (else they share the io dtype DT).  MASK: a token
-// mask is given (without one no mask bytes are read or applied).
-template <int D, int DT, bool W32, bool MASK>
+// mask is given (without one no mask bytes are read or applied).  R: tokens
+// per wavefront (16 for prefill; 1 and 4 for decode and verify rows, so a
+// short row does not compute a 16-token run).
+template <int D, int DT, bool W32, bool MASK, int R>
 __global__ __launch_bounds__(256) void prologue_kernel(const ProParams p) {
   constexpr int LPH = D / CPL;   // lanes per head
   constexpr int HPW = 64 / LPH;  // heads per wavefront
@@ -70,10 +73,10 @@ __global__ __launch_bounds__(256) void prologue_kernel(const ProParams p) {
   const int wave = threadIdx.x >> 6;
   int seq, len, run;
   int64_t start;
-  if (!locate(p, seq, start, len, run)) return;
-  const int t_begin = run * (kRun * kWaves) + wave * kRun;
+  if (!locate<R>(p, seq, start, len, run)) return;
+  const int t_begin = run * (R * kWaves) + wave * R;
   if (t_begin >= len && !(len == 0 && t_begin == 0)) return;
-  const int t_end = t_begin + kRun < len ? t_begin + kRun : len;
+  const int t_end = t_begin + R < len ? t_begin + R : len;
 
   // This lane's head (over the 2 Hk + Hv heads of the mixed row) and its 8
   // channels; lanes past the last head work on a copy of it and store nothing.
@@ -118,11 +121,11 @@ __global__ __launch_bounds__(256) void prologue_kernel(const ProParams p) {
   // Issue every load first: the run's tokens (rows past the end re-read the
   // last row and are never stored), the window of the 3 inputs before the
   // run, the taps.  A masked token reads as zero (mask byte as multiplier).
-  Raw8<DT> xs[kRun];
-  float xm[kRun];
+  Raw8<DT> xs[R];
+  float xm[R];
   const int t_last = t_end - 1;
 #pragma unroll
-  for (int u = 0; u < kRun; ++u) {
+  for (int u = 0; u < R; ++u) {
     const int64_t tok = start + min(t_begin + u, t_last);
     xs[u] = load_raw8<DT>(p.qkv, tok * C + c0);
     if constexpr (MASK) xm[u] = p.mask[tok] != 0 ? 1.0f : 0.0f;
@@ -160,7 +163,7 @@ __global__ __launch_bounds__(256) void prologue_kernel(const ProParams p) {
   // Every token of the run is computed (tokens past the end repeat the last
   // row, so no control flow splits the window); only real tokens are stored.
 #pragma unroll
-  for (int u = 0; u < kRun; ++u) {
+  for (int u = 0; u < R; ++u) {
     float x[CPL], o[CPL];
     unpack8<DT>(xs[u], x);
     float ss = 0.0f;
@@ -274,7 +277,9 @@ extern "C" int gdn_conv_prologue(const void* qkv, int io_dtype, const void* conv
   p.C = static_cast<int>(2 * Hk * Dk + Hv * Dv);
   p.eps = eps;
 
-  constexpr int RW = kRun * kWaves;
+  // tokens per wavefront: short unpacked rows (decode, verify) take a short run
+  const int run = (cu_seqlens == nullptr && S <= 1) ? 1 : ((cu_seqlens == nullptr && S <= 4) ? 4 : kRun);
+  const int64_t RW = static_cast<int64_t>(run) * kWaves;
   dim3 block(64 * kWaves);
   dim3 grid;
   const int64_t heads_per_wave = 512 / Dk;  // a lane covers 8 channels
@@ -287,11 +292,19 @@ extern "C" int gdn_conv_prologue(const void* qkv, int io_dtype, const void* conv
     grid.z = static_cast<unsigned>(B);
   }
   hipStream_t st = static_cast<hipStream_t>(stream);
-#define GDN_PRO_LAUNCH_M(D_, DT_, W_)                                                    \
-  if (mask != nullptr)                                                                  \
-    hipLaunchKernelGGL((prologue_kernel<D_, DT_, W_, true>), grid, block, 0, st, p);    \
-  else                                                                                  \
-    hipLaunchKernelGGL((prologue_kernel<D_, DT_, W_, false>), grid, block, 0, st, p)
+#define GDN_PRO_LAUNCH_R(D_, DT_, W_, M_)                                                   \
+  if (run == 1)                                                                            \
+    hipLaunchKernelGGL((prologue_kernel<D_, DT_, W_, M_, 1>), grid, block, 0, st, p);      \
+  else if (run == 4)                                                                       \
+    hipLaunchKernelGGL((prologue_kernel<D_, DT_, W_, M_, 4>), grid, block, 0, st, p);      \
+  else                                                                                     \
+    hipLaunchKernelGGL((prologue_kernel<D_, DT_, W_, M_, kRun>), grid, block, 0, st, p)
+#define GDN_PRO_LAUNCH_M(D_, DT_, W_)    \
+  if (mask != nullptr) {                 \
+    GDN_PRO_LAUNCH_R(D_, DT_, W_, true);  \
+  } else {                               \
+    GDN_PRO_LAUNCH_R(D_, DT_, W_, false); \
+  }
 #define GDN_PRO_LAUNCH(D_, DT_)            \
   if (w_dtype == GDN_DTYPE_F32) {          \
     GDN_PRO_LAUNCH_M(D_, DT_, true);       \
@@ -312,6 +325,7 @@ extern "C" int gdn_conv_prologue(const void* qkv, int io_dtype, const void* conv
 #undef GDN_PRO_DT
 #undef GDN_PRO_LAUNCH
 #undef GDN_PRO_LAUNCH_M
+#undef GDN_PRO_LAUNCH_R
   return gdn_host::check_launch("gdn_conv_prologue");
 }
 

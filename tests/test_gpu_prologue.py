@@ -52,6 +52,16 @@ def check(qkv, w, cs, mask, Hk, Hv, D, cu=None):
     return q, k, v, cs_out
 
 
+@pytest.mark.parametrize("S", [1, 2, 4, 5])
+@pytest.mark.parametrize("D", [64, 128, 256])
+def test_short_rows(S, D):
+    """Decode (S = 1) and verify-sized rows run 1- and 4-token waves."""
+    qkv, w, cs, mask = draw_prologue(60 + S + D, 3, S, 2, 4, D, mask_p=0.3 if S > 1 else None)
+    check(qkv, w, cs, mask, 2, 4, D)
+    qkv, w, _, _ = draw_prologue(61 + S + D, 2, S, 2, 4, D, with_state=False)
+    check(qkv, w, None, None, 2, 4, D)
+
+
 @pytest.mark.parametrize("D", [64, 128, 256])
 def test_prefill_prologue(D):
     qkv, w, cs, mask = draw_prologue(20 + D, 2, 77, 2, 4, D)
