@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define GDN_ABI_VERSION 2
+#define GDN_ABI_VERSION 3
 
 /* dtype codes for the void* operands */
 #define GDN_DTYPE_F32 0
@@ -108,6 +108,9 @@ int gdn_gated_delta_kernel(const void* q, const void* k, const void* v, int qkv_
  *              [0, n_slots) is not processed: its y and its slot are left
  *              as they are.  Rows that write state must use distinct slots.
  *              No counterpart in the reference, which concatenates states.
+ *   gate_stride elements from one token's gate row (gx, gy) to the next,
+ *              >= Hv; 0 = Hv (contiguous).  Lets a and b be column slices of
+ *              one fused in_proj output.
  * Rows run independently; a launch never reads another row's state.
  */
 typedef struct gdn_recurrent_args {
@@ -133,6 +136,7 @@ typedef struct gdn_recurrent_args {
   int64_t B, T;              /* T = tokens per row, or N_tok when packed */
   int64_t Hk, Hv, Dk, Dv;
   int64_t n_slots;           /* pool size when state_index != NULL */
+  int64_t gate_stride;       /* elements between tokens' gate rows (0 = Hv) */
   void* stream;
 } gdn_recurrent_args;
 
@@ -148,7 +152,8 @@ int gdn_recurrent(const gdn_recurrent_args* args);
  * state_out may alias state_in.  state_index [n_seqs] int32 or NULL:
  * pooled states as in gdn_recurrent_args (state_in / state_out are pools of
  * n_slots states; sequence n uses slot state_index[n]; out-of-range slots
- * are skipped).  No mask.  chunk must be 64.
+ * are skipped).  gate_stride as in gdn_recurrent_args.  No mask.  chunk
+ * must be 64.
  * workspace must hold gdn_chunk_workspace_bytes(...) bytes (256-B aligned).
  */
 size_t gdn_chunk_workspace_bytes(int64_t n_seqs, int64_t n_tok, int64_t Hv,
@@ -156,6 +161,7 @@ size_t gdn_chunk_workspace_bytes(int64_t n_seqs, int64_t n_tok, int64_t Hv,
 
 int gdn_chunk_fwd(const void* q, const void* k, const void* v, int qkv_dtype,
                   int gate_mode, const void* gx, const void* gy, int gate_dtype,
+                  int64_t gate_stride,
                   const void* A_log, const void* dt_bias, int param_dtype,
                   const float* state_in, void* y, float* state_out,
                   const int32_t* state_index, int64_t n_slots,
@@ -175,10 +181,13 @@ int gdn_chunk_fwd(const void* q, const void* k, const void* v, int qkv_dtype,
  *   mask           [B,S] uint8 or NULL
  *   q_out, k_out   [B,S,Hk,Dk];  v_out [B,S,Hv,Dv]   (io_dtype)
  *   conv_state_out [B,Kt-1,C] or NULL; must not alias conv_state_in
+ *   qkv_stride     elements from one qkv row (token) to the next, >= C and
+ *                  16-byte aligned; 0 = C.  Lets qkv be a column slice of one
+ *                  fused in_proj output.
  * cu_seqlens: packed sequences as in gdn_chunk_fwd (B = n_seqs, S = n_tok).
  * Requires Dk == Dv in {64, 128, 256}.
  */
-int gdn_conv_prologue(const void* qkv, int io_dtype, const void* conv_state_in,
+int gdn_conv_prologue(const void* qkv, int io_dtype, int64_t qkv_stride, const void* conv_state_in,
                       const void* weight, int w_dtype, const uint8_t* mask,
                       const int32_t* cu_seqlens,
                       void* q_out, void* k_out, void* v_out, void* conv_state_out,
@@ -189,10 +198,10 @@ int gdn_conv_prologue(const void* qkv, int io_dtype, const void* conv_state_in,
  * Conv-state commit of a partially accepted verify (dflash.py:424-425):
  * conv_state_out[b] = concat(conv_state_in[b], masked qkv[b])[n : n+Kt-1]
  * with n = n_commit[b] in [0, T].  conv_state_out must not alias
- * conv_state_in.
+ * conv_state_in.  qkv_stride as in gdn_conv_prologue.
  */
 int gdn_conv_state_commit(const void* conv_state_in, const void* qkv, int io_dtype,
-                          const uint8_t* mask, const int32_t* n_commit,
+                          int64_t qkv_stride, const uint8_t* mask, const int32_t* n_commit,
                           void* conv_state_out, int64_t B, int64_t T, int64_t C,
                           int64_t Kt, void* stream);
 
@@ -204,10 +213,15 @@ int gdn_conv_state_commit(const void* conv_state_in, const void* qkv, int io_dty
  *   n = x / sqrt(mean(x^2) + eps)       rounded to io_dtype
  *   m = weight * n                      rounded to io_dtype if w_dtype == io_dtype
  *   out = m * silu(gate)                (fp32 product, rounded once)
- *   x, gate, out  [rows, D] io_dtype;  weight [D] w_dtype, or NULL for ones
- * out may alias x or gate.  Requires D in {64, 128, 256}.
+ *   x, out  [rows, D] io_dtype;  weight [D] w_dtype, or NULL for ones
+ *   gate     io_dtype: row r at (r / gate_group) * gate_stride +
+ *            (r % gate_group) * D (lines of gate_group rows, e.g. one
+ *            token's heads, gate_stride elements apart); gate_group = 0
+ *            means [rows, D] contiguous.
+ * out may alias x (or a contiguous gate).  Requires D in {64, 128, 256}.
  */
 int gdn_gated_rmsnorm(const void* x, const void* gate, int io_dtype,
+                      int64_t gate_group, int64_t gate_stride,
                       const void* weight, int w_dtype, void* out,
                       int64_t rows, int64_t D, float eps, void* stream);
 

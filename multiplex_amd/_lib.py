@@ -13,7 +13,7 @@ from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libgdn.so"
 
-GDN_ABI_VERSION = 2
+GDN_ABI_VERSION = 3
 
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
@@ -72,6 +72,7 @@ class RecurrentArgs(Structure):
         ("Dk", c_int64),
         ("Dv", c_int64),
         ("n_slots", c_int64),
+        ("gate_stride", c_int64),
         ("stream", c_void_p),
     ]
 
@@ -107,21 +108,21 @@ _SIGNATURES = {
     "gdn_chunk_workspace_bytes": (c_size_t, [_I64, _I64, _I64, _I64, _I64, _I64]),
     "gdn_chunk_fwd": (
         c_int,
-        [_P, _P, _P, c_int, c_int, _P, _P, c_int, _P, _P, c_int, _P, _P, _P, _P, _I64, _P,
+        [_P, _P, _P, c_int, c_int, _P, _P, c_int, _I64, _P, _P, c_int, _P, _P, _P, _P, _I64, _P,
          _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P, c_size_t, _P],
     ),
     "gdn_conv_prologue": (
         c_int,
-        [_P, c_int, _P, _P, c_int, _P, _P, _P, _P, _P, _P,
+        [_P, c_int, _I64, _P, _P, c_int, _P, _P, _P, _P, _P, _P,
          _I64, _I64, _I64, _I64, _I64, _I64, _I64, c_float, _P],
     ),
     "gdn_conv_state_commit": (
         c_int,
-        [_P, _P, c_int, _P, _P, _P, _I64, _I64, _I64, _I64, _P],
+        [_P, _P, c_int, _I64, _P, _P, _P, _I64, _I64, _I64, _I64, _P],
     ),
     "gdn_gated_rmsnorm": (
         c_int,
-        [_P, _P, c_int, _P, c_int, _P, _I64, _I64, c_float, _P],
+        [_P, _P, c_int, _I64, _I64, _P, c_int, _P, _I64, _I64, c_float, _P],
     ),
 }
 

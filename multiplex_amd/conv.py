@@ -16,7 +16,7 @@ import torch
 
 from . import _lib
 from .gated_delta import (IntSeq, PreparedCall, _contig, _cu_seqlens, _dtype_code, _int_rows, _mask_u8, _ptr,
-                          _require_device, _stream)
+                          _require_device, _stream, _token_rows)
 
 __all__ = ["gdn_conv_prologue", "prepare_conv_prologue", "conv_state_commit"]
 
@@ -34,6 +34,16 @@ def _weight_2d(conv_weight: torch.Tensor, C: int) -> torch.Tensor:
     if w.dim() != 2 or w.shape[0] != C:
         raise ValueError(f"conv weight must be [C={C}, K] (got {tuple(conv_weight.shape)})")
     return w.contiguous()
+
+
+def _qkv_rows(qkv: torch.Tensor, C: int):
+    """``(qkv, qkv_stride)``: a column slice of a wider row-major buffer (e.g.
+    a fused in_proj output) is read in place when its rows stay 16-byte
+    aligned; anything else is made contiguous (stride 0)."""
+    ld = _token_rows(qkv, C)
+    if ld is not None and (ld * qkv.element_size()) % 16 == 0 and qkv.data_ptr() % 16 == 0:
+        return qkv, (0 if ld == C else ld)
+    return qkv.contiguous(), 0
 
 
 def _prologue_args(qkv, conv_weight, num_k_heads, num_v_heads, head_k_dim, head_v_dim, conv_state, mask,
@@ -58,12 +68,12 @@ def _prologue_args(qkv, conv_weight, num_k_heads, num_v_heads, head_k_dim, head_
             raise ValueError(f"conv_state must be {(n_rows, Kt - 1, C)} of dtype {qkv.dtype}")
         conv_state = conv_state.contiguous()
     m = _mask_u8(mask, (B, S))
-    qkv = _contig(qkv)
+    qkv, ld = _qkv_rows(qkv, C)
     q = torch.empty(B, S, Hk, Dk, dtype=qkv.dtype, device=dev)
     k = torch.empty(B, S, Hk, Dk, dtype=qkv.dtype, device=dev)
     v = torch.empty(B, S, Hv, Dv, dtype=qkv.dtype, device=dev)
     cs_out = torch.empty(n_rows, Kt - 1, C, dtype=qkv.dtype, device=dev) if write_conv_state else None
-    args = (_ptr(qkv), io, _ptr(conv_state), _ptr(w), wdt, _ptr(m), _ptr(cu), _ptr(q), _ptr(k), _ptr(v),
+    args = (_ptr(qkv), io, ld, _ptr(conv_state), _ptr(w), wdt, _ptr(m), _ptr(cu), _ptr(q), _ptr(k), _ptr(v),
             _ptr(cs_out), n_rows, S, Hk, Hv, Dk, Dv, Kt, float(eps), _stream(dev))
     keep = dict(qkv=qkv, conv_state=conv_state, w=w, mask=m, cu=cu)
     return args, keep, (q, k, v, cs_out), dev
@@ -98,12 +108,13 @@ def prepare_conv_prologue(qkv: torch.Tensor, conv_weight: torch.Tensor, num_k_he
                           write_conv_state: bool = True) -> PreparedCall:
     """Validates the prologue once; ``launch()`` re-issues it (``outputs`` = ``(q, k, v, conv_state)``).
 
-    qkv must be contiguous (it is bound by address, so refill it in place).
+    qkv must be contiguous or a column slice with one row stride (it is bound
+    by address, so refill it in place).
     """
-    if not qkv.is_contiguous():
-        raise ValueError("qkv must be contiguous for a prepared launch")
     args, keep, outs, dev = _prologue_args(qkv, conv_weight, num_k_heads, num_v_heads, head_k_dim,
                                            head_v_dim, conv_state, mask, cu_seqlens, eps, write_conv_state)
+    if keep["qkv"].data_ptr() != qkv.data_ptr():
+        raise ValueError("qkv must be contiguous (or a one-stride column slice) for a prepared launch")
     keep.update(q=outs[0], k=outs[1], v=outs[2], cs_out=outs[3])
     return PreparedCall("gdn_conv_prologue", args, keep, outs, dev)
 
@@ -126,8 +137,10 @@ def conv_state_commit(conv_state: Optional[torch.Tensor], qkv: torch.Tensor, n_c
     n = _int_rows(n_commit, B, dev, "n_commit")
     m = _mask_u8(mask, (B, T))
     out = torch.empty(B, Kt - 1, C, dtype=qkv.dtype, device=dev)
-    qkv = _contig(qkv)
+    ld = _token_rows(qkv, C)
+    if ld is None:
+        qkv, ld = qkv.contiguous(), C
     with torch.cuda.device(dev):
-        _lib.call("gdn_conv_state_commit", _ptr(conv_state), _ptr(qkv), io, _ptr(m), _ptr(n), _ptr(out),
+        _lib.call("gdn_conv_state_commit", _ptr(conv_state), _ptr(qkv), io, ld, _ptr(m), _ptr(n), _ptr(out),
                   B, T, C, Kt, _stream(dev))
     return out

@@ -225,7 +225,7 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(const ChunkParams p) {
   // K/Q rows queued behind; then the rows (rows past the chunk's end read its
   // last row and are zeroed at the LDS store).
   float lg = 0.0f, bt = 0.0f;
-  if (wave == 0) load_log_gates(p.ga, (tok0 + min(lane, len - 1)) * p.Hv + hv, hv, lg, bt);
+  if (wave == 0) load_log_gates(p.ga, (tok0 + min(lane, len - 1)) * p.ga.ld + hv, hv, lg, bt);
   u32x4 kr[4], qr[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
@@ -746,6 +746,7 @@ extern "C" size_t gdn_chunk_workspace_bytes(int64_t n_seqs, int64_t n_tok, int64
 
 extern "C" int gdn_chunk_fwd(const void* q, const void* k, const void* v, int qkv_dtype,
                              int gate_mode, const void* gx, const void* gy, int gate_dtype,
+                             int64_t gate_stride,
                              const void* A_log, const void* dt_bias, int param_dtype,
                              const float* state_in, void* y, float* state_out,
                              const int32_t* state_index, int64_t n_slots,
@@ -772,6 +773,9 @@ extern "C" int gdn_chunk_fwd(const void* q, const void* k, const void* v, int qk
   if (n_tok > 0 && (!q || !k || !v || !gx || !gy || !y))
     return fail(GDN_ERR_INVALID, "gdn_chunk_fwd: q, k, v, gates and y are required");
   if (!state_out) return fail(GDN_ERR_INVALID, "gdn_chunk_fwd: state_out is required");
+  if (gate_stride != 0 && gate_stride < Hv)
+    return fail(GDN_ERR_INVALID, "gdn_chunk_fwd: gate_stride=%lld is below Hv=%lld", (long long)gate_stride,
+                (long long)Hv);
   if (state_index != nullptr && (n_slots < 0 || n_slots > INT32_MAX))
     return fail(GDN_ERR_INVALID, "gdn_chunk_fwd: n_slots=%lld out of range", (long long)n_slots);
   if (n_seqs == 0) return GDN_OK;
@@ -792,6 +796,7 @@ extern "C" int gdn_chunk_fwd(const void* q, const void* k, const void* v, int qk
   p.v = static_cast<const uint16_t*>(v);
   p.ga.gx = gx;
   p.ga.gy = gy;
+  p.ga.ld = gate_stride > 0 ? gate_stride : Hv;
   p.ga.A_log = A_log;
   p.ga.dt_bias = dt_bias;
   p.ga.mode = gate_mode;

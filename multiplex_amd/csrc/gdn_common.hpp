@@ -155,6 +155,7 @@ struct GateArgs {
   const void* gy;  // b or beta
   const void* A_log;
   const void* dt_bias;
+  int64_t ld;      // elements from one token's gate row to the next (Hv when packed)
   int mode, gdt, pdt;
 };
 

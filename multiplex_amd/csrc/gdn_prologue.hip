@@ -30,6 +30,7 @@ struct ProParams {
   void* v_out;
   void* cs_out;
   int n_seqs, S, Hk, Hv, C;
+  int64_t ld;  // elements from one qkv row to the next (>= C)
   float eps;
 };
 
@@ -98,7 +99,7 @@ __global__ __launch_bounds__(256) void prologue_kernel(const ProParams p) {
       }
     } else {
       const int64_t tok = start + xi - (KT - 1);
-      unpack8<DT>(load_raw8<DT>(p.qkv, tok * C + c0), dst);
+      unpack8<DT>(load_raw8<DT>(p.qkv, tok * p.ld + c0), dst);
       if constexpr (MASK) {
         const float wm = p.mask[tok] != 0 ? 1.0f : 0.0f;
 #pragma unroll
@@ -127,7 +128,7 @@ __global__ __launch_bounds__(256) void prologue_kernel(const ProParams p) {
 #pragma unroll
   for (int u = 0; u < R; ++u) {
     const int64_t tok = start + min(t_begin + u, t_last);
-    xs[u] = load_raw8<DT>(p.qkv, tok * C + c0);
+    xs[u] = load_raw8<DT>(p.qkv, tok * p.ld + c0);
     if constexpr (MASK) xm[u] = p.mask[tok] != 0 ? 1.0f : 0.0f;
   }
   // window[i] = X[t + i] for the run's first token t
@@ -207,7 +208,7 @@ template <int DT>
 __global__ __launch_bounds__(256) void conv_commit_kernel(const void* cs_in, const void* qkv,
                                                           const uint8_t* mask,
                                                           const int32_t* n_commit, void* cs_out,
-                                                          int T, int C, int KT1, int64_t total) {
+                                                          int T, int C, int64_t ld, int KT1, int64_t total) {
   const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (idx >= total) return;
   const int c = static_cast<int>(idx % C);
@@ -222,14 +223,14 @@ __global__ __launch_bounds__(256) void conv_commit_kernel(const void* cs_in, con
     val = cs_in != nullptr ? IO<DT>::load1(cs_in, (b * KT1 + xi) * C + c) : 0.0f;
   } else {
     const int64_t tok = b * T + (xi - KT1);
-    val = (mask == nullptr || mask[tok] != 0) ? IO<DT>::load1(qkv, tok * C + c) : 0.0f;
+    val = (mask == nullptr || mask[tok] != 0) ? IO<DT>::load1(qkv, tok * ld + c) : 0.0f;
   }
   IO<DT>::store1(cs_out, idx, val);
 }
 
 }  // namespace
 
-extern "C" int gdn_conv_prologue(const void* qkv, int io_dtype, const void* conv_state_in,
+extern "C" int gdn_conv_prologue(const void* qkv, int io_dtype, int64_t qkv_stride, const void* conv_state_in,
                                  const void* weight, int w_dtype, const uint8_t* mask,
                                  const int32_t* cu_seqlens, void* q_out, void* k_out,
                                  void* v_out, void* conv_state_out, int64_t B, int64_t S,
@@ -251,6 +252,9 @@ extern "C" int gdn_conv_prologue(const void* qkv, int io_dtype, const void* conv
   if (conv_state_out != nullptr && conv_state_out == conv_state_in)
     return fail(GDN_ERR_INVALID, "gdn_conv_prologue: conv_state_out must not alias conv_state_in");
   if (!(eps >= 0.0f)) return fail(GDN_ERR_INVALID, "gdn_conv_prologue: eps must be >= 0");
+  if (qkv_stride != 0 && (qkv_stride < 2 * Hk * Dk + Hv * Dv || (qkv_stride * (io_dtype == GDN_DTYPE_F32 ? 4 : 2)) % 16 != 0))
+    return fail(GDN_ERR_INVALID, "gdn_conv_prologue: qkv_stride=%lld must be >= C and keep rows 16-byte aligned",
+                (long long)qkv_stride);
   if (!gdn_host::aligned(qkv, 16) || !gdn_host::aligned(q_out, 16) || !gdn_host::aligned(k_out, 16) ||
       !gdn_host::aligned(v_out, 16) || !gdn_host::aligned(conv_state_in, 16) ||
       !gdn_host::aligned(conv_state_out, 16) || !gdn_host::aligned(weight, 16))
@@ -275,6 +279,7 @@ extern "C" int gdn_conv_prologue(const void* qkv, int io_dtype, const void* conv
   p.Hk = static_cast<int>(Hk);
   p.Hv = static_cast<int>(Hv);
   p.C = static_cast<int>(2 * Hk * Dk + Hv * Dv);
+  p.ld = qkv_stride > 0 ? qkv_stride : p.C;
   p.eps = eps;
 
   // tokens per wavefront: short unpacked rows (decode, verify) take a short run
@@ -330,7 +335,7 @@ extern "C" int gdn_conv_prologue(const void* qkv, int io_dtype, const void* conv
 }
 
 extern "C" int gdn_conv_state_commit(const void* conv_state_in, const void* qkv, int io_dtype,
-                                     const uint8_t* mask, const int32_t* n_commit,
+                                     int64_t qkv_stride, const uint8_t* mask, const int32_t* n_commit,
                                      void* conv_state_out, int64_t B, int64_t T, int64_t C,
                                      int64_t Kt, void* stream) {
   using gdn_host::fail;
@@ -341,6 +346,10 @@ extern "C" int gdn_conv_state_commit(const void* conv_state_in, const void* qkv,
     return fail(GDN_ERR_INVALID, "gdn_conv_state_commit: qkv, n_commit and conv_state_out are required");
   if (conv_state_out == conv_state_in)
     return fail(GDN_ERR_INVALID, "gdn_conv_state_commit: conv_state_out must not alias conv_state_in");
+  if (qkv_stride != 0 && qkv_stride < C)
+    return fail(GDN_ERR_INVALID, "gdn_conv_state_commit: qkv_stride=%lld is below C=%lld", (long long)qkv_stride,
+                (long long)C);
+  const int64_t ld = qkv_stride > 0 ? qkv_stride : C;
   const int64_t total = B * (Kt - 1) * C;
   if (total == 0) return GDN_OK;
   if (T > INT32_MAX || C > INT32_MAX) return fail(GDN_ERR_UNSUPPORTED, "gdn_conv_state_commit: too large");
@@ -352,15 +361,15 @@ extern "C" int gdn_conv_state_commit(const void* conv_state_in, const void* qkv,
   switch (io_dtype) {
     case GDN_DTYPE_BF16:
       hipLaunchKernelGGL((conv_commit_kernel<GDN_DTYPE_BF16>), dim3(blocks), dim3(threads), 0, st,
-                         conv_state_in, qkv, mask, n_commit, conv_state_out, Ti, Ci, K1, total);
+                         conv_state_in, qkv, mask, n_commit, conv_state_out, Ti, Ci, ld, K1, total);
       break;
     case GDN_DTYPE_F16:
       hipLaunchKernelGGL((conv_commit_kernel<GDN_DTYPE_F16>), dim3(blocks), dim3(threads), 0, st,
-                         conv_state_in, qkv, mask, n_commit, conv_state_out, Ti, Ci, K1, total);
+                         conv_state_in, qkv, mask, n_commit, conv_state_out, Ti, Ci, ld, K1, total);
       break;
     default:
       hipLaunchKernelGGL((conv_commit_kernel<GDN_DTYPE_F32>), dim3(blocks), dim3(threads), 0, st,
-                         conv_state_in, qkv, mask, n_commit, conv_state_out, Ti, Ci, K1, total);
+                         conv_state_in, qkv, mask, n_commit, conv_state_out, Ti, Ci, ld, K1, total);
       break;
   }
   return gdn_host::check_launch("gdn_conv_state_commit");

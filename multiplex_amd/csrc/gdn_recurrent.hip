@@ -73,7 +73,7 @@ __device__ __forceinline__ void load_token(const RecParams& p, int64_t tok, int 
   constexpr int NV = DK / kLanesPerRow / 4;
   const uint8_t* mp = p.mask != nullptr ? p.mask + tok : &kActive;
   in.m = *mp;
-  gate_load<GF, DT>(p.ga, tok * p.Hv + hv, in.gx, in.gy);
+  gate_load<GF, DT>(p.ga, tok * p.ga.ld + hv, in.gx, in.gy);
   const int64_t kq = (tok * p.Hk + hk) * DK + sub * 4;
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
@@ -271,7 +271,7 @@ __global__ __launch_bounds__(kTileThreads) void recurrent_tile_kernel(const RecP
     }
     if (tid < kTile) {
       const int64_t tok = c.tok0 + t0 + min(tid, n - 1);
-      gate_load<GF, DT>(p.ga, tok * p.Hv + c.hv, gx, gy);
+      gate_load<GF, DT>(p.ga, tok * p.ga.ld + c.hv, gx, gy);
       const uint8_t* mp = p.mask != nullptr ? p.mask + tok : &kActive;
       mm = *mp;
     }
@@ -405,7 +405,7 @@ __global__ __launch_bounds__(kTileThreads) void verify_wy_kernel(const RecParams
   }
   if (tid < TM) {
     const int64_t tok = c.tok0 + min(tid, T - 1);
-    gate_load<GF, DT>(p.ga, tok * p.Hv + c.hv, gx, gy);
+    gate_load<GF, DT>(p.ga, tok * p.ga.ld + c.hv, gx, gy);
     const uint8_t* mp = p.mask != nullptr ? p.mask + tok : &kActive;
     mm = *mp;
   }
@@ -575,6 +575,9 @@ int run_recurrent(const gdn_recurrent_args* a) {
       !gdn_host::aligned(a->state_in, 16) || !gdn_host::aligned(a->state_out, 16) ||
       !gdn_host::aligned(a->snapshots, 16))
     return fail(GDN_ERR_INVALID, "gdn_recurrent: q/k or state pointers are misaligned");
+  if (a->gate_stride != 0 && a->gate_stride < a->Hv)
+    return fail(GDN_ERR_INVALID, "gdn_recurrent: gate_stride=%lld is below Hv=%lld", (long long)a->gate_stride,
+                (long long)a->Hv);
   if (a->state_index != nullptr && (a->n_slots < 0 || a->n_slots > INT32_MAX))
     return fail(GDN_ERR_INVALID, "gdn_recurrent: n_slots=%lld out of range", (long long)a->n_slots);
   if (a->B == 0) return GDN_OK;
@@ -586,6 +589,7 @@ int run_recurrent(const gdn_recurrent_args* a) {
   p.v = a->v;
   p.ga.gx = a->gx;
   p.ga.gy = a->gy;
+  p.ga.ld = a->gate_stride > 0 ? a->gate_stride : a->Hv;
   p.ga.A_log = a->A_log;
   p.ga.dt_bias = a->dt_bias;
   p.ga.mode = a->gate_mode;

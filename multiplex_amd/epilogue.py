@@ -20,6 +20,28 @@ from .gated_delta import PreparedCall, _dtype_code, _ptr, _require_device, _stre
 __all__ = ["gated_rms_norm", "prepare_gated_rms_norm"]
 
 
+def _gate_lines(gate: torch.Tensor, D: int):
+    """``(gate, gate_group, gate_stride)``: a gate ``[..., G, D]`` whose rows
+    are D contiguous elements, G rows per line, lines one stride apart (a
+    column slice of a fused in_proj output) is read in place; anything else
+    is made contiguous (group 0)."""
+    if gate.is_contiguous() or gate.dim() < 3:
+        return gate.contiguous(), 0, 0
+    G = gate.shape[-2]
+    if gate.stride(-1) != 1 or gate.stride(-2) != D:
+        return gate.contiguous(), 0, 0
+    lead = [i for i in range(gate.dim() - 2) if gate.shape[i] > 1]
+    ld = gate.stride(lead[-1]) if lead else G * D
+    expect = ld
+    for i in reversed(lead):
+        if gate.stride(i) != expect:
+            return gate.contiguous(), 0, 0
+        expect *= gate.shape[i]
+    if ld < G * D or (ld * gate.element_size()) % 16 != 0 or gate.data_ptr() % 16 != 0:
+        return gate.contiguous(), 0, 0
+    return gate, G, ld
+
+
 def _norm_args(x, gate, weight, eps, out):
     dev = _require_device([x, gate, weight, out], ["x", "gate", "weight", "out"])
     if gate.shape != x.shape:
@@ -41,9 +63,9 @@ def _norm_args(x, gate, weight, eps, out):
     elif out.shape != x.shape or out.dtype != x.dtype or not out.is_contiguous():
         raise ValueError("out must be a contiguous tensor of x's shape and dtype")
     x = x.contiguous()
-    gate = gate.contiguous()
+    gate, g_group, g_ld = _gate_lines(gate, D)
     rows = x.numel() // D if D > 0 else 0
-    args = (_ptr(x), _ptr(gate), io, _ptr(weight), wdt, _ptr(out), rows, D, float(eps), _stream(dev))
+    args = (_ptr(x), _ptr(gate), io, g_group, g_ld, _ptr(weight), wdt, _ptr(out), rows, D, float(eps), _stream(dev))
     return args, dict(x=x, gate=gate, weight=weight), out, dev
 
 
@@ -57,7 +79,9 @@ def gated_rms_norm(x: torch.Tensor, gate: torch.Tensor, weight: Optional[torch.T
     (``models/qwen3_next/modeling_qwen3_next.py:57-74``): the normalised value
     is rounded to x's dtype, so is its product with a weight of that dtype,
     and the gate product is rounded once.  ``out`` (same shape and dtype,
-    contiguous) may be x or gate.
+    contiguous) may be x.  The gate may be a column slice of a wider buffer
+    (``[..., G, D]`` rows of D contiguous channels, lines of G rows one stride
+    apart, as a fused in_proj output gives); it is then read in place.
     """
     args, _, out, _ = _norm_args(x, gate, weight, eps, out)
     _lib.call("gdn_gated_rmsnorm", *args)
@@ -68,10 +92,13 @@ def prepare_gated_rms_norm(x: torch.Tensor, gate: torch.Tensor, weight: Optional
                            eps: float = 1e-6, *, out: Optional[torch.Tensor] = None) -> PreparedCall:
     """Validates :func:`gated_rms_norm` once; ``launch()`` re-issues it.
 
-    The tensors are bound by address (x and gate must already be contiguous,
-    so the launch reads the caller's buffers); ``outputs`` is ``(out,)``.
+    The tensors are bound by address (x contiguous; the gate contiguous or
+    lines of rows as :func:`gated_rms_norm` accepts), so the launch reads the
+    caller's buffers; ``outputs`` is ``(out,)``.
     """
-    if not (x.is_contiguous() and gate.is_contiguous()):
-        raise ValueError("prepare_gated_rms_norm binds x and gate by address: pass contiguous tensors")
+    if not x.is_contiguous():
+        raise ValueError("prepare_gated_rms_norm binds x by address: pass a contiguous x")
     args, keep, out, dev = _norm_args(x, gate, weight, eps, out)
+    if keep["gate"].data_ptr() != gate.data_ptr():
+        raise ValueError("prepare_gated_rms_norm binds the gate by address: pass it contiguous or as lines of rows")
     return PreparedCall("gdn_gated_rmsnorm", args, keep, (out,), dev)

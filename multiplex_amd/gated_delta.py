@@ -86,6 +86,30 @@ def _contig(t: Optional[torch.Tensor]) -> Optional[torch.Tensor]:
     return None if t is None else t.contiguous()
 
 
+def _token_rows(t: torch.Tensor, width: int):
+    """Token stride (elements) of a ``[B, T, width]`` tensor whose rows are
+    ``width`` contiguous elements with one stride from token to token (a
+    column slice of a wider row-major buffer), or None if it is laid out
+    otherwise."""
+    if t.dim() != 3 or t.shape[2] != width or (width > 1 and t.stride(2) != 1):
+        return None
+    B, T = t.shape[0], t.shape[1]
+    ld = t.stride(1) if T > 1 else (t.stride(0) if B > 1 else width)
+    if ld < width or (B > 1 and T > 1 and t.stride(0) != T * ld):
+        return None
+    return int(ld)
+
+
+def _gate_pair(gx: torch.Tensor, gy: torch.Tensor, Hv: int):
+    """``(gx, gy, gate_stride)``: the gates as given when both are column
+    slices with one token stride (e.g. of a fused in_proj output), else
+    contiguous copies and stride 0."""
+    lx, ly = _token_rows(gx, Hv), _token_rows(gy, Hv)
+    if lx is not None and lx == ly:
+        return gx, gy, (0 if lx == Hv else lx)
+    return gx.contiguous(), gy.contiguous(), 0
+
+
 def _stream(dev: torch.device) -> int:
     return torch.cuda.current_stream(dev).cuda_stream
 
@@ -277,7 +301,8 @@ def _recurrent(q, k, v, gx, gy, gate_mode, A_log, dt_bias, state, mask, *,
     dev = _require_device([q, k, v, gx, gy, A_log, dt_bias, state, mask, state_out], names)
     packed = cu_seqlens is not None
     sh = _Shapes(q, k, v, gx, gy, packed)
-    q, k, v, gx, gy = (_contig(t) for t in (q, k, v, gx, gy))
+    q, k, v = (_contig(t) for t in (q, k, v))
+    gx, gy, g_ld = _gate_pair(gx, gy, sh.Hv)
     qkv_code = _dtype_code(k, "q/k/v")
     gate_code = _gate_codes(gx, gy)
     if gate_mode == _lib.GATES_RAW:
@@ -302,7 +327,7 @@ def _recurrent(q, k, v, gx, gy, gate_mode, A_log, dt_bias, state, mask, *,
         A_log=_ptr(A_log), dt_bias=_ptr(dt_bias), state_in=_ptr(state),
         state_out=_ptr(out_state), snapshots=_ptr(snaps), y=_ptr(y_t), mask=_ptr(mask_u8),
         cu_seqlens=_ptr(cu), commit_len=_ptr(commit), state_index=_ptr(idx), B=n_rows, T=sh.T, Hk=sh.Hk,
-        Hv=sh.Hv, Dk=sh.Dk, Dv=sh.Dv, n_slots=n_slots, stream=_stream(dev),
+        Hv=sh.Hv, Dk=sh.Dk, Dv=sh.Dv, n_slots=n_slots, gate_stride=g_ld, stream=_stream(dev),
     )
     with torch.cuda.device(dev):
         _lib.call("gdn_recurrent", _lib.ctypes.byref(args))
@@ -343,9 +368,12 @@ def prepare_recurrent(q, k, v, a, b, A_log, dt_bias, state, mask=None, *, y=True
     dev = _require_device([q, k, v, a, b, A_log, dt_bias, state, mask, state_out], names)
     packed = cu_seqlens is not None
     sh = _Shapes(q, k, v, a, b, packed)
-    for t, n in ((q, "q"), (k, "k"), (v, "v"), (a, "a"), (b, "b")):
+    for t, n in ((q, "q"), (k, "k"), (v, "v")):
         if t is not None and not t.is_contiguous():
             raise ValueError(f"{n} must be contiguous for a prepared launch")
+    a_g, b_g, g_ld = _gate_pair(a, b, sh.Hv)
+    if a_g is not a or b_g is not b:
+        raise ValueError("a and b must be contiguous, or column slices with one token stride, for a prepared launch")
     qkv_code = _dtype_code(k, "q/k/v")
     gate_code = _gate_codes(a, b)
     param_code = _param_codes(A_log, dt_bias, sh.Hv) if mode == _lib.GATES_RAW else _lib.DTYPE_F32
@@ -367,7 +395,7 @@ def prepare_recurrent(q, k, v, a, b, A_log, dt_bias, state, mask=None, *, y=True
         dt_bias=_ptr(dt_bias) if mode == _lib.GATES_RAW else None, state_in=_ptr(state),
         state_out=_ptr(out_state), snapshots=_ptr(snaps), y=_ptr(y_t), mask=_ptr(mask_u8),
         cu_seqlens=_ptr(cu), commit_len=_ptr(commit), state_index=_ptr(idx), B=n_rows, T=sh.T, Hk=sh.Hk,
-        Hv=sh.Hv, Dk=sh.Dk, Dv=sh.Dv, n_slots=n_slots, stream=_stream(dev),
+        Hv=sh.Hv, Dk=sh.Dk, Dv=sh.Dv, n_slots=n_slots, gate_stride=g_ld, stream=_stream(dev),
     )
     keep = dict(q=q, k=k, v=v, a=a, b=b, A_log=A_log, dt_bias=dt_bias, state=state, mask=mask_u8,
                 cu=cu, commit=commit, y=y_t, state_out=out_state, snapshots=snaps, state_index=idx)
@@ -407,7 +435,8 @@ def _chunk_args(q, k, v, gx, gy, gate_mode, A_log, dt_bias, state, *, cu_seqlens
     dev = _require_device([q, k, v, gx, gy, A_log, dt_bias, state, state_out], names)
     packed = cu_seqlens is not None
     sh = _Shapes(q, k, v, gx, gy, packed)
-    q, k, v, gx, gy = (_contig(t) for t in (q, k, v, gx, gy))
+    q, k, v = (_contig(t) for t in (q, k, v))
+    gx, gy, g_ld = _gate_pair(gx, gy, sh.Hv)
     qkv_code = _dtype_code(k, "q/k/v")
     gate_code = _gate_codes(gx, gy)
     if gate_mode == _lib.GATES_RAW:
@@ -424,7 +453,7 @@ def _chunk_args(q, k, v, gx, gy, gate_mode, A_log, dt_bias, state, *, cu_seqlens
     ws_bytes = chunk_workspace_bytes(n_seqs, n_tok, sh.Hv, sh.Dk, sh.Dv, CHUNK)
     if workspace is None or workspace.numel() * workspace.element_size() < ws_bytes:
         workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
-    args = (_ptr(q), _ptr(k), _ptr(v), qkv_code, gate_mode, _ptr(gx), _ptr(gy), gate_code, _ptr(A_log),
+    args = (_ptr(q), _ptr(k), _ptr(v), qkv_code, gate_mode, _ptr(gx), _ptr(gy), gate_code, g_ld, _ptr(A_log),
             _ptr(dt_bias), param_code, _ptr(state), _ptr(y_t), _ptr(out_state), _ptr(idx), n_slots, _ptr(cu),
             n_seqs, n_tok, sh.Hk, sh.Hv, sh.Dk, sh.Dv, CHUNK, _ptr(workspace), ws_bytes, _stream(dev))
     keep = dict(q=q, k=k, v=v, gx=gx, gy=gy, A_log=A_log, dt_bias=dt_bias, state=state, cu=cu,
@@ -456,7 +485,7 @@ def prepare_chunked(q, k, v, a, b, A_log, dt_bias, state=None, *, cu_seqlens=Non
                                                   workspace=workspace, state_index=state_index)
     for name in ("q", "k", "v", "gx", "gy"):
         if keep[name].data_ptr() != {"q": q, "k": k, "v": v, "gx": a, "gy": b}[name].data_ptr():
-            raise ValueError(f"{name} must be contiguous for a prepared launch")
+            raise ValueError(f"{name} must be contiguous (gates: or one-stride column slices) for a prepared launch")
     keep.update(y=y_t, state_out=out_state)
     return PreparedCall("gdn_chunk_fwd", args, keep, (y_t, out_state), dev)
 

@@ -10,7 +10,8 @@ array, or a :class:`~multiplex_amd.state_pool.PooledBatch` whose slots the
 kernels update in place.
 
 Data path per call:
-  in_proj_qkv / z / b / a      library GEMMs (hipBLASLt through torch)
+  in_proj_qkv / z / b / a      one library GEMM (hipBLASLt through torch); the
+                               kernels below read its column slices in place
   gdn_conv_prologue            fused conv1d + SiLU + q/k norm (HIP)
   gated_delta_update           recurrent or chunked kernel (HIP)
   gated_rms_norm               fused gated RMSNorm (HIP)
@@ -75,6 +76,17 @@ class GatedDeltaNet(torch.nn.Module):
         self.in_proj_z = torch.nn.Linear(hidden_size, self.value_dim, bias=False, **kw)
         self.in_proj_b = torch.nn.Linear(hidden_size, num_v_heads, bias=False, **kw)
         self.in_proj_a = torch.nn.Linear(hidden_size, num_v_heads, bias=False, **kw)
+        # The four in_proj weights live in one [conv_dim + value_dim + 2 Hv,
+        # hidden] buffer (qkv | z | b | a), each module's weight a row slice
+        # of it, so the projections run as one GEMM whose output the
+        # prologue, the GDN kernel and the norm read in place as column
+        # slices.  The parameter names stay the reference's.
+        self._splits = (self.conv_dim, self.conv_dim + self.value_dim, self.conv_dim + self.value_dim + num_v_heads)
+        fused = torch.empty(self._splits[2] + num_v_heads, hidden_size, **kw)
+        bounds = (0,) + self._splits + (fused.shape[0],)
+        for lin, lo, hi in zip(self._in_projs(), bounds[:-1], bounds[1:]):
+            lin.weight = torch.nn.Parameter(fused[lo:hi])
+        self._in_proj_fused = fused
         self.conv1d_weight = torch.nn.Parameter(torch.empty(self.conv_dim, conv_kernel_size, **kw))
         self.A_log = torch.nn.Parameter(torch.empty(num_v_heads, dtype=torch.float32, device=device))
         self.dt_bias = torch.nn.Parameter(torch.empty(num_v_heads, dtype=torch.float32, device=device))
@@ -94,13 +106,51 @@ class GatedDeltaNet(torch.nn.Module):
         self.dt_bias.copy_(torch.rand(self.num_v_heads, generator=generator) * 2 - 1)
         self.norm_weight.fill_(1.0)
 
+    def _in_projs(self):
+        return (self.in_proj_qkv, self.in_proj_z, self.in_proj_b, self.in_proj_a)
+
+    def _apply(self, fn, *args, **kwargs):
+        # .to() / .cuda() move each parameter on its own: stack the in_proj
+        # weights into one buffer again afterwards
+        out = super()._apply(fn, *args, **kwargs)
+        with torch.no_grad():
+            fused = torch.cat([lin.weight for lin in self._in_projs()], dim=0)
+            bounds = (0,) + self._splits + (fused.shape[0],)
+            for lin, lo, hi in zip(self._in_projs(), bounds[:-1], bounds[1:]):
+                lin.weight = torch.nn.Parameter(fused[lo:hi], requires_grad=lin.weight.requires_grad)
+        self._in_proj_fused = fused
+        return out
+
+    def _fused_in_proj_weight(self) -> torch.Tensor:
+        """The stacked in_proj weight; rebuilt (a copy) if a module's weight
+        was replaced by a tensor outside the shared buffer."""
+        f = self._in_proj_fused
+        row = f.stride(0) * f.element_size()
+        bounds = (0,) + self._splits
+        if all(lin.weight.data_ptr() == f.data_ptr() + lo * row for lin, lo in zip(self._in_projs(), bounds)):
+            return f
+        return torch.cat([lin.weight for lin in self._in_projs()], dim=0)
+
     def _project(self, inputs):
+        """in_proj_qkv / z / b / a as column slices of fused GEMM outputs.
+
+        Up to 256 tokens the GEMM reads the weights once and is bound by
+        that: one launch for all four.  Beyond, the library's tiling favours
+        [qkv | z] (a multiple of 256 columns) and [b | a] as two GEMMs.
+        """
         B, S, _ = inputs.shape
-        qkv = self.in_proj_qkv(inputs)
-        z = self.in_proj_z(inputs).reshape(B, S, self.num_v_heads, self.head_v_dim)
-        b = self.in_proj_b(inputs)
-        a = self.in_proj_a(inputs)
-        return qkv, z, a, b
+        w = self._fused_in_proj_weight()
+        c1, c2, c3 = self._splits
+        if B * S <= 256:
+            out = torch.nn.functional.linear(inputs, w)
+            qkv, z, ba = out[..., :c1], out[..., c1:c2], out[..., c2:]
+        else:
+            out = torch.nn.functional.linear(inputs, w[:c2])
+            ba = torch.nn.functional.linear(inputs, w[c2:])
+            qkv, z = out[..., :c1], out[..., c1:]
+        z = z.unflatten(-1, (self.num_v_heads, self.head_v_dim))
+        hv = self.num_v_heads
+        return qkv, z, ba[..., hv:], ba[..., :hv]
 
     def _epilogue(self, y, z):
         B, S = y.shape[:2]

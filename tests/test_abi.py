@@ -37,14 +37,15 @@ def test_exports_match_header(lib):
 
 
 def test_abi_version(lib):
-    assert lib.gdn_abi_version() == _lib.GDN_ABI_VERSION == 2
+    assert lib.gdn_abi_version() == _lib.GDN_ABI_VERSION == 3
 
 
 def test_struct_layout_matches_header():
-    # gdn_recurrent_args: 27 fields; pointers 8 B, int32 fields packed in pairs.
-    assert ctypes.sizeof(_lib.RecurrentArgs) == 8 * 3 + 4 * 2 + 8 * 2 + 4 * 2 + 8 * 10 + 8 * 6 + 8 + 8
+    # gdn_recurrent_args: 28 fields; pointers 8 B, int32 fields packed in pairs.
+    assert ctypes.sizeof(_lib.RecurrentArgs) == 8 * 3 + 4 * 2 + 8 * 2 + 4 * 2 + 8 * 10 + 8 * 6 + 8 + 8 + 8
     assert _lib.RecurrentArgs.state_index.offset == _lib.RecurrentArgs.commit_len.offset + 8
     assert _lib.RecurrentArgs.n_slots.offset == _lib.RecurrentArgs.Dv.offset + 8
+    assert _lib.RecurrentArgs.gate_stride.offset == _lib.RecurrentArgs.n_slots.offset + 8
 
 
 def _update(lib, **kw):
@@ -92,11 +93,11 @@ def test_recurrent_null_args(lib):
 
 def test_prologue_rejects_bad_arguments(lib):
     def call(**kw):
-        args = dict(qkv=FAKE, io=_lib.DTYPE_BF16, cs=None, w=FAKE, wdt=_lib.DTYPE_BF16, mask=None,
+        args = dict(qkv=FAKE, io=_lib.DTYPE_BF16, ld=0, cs=None, w=FAKE, wdt=_lib.DTYPE_BF16, mask=None,
                     cu=None, q=FAKE, k=FAKE, v=FAKE, cso=FAKE, B=1, S=4, Hk=16, Hv=32, Dk=128, Dv=128,
                     Kt=4, eps=1e-6)
         args.update(kw)
-        return lib.gdn_conv_prologue(args["qkv"], args["io"], args["cs"], args["w"], args["wdt"], args["mask"],
+        return lib.gdn_conv_prologue(args["qkv"], args["io"], args["ld"], args["cs"], args["w"], args["wdt"], args["mask"],
                                      args["cu"], args["q"], args["k"], args["v"], args["cso"], args["B"],
                                      args["S"], args["Hk"], args["Hv"], args["Dk"], args["Dv"], args["Kt"],
                                      args["eps"], None)
@@ -107,19 +108,22 @@ def test_prologue_rejects_bad_arguments(lib):
     assert call(q=None) == _lib.ERR_INVALID
     assert call(eps=-1.0) == _lib.ERR_INVALID
     assert call(B=0) == _lib.OK
+    assert call(ld=100) == _lib.ERR_INVALID        # below C
+    assert call(ld=8192 + 4) == _lib.ERR_INVALID   # rows not 16-byte aligned
 
 
 def test_conv_commit_rejects_bad_arguments(lib):
-    assert lib.gdn_conv_state_commit(FAKE, FAKE, _lib.DTYPE_BF16, None, None, FAKE, 2, 4, 8192, 4, None) == _lib.ERR_INVALID
-    assert lib.gdn_conv_state_commit(FAKE, FAKE, _lib.DTYPE_BF16, None, FAKE, FAKE, 2, 4, 8192, 1, None) == _lib.ERR_INVALID
-    assert lib.gdn_conv_state_commit(FAKE, FAKE, _lib.DTYPE_BF16, None, FAKE, 2 * FAKE, 0, 4, 8192, 4, None) == _lib.OK
-    assert lib.gdn_conv_state_commit(FAKE, FAKE, _lib.DTYPE_BF16, None, FAKE, FAKE, 2, 4, 8192, 4, None) == _lib.ERR_INVALID
+    assert lib.gdn_conv_state_commit(FAKE, FAKE, _lib.DTYPE_BF16, 0, None, None, FAKE, 2, 4, 8192, 4, None) == _lib.ERR_INVALID
+    assert lib.gdn_conv_state_commit(FAKE, FAKE, _lib.DTYPE_BF16, 0, None, FAKE, FAKE, 2, 4, 8192, 1, None) == _lib.ERR_INVALID
+    assert lib.gdn_conv_state_commit(FAKE, FAKE, _lib.DTYPE_BF16, 0, None, FAKE, 2 * FAKE, 0, 4, 8192, 4, None) == _lib.OK
+    assert lib.gdn_conv_state_commit(FAKE, FAKE, _lib.DTYPE_BF16, 0, None, FAKE, FAKE, 2, 4, 8192, 4, None) == _lib.ERR_INVALID
+    assert lib.gdn_conv_state_commit(FAKE, FAKE, _lib.DTYPE_BF16, 100, None, FAKE, 2 * FAKE, 2, 4, 8192, 4, None) == _lib.ERR_INVALID
 
 
 def test_chunk_rejects_bad_arguments(lib):
     def call(**kw):
         args = dict(q=FAKE, k=FAKE, v=FAKE, qkv=_lib.DTYPE_BF16, mode=_lib.GATES_RAW, gx=FAKE, gy=FAKE,
-                    gdt=_lib.DTYPE_BF16, A_log=FAKE, dt_bias=FAKE, pdt=_lib.DTYPE_F32, s_in=None, y=FAKE,
+                    gdt=_lib.DTYPE_BF16, g_ld=0, A_log=FAKE, dt_bias=FAKE, pdt=_lib.DTYPE_F32, s_in=None, y=FAKE,
                     s_out=FAKE, index=None, n_slots=0, cu=None, n_seqs=1, n_tok=4096, Hk=16, Hv=32, Dk=128, Dv=128, chunk=64,
                     ws=FAKE, ws_bytes=1 << 40)
         args.update(kw)
@@ -133,6 +137,7 @@ def test_chunk_rejects_bad_arguments(lib):
     assert call(n_seqs=2, n_tok=4095) == _lib.ERR_INVALID  # not n_seqs rows of equal length
     assert call(n_seqs=0, n_tok=0) == _lib.OK
     assert call(index=FAKE, n_slots=-1) == _lib.ERR_INVALID
+    assert call(g_ld=16) == _lib.ERR_INVALID       # below Hv
 
 
 def test_recurrent_rejects_bad_pool_size(lib):
