@@ -363,16 +363,17 @@ __global__ __launch_bounds__(kTileThreads) void recurrent_tile_kernel(const RecP
 // masked token has g = 1, beta = 0 and y = 0.
 constexpr int kVerifyMaxT = 8;
 
-template <int DK, int DT, int GF>
+// TM: tokens the kernel is built for (4 or kVerifyMaxT), T <= TM at run time.
+template <int DK, int DT, int GF, int TM>
 __global__ __launch_bounds__(kTileThreads) void verify_wy_kernel(const RecParams p) {
   constexpr int EPL = DK / kLanesPerRow;
   constexpr int NV = EPL / 4;
-  constexpr int TM = kVerifyMaxT;
+  static_assert(TM * kTileRows <= kTileThreads, "one v value per thread");
   const RowCtx c = row_ctx<DK>(p);
   if (c.skip) return;  // uniform: a workgroup serves one row, before any barrier
   const int tid = threadIdx.x;
   const int dv0 = blockIdx.x * kTileRows;
-  const int T = c.L;  // 1 <= T <= kVerifyMaxT on this path
+  const int T = c.L;  // 1 <= T <= TM on this path
 
   __shared__ __align__(16) float Ks[TM][DK];
   __shared__ __align__(16) float Qs[TM][DK];
@@ -399,7 +400,7 @@ __global__ __launch_bounds__(kTileThreads) void verify_wy_kernel(const RecParams
   float vr = 0.0f, gx = 0.0f, gy = 0.0f;
   uint8_t mm = 1;
   {
-    const int j = tid / kTileRows, r = tid % kTileRows;  // TM * kTileRows == kTileThreads
+    const int j = min(tid / kTileRows, TM - 1), r = tid % kTileRows;
     const int64_t tok = c.tok0 + min(j, T - 1);
     vr = IO<DT>::load1(p.v, (tok * p.Hv + c.hv) * p.Dv + min(dv0 + r, p.Dv - 1));
   }
@@ -420,7 +421,7 @@ __global__ __launch_bounds__(kTileThreads) void verify_wy_kernel(const RecParams
       *reinterpret_cast<f32x4*>(&Qs[j][e]) = qr[it.value];
     }
   });
-  Vs[tid / kTileRows][tid % kTileRows] = vr;
+  if (tid < TM * kTileRows) Vs[tid / kTileRows][tid % kTileRows] = vr;
   if (tid < TM) {
     float g, beta;
     gate_transform<GF>(p.ga.mode, gx, gy, ea, db, g, beta);
@@ -513,7 +514,9 @@ enum KernelKind { K_DECODE = 0, K_TILE = 1, K_VERIFY = 2 };
 
 template <int DK, int DT, int GF>
 int launch_pf(int kind, dim3 grid, dim3 block, hipStream_t st, const RecParams& p) {
-  if (kind == K_VERIFY) hipLaunchKernelGGL((verify_wy_kernel<DK, DT, GF>), grid, block, 0, st, p);
+  if (kind == K_VERIFY && p.T <= 4) hipLaunchKernelGGL((verify_wy_kernel<DK, DT, GF, 4>), grid, block, 0, st, p);
+  else if (kind == K_VERIFY)
+    hipLaunchKernelGGL((verify_wy_kernel<DK, DT, GF, kVerifyMaxT>), grid, block, 0, st, p);
   else if (kind == K_TILE) hipLaunchKernelGGL((recurrent_tile_kernel<DK, DT, GF>), grid, block, 0, st, p);
   else hipLaunchKernelGGL((recurrent_kernel<DK, DT, GF>), grid, block, 0, st, p);
   return gdn_host::check_launch("gdn_recurrent");
