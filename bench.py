@@ -451,10 +451,35 @@ def cpu_baseline(torch, budget_s=12.0):
     q, k, v, _ = ops_path.conv_prologue(qkv, w, Hk, Hv, Dk, Dv, torch.zeros(1, KT - 1, C_DIM))
     ops_path.gated_delta_update(q, k, v, a, b, A_log, dt_bias, torch.zeros(1, Hv, Dv, Dk))
     tp = time.perf_counter() - t1
+    # decode B=1: median of 20 steps
+    gen = torch.Generator().manual_seed(1000)
+    d1 = draw(gen, 1, 1, torch, "cpu")
+    S1, times = d1["state"].float(), []
+    for _ in range(20):
+        t2 = time.perf_counter()
+        _, S1 = ops_path.gated_delta_update(d1["q"], d1["k"], d1["v"], d1["a"], d1["b"], d1["A_log"], d1["dt_bias"], S1)
+        times.append(time.perf_counter() - t2)
+    t_b1 = sorted(times)[len(times) // 2]
+    # MTP verify B=32, T=4, then the reference's rollback: restore the
+    # snapshot and replay each row's accepted prefix (engine.py:337-359)
+    gen = torch.Generator().manual_seed(1002)
+    dv = draw(gen, 32, 4, torch, "cpu")
+    n_b = torch.randint(1, 5, (32,), generator=gen)
+    t3 = time.perf_counter()
+    S0 = dv["state"].float().clone()
+    ops_path.gated_delta_update(dv["q"], dv["k"], dv["v"], dv["a"], dv["b"], dv["A_log"], dv["dt_bias"], S0)
+    for n in sorted(set(n_b.tolist())):
+        rows = (n_b == n).nonzero().flatten()
+        sl = lambda t: t[rows][:, :n]
+        ops_path.gated_delta_update(sl(dv["q"]), sl(dv["k"]), sl(dv["v"]), sl(dv["a"]), sl(dv["b"]), dv["A_log"],
+                                    dv["dt_bias"], S0[rows])
+    t_ver = time.perf_counter() - t3
     return dict(value=decode_bytes(64) / dt / 1e9, unit="GB/s", cores=threads, kind="port",
                 sample=f"{done} decode steps at B=64 (ops-path port, fp32, torch CPU), "
-                       f"{dt * 1e3:.1f} ms/step; prefill 512 tokens with conv prologue: {T / tp:.0f} tokens/s",
-                ms_per_step=dt * 1e3, prefill_tokens_per_s=T / tp,
+                       f"{dt * 1e3:.1f} ms/step; prefill 512 tokens with conv prologue: {T / tp:.0f} tokens/s; "
+                       f"decode B=1 {t_b1 * 1e6:.0f} us/step; verify B=32 T=4 + replay rollback {t_ver * 1e3:.1f} ms; "
+                       f"host {platform.processor() or platform.machine()}, {os.cpu_count()} logical cpus",
+                ms_per_step=dt * 1e3, prefill_tokens_per_s=T / tp, decode_b1_us=t_b1 * 1e6, verify_ms=t_ver * 1e3,
                 cpu=platform.processor() or platform.machine())
 
 
@@ -588,6 +613,11 @@ def main():
         "prefill": None,
         "configs": configs,
     }
+    if base is not None:
+        if "decode_b1" in configs:
+            configs["decode_b1"]["cpu_us_per_step"] = round(base["decode_b1_us"], 1)
+        if "verify_b32_t4" in configs:
+            configs["verify_b32_t4"]["cpu_ms_verify_plus_rollback"] = round(base["verify_ms"], 2)
     if "prefill_t4096" in configs:
         p = configs["prefill_t4096"]
         line["prefill"] = {"tokens_per_s": round(p["tokens_per_s"], 1), "ms": round(p["ms_total"], 4),
