@@ -157,7 +157,17 @@ def bench_decode_b1(torch, mx, dev, timer, iters=200):
         plan.launch()
     total = timer.total_ms(lambda i: plan.launch(), iters)
     per, med = timer.per_launch_ms(lambda i: plan.launch(), iters)
-    return dict(us_per_step=1e3 * total / iters, kernel_us=1e3 * per, bytes=decode_bytes(1))
+    # the same steps captured in one HIP graph: device time per step without
+    # the host's per-launch cost
+    graph, n = torch.cuda.CUDAGraph(), 50
+    with torch.cuda.graph(graph):
+        cap = torch.cuda.current_stream(dev)
+        for _ in range(n):
+            plan.launch(cap)
+    graph.replay()
+    t_graph = timer.total_ms(lambda i: graph.replay(), 4) / (4 * n)
+    return dict(us_per_step=1e3 * total / iters, kernel_us=1e3 * per, us_per_step_graph=1e3 * t_graph,
+                bytes=decode_bytes(1))
 
 
 def bench_verify(torch, mx, dev, timer, iters=50):

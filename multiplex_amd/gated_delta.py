@@ -113,6 +113,11 @@ def _gate_pair(gx: torch.Tensor, gy: torch.Tensor, Hv: int):
     return gx.contiguous(), gy.contiguous(), 0
 
 
+def _stream_handle(stream) -> int:
+    """A ``torch.cuda.Stream`` or a raw ``hipStream_t`` value."""
+    return stream.cuda_stream if hasattr(stream, "cuda_stream") else int(stream)
+
+
 def _stream(dev: torch.device) -> int:
     return torch.cuda.current_stream(dev).cuda_stream
 
@@ -343,7 +348,9 @@ class PreparedRecurrent:
     Holds the argument block and keeps every tensor it points to alive.  Each
     ``launch()`` enqueues the same kernel on the stream current at
     ``prepare`` time (the same work a serving loop repeats every step, e.g.
-    decode with ``state_out=state``).  Safe to capture in a HIP graph.
+    decode with ``state_out=state``), or on ``stream`` when one is given --
+    e.g. ``torch.cuda.current_stream()`` inside a ``torch.cuda.graph``
+    capture.
     """
 
     def __init__(self, args, keep, dev):
@@ -352,8 +359,12 @@ class PreparedRecurrent:
         self.device = dev
         self._lib = _lib.load()
 
-    def launch(self):
-        st = self._lib.gdn_recurrent(_lib.ctypes.byref(self._args))
+    def launch(self, stream=None):
+        args = self._args
+        if stream is not None:
+            args = _lib.RecurrentArgs.from_buffer_copy(self._args)
+            args.stream = _stream_handle(stream)
+        st = self._lib.gdn_recurrent(_lib.ctypes.byref(args))
         if st != _lib.OK:
             _lib.check("gdn_recurrent", st)
 
@@ -414,8 +425,8 @@ class PreparedCall:
 
     Holds the argument tuple and keeps every tensor it points to alive; each
     ``launch()`` enqueues the same work on the stream current at ``prepare``
-    time (what a serving loop repeats every step).  ``outputs`` are the
-    tensors the call writes.
+    time (what a serving loop repeats every step), or on ``stream`` when one
+    is given.  ``outputs`` are the tensors the call writes.
     """
 
     def __init__(self, fn: str, args: tuple, keep: dict, outputs: tuple, dev):
@@ -426,8 +437,9 @@ class PreparedCall:
         self.device = dev
         self._fn = getattr(_lib.load(), fn)
 
-    def launch(self):
-        st = self._fn(*self._args)
+    def launch(self, stream=None):
+        args = self._args if stream is None else self._args[:-1] + (_stream_handle(stream),)
+        st = self._fn(*args)
         if st != _lib.OK:
             _lib.check(self._fn_name, st)
 

@@ -70,3 +70,35 @@ def test_decode_step_graph_replays_match_eager():
         cs.copy_(cs_new_g)
         ref_cs = cs_e
         torch.cuda.synchronize()
+
+
+@torch.no_grad()
+def test_prepared_launches_replay_in_a_graph():
+    """Prepared launches (validated once) captured with ``launch(stream)``:
+    50 decode steps in one graph equal 50 eager launches."""
+    g = torch.Generator().manual_seed(43)
+    q = torch.nn.functional.normalize(torch.randn(B, 1, Hk, D, generator=g), dim=-1).to(torch.bfloat16).to(DEV)
+    k = torch.nn.functional.normalize(torch.randn(B, 1, Hk, D, generator=g), dim=-1).to(torch.bfloat16).to(DEV)
+    v = torch.randn(B, 1, Hv, D, generator=g).to(torch.bfloat16).to(DEV)
+    a = torch.randn(B, 1, Hv, generator=g).to(torch.bfloat16).to(DEV)
+    b = torch.randn(B, 1, Hv, generator=g).to(torch.bfloat16).to(DEV)
+    A_log = (torch.rand(Hv, generator=g) * 2.7).to(DEV)
+    dt_bias = (torch.rand(Hv, generator=g) * 2 - 1).to(DEV)
+    state = (torch.randn(B, Hv, D, D, generator=g) * 0.02).to(DEV)
+    ref = state.clone()
+    plan = mx.prepare_recurrent(q, k, v, a, b, A_log, dt_bias, state, state_out=state)
+    eager = mx.prepare_recurrent(q, k, v, a, b, A_log, dt_bias, ref, state_out=ref)
+    graph, n = torch.cuda.CUDAGraph(), 50
+    with torch.cuda.graph(graph):
+        cap = torch.cuda.current_stream()
+        for _ in range(n):
+            plan.launch(cap)
+    assert torch.equal(state, ref)
+    for r in range(3):
+        for _ in range(n):
+            eager.launch()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(state, ref), f"replay {r}"
+        assert torch.equal(plan.outputs[0], eager.outputs[0]), f"replay {r}: y"
