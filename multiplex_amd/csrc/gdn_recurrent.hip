@@ -510,7 +510,213 @@ __global__ __launch_bounds__(kTileThreads) void verify_wy_kernel(const RecParams
   });
 }
 
+// Verify on MFMA (Dk = 128, bf16 q/k).  The 2T dot products of a state row
+// (a_t = S k_t, b_t = S q_t) are one matrix product per 16-row wave tile,
+// D = A S^T, with A = [k_0 .. k_{TM-1}; q_0 .. q_{TM-1}] (bf16, exact) and the
+// fp32 state split as hi + lo bf16 (two passes, ~2^-16 relative per
+// product, fp32 accumulation).
+//
+// Lane (r, g) of a wave (r = lane % 16, g = lane / 16) holds state row
+// dv0 + 16 w + r at columns 32 s + 4 g .. +3 and 32 s + 16 + 4 g .. +3
+// (s < 4), so one load instruction covers 64 contiguous bytes of 16 rows.
+// Those 8 columns are the lane's 8 k-slots of the MFMA B operand for
+// k-step s; A is read from LDS in the same column order.  D[m][r] lands in
+// lane (r, m / 4): with TM = 4 lanes g = 0 / 1 hold a_0..3 / b_0..3 of row
+// r (TM = 8: a in g = 0, 1 and b in g = 2, 3).  The coefficients k_s . k_t
+// and k_s . q_t come from the product A K^T (4 MFMAs per wave).
+constexpr int kVmRows = 64;  // state rows per workgroup, 16 per wave
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ f32x4 mfma_bf16(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// hi = bf16(x) and lo = bf16(x - hi) of 8 floats, as MFMA operands (element
+// e of the result is x[e]).  The residual takes hi back from the packed pair.
+__device__ __forceinline__ void split8(const f32x4& x0, const f32x4& x1, bf16x8& hi, bf16x8& lo) {
+  const uint32_t h[4] = {pk_bf16(x0.x, x0.y), pk_bf16(x0.z, x0.w), pk_bf16(x1.x, x1.y), pk_bf16(x1.z, x1.w)};
+  const float v[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+  uint32_t l[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const float r0 = v[2 * k] - __builtin_bit_cast(float, h[k] << 16);
+    const float r1 = v[2 * k + 1] - __builtin_bit_cast(float, h[k] & 0xffff0000u);
+    l[k] = pk_bf16(r0, r1);
+  }
+  hi = __builtin_bit_cast(bf16x8, u32x4{h[0], h[1], h[2], h[3]});
+  lo = __builtin_bit_cast(bf16x8, u32x4{l[0], l[1], l[2], l[3]});
+}
+
+template <int GF, int TM>
+__global__ __launch_bounds__(256) void verify_mfma_kernel(const RecParams p) {
+  constexpr int DK = 128;
+  constexpr int DT = GDN_DTYPE_BF16;
+  constexpr int KP = DK + 8;  // padded LDS row (bf16)
+  static_assert(2 * TM <= 16, "the k and q rows fill at most one 16-row MFMA tile");
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int lr = lane & 15, lg = lane >> 4;
+  const int hv = blockIdx.y, row = blockIdx.z, hk = hv / p.group;
+  const int dv0 = blockIdx.x * kVmRows;
+  int slot = row;
+  if (p.state_index != nullptr) {
+    slot = p.state_index[row];
+    if (slot < 0 || slot >= p.n_slots) return;  // uniform, before any barrier
+  }
+  const int T = p.T;  // 1 <= T <= TM on this path
+  const int64_t tok0 = static_cast<int64_t>(row) * T;
+
+  __shared__ __align__(16) uint16_t KQ[16][KP];  // k_0..k_{TM-1}, q_0..q_{TM-1}, then zero rows
+  __shared__ float Vs[TM][kVmRows];
+  __shared__ float Gs[TM], Bs[TM];  // g_t, beta_t (1 and 0 when masked)
+  __shared__ uint8_t Ms[TM];
+  __shared__ float Cf[4][2][TM][TM];  // per wave: r(t,s) k_s.k_t (s < t), r(t,s) k_s.q_t (s <= t)
+
+  float ea, db;
+  param_load<GF, DT>(p.ga, hv, ea, db);
+
+  // token loads first (memory returns in issue order), then the state rows
+  u32x4 kq;
+  {
+    const int m = tid >> 4, e = (tid & 15) * 8;  // 16 bytes a thread, row m
+    const int t = m < TM ? m : m - TM;
+    const uint16_t* src = static_cast<const uint16_t*>(m < TM ? p.k : p.q);
+    kq = *reinterpret_cast<const u32x4*>(src + ((tok0 + min(t, T - 1)) * p.Hk + hk) * DK + e);
+    const bool keep = m < 2 * TM && t < T;
+    kq = u32x4{keep ? kq.x : 0u, keep ? kq.y : 0u, keep ? kq.z : 0u, keep ? kq.w : 0u};
+  }
+  constexpr int NVS = (TM * kVmRows + 255) / 256;
+  float vr[NVS];
+#pragma unroll
+  for (int j = 0; j < NVS; ++j) {
+    const int i = min(tid + 256 * j, TM * kVmRows - 1);
+    const int t = i / kVmRows, r = i % kVmRows;
+    vr[j] = IO<DT>::load1(p.v, ((tok0 + min(t, T - 1)) * p.Hv + hv) * p.Dv + min(dv0 + r, p.Dv - 1));
+  }
+  float gx = 0.0f, gy = 0.0f;
+  uint8_t mm = 1;
+  if (tid < TM) {
+    const int64_t tok = tok0 + min(tid, T - 1);
+    gate_load<GF, DT>(p.ga, tok * p.ga.ld + hv, gx, gy);
+    mm = p.mask != nullptr ? p.mask[tok] : kActive;
+  }
+  const int rown = dv0 + 16 * wave + lr;
+  const int64_t srow = ((static_cast<int64_t>(slot) * p.Hv + hv) * p.Dv + min(rown, p.Dv - 1)) * DK;
+  const float* src = p.state_in != nullptr ? p.state_in + srow : kZeroRow;
+  f32x4 x0[4], x1[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    x0[s] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(src + 32 * s + 4 * lg));
+    x1[s] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(src + 32 * s + 16 + 4 * lg));
+  }
+
+  *reinterpret_cast<u32x4*>(&KQ[tid >> 4][(tid & 15) * 8]) = kq;
+#pragma unroll
+  for (int j = 0; j < NVS; ++j) {
+    const int i = tid + 256 * j;
+    if (i < TM * kVmRows) Vs[i / kVmRows][i % kVmRows] = vr[j];
+  }
+  if (tid < TM) {
+    float g, beta;
+    gate_transform<GF>(p.ga.mode, gx, gy, ea, db, g, beta);
+    const bool on = mm != 0 && tid < T;
+    Gs[tid] = on ? g : 1.0f;
+    Bs[tid] = on ? beta : 0.0f;
+    Ms[tid] = on ? 1 : 0;
+  }
+  __syncthreads();
+
+  // A fragments (rows of KQ, columns in the state lanes' order)
+  bf16x8 a[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    const u32x2 lo4 = *reinterpret_cast<const u32x2*>(&KQ[lr][32 * s + 4 * lg]);
+    const u32x2 hi4 = *reinterpret_cast<const u32x2*>(&KQ[lr][32 * s + 16 + 4 * lg]);
+    a[s] = __builtin_bit_cast(bf16x8, u32x4{lo4.x, lo4.y, hi4.x, hi4.y});
+  }
+
+  // Coefficients: D_kk = A K^T (B = the k rows of A; lane (n, g) holds
+  // D_kk[4 g + i][n]), scaled by r(t, s) = prod_{s < u <= t} g_u.
+  {
+    const bf16x8 zero8 = {};
+    f32x4 dkk = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int s = 0; s < 4; ++s) dkk = mfma_bf16(a[s], lr < TM ? a[s] : zero8, dkk);
+    if (lr < TM) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int m = 4 * lg + i, sidx = lr;
+        const int t = m < TM ? m : m - TM;
+        if (m < 2 * TM) {
+          float r = 1.0f;
+          for (int u = sidx + 1; u <= t; ++u) r *= Gs[u];
+          const bool kk = m < TM;
+          const bool on = t < T && (kk ? sidx < t : sidx <= t);
+          Cf[wave][kk ? 0 : 1][t][sidx] = on ? r * dkk[i] : 0.0f;
+        }
+      }
+    }
+  }
+
+  // a_t, b_t of this wave's 16 rows
+  f32x4 d = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    bf16x8 sh, sl;
+    split8(x0[s], x1[s], sh, sl);
+    d = mfma_bf16(a[s], sh, d);
+    d = mfma_bf16(a[s], sl, d);
+  }
+  // gather a and b of row r into lane (r, 0)
+  float av[TM], bv[TM];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    if constexpr (TM == 4) {
+      av[i] = d[i];
+      bv[i] = __shfl(d[i], lane + 16, 64);
+    } else {
+      av[i] = d[i];
+      av[4 + i] = __shfl(d[i], lane + 16, 64);
+      bv[i] = __shfl(d[i], lane + 32, 64);
+      bv[4 + i] = __shfl(d[i], lane + 48, 64);
+    }
+  }
+  // Cf was written by this wave only
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+  // the scalar recurrence of the unrolled verify (as in verify_wy_kernel)
+  const bool store = lg == 0 && rown < p.Dv;
+  float dl[TM];
+  float gam = 1.0f;
+  static_for<TM>([&](auto tt) {
+    constexpr int t = tt.value;
+    dl[t] = 0.0f;
+    if (t < T) {
+      gam *= Gs[t];
+      float u = Vs[t][16 * wave + lr] - gam * av[t];
+      float yv = gam * bv[t];
+      static_for<t>([&](auto ss) { u = fmaf(-Cf[wave][0][t][ss.value], dl[ss.value], u); });
+      dl[t] = Bs[t] * u;
+      static_for<t + 1>([&](auto ss) { yv = fmaf(Cf[wave][1][t][ss.value], dl[ss.value], yv); });
+      if (Ms[t] == 0) yv = 0.0f;
+      if (store) IO<DT>::store1(p.y, ((tok0 + t) * p.Hv + hv) * p.Dv + rown, yv);
+    }
+  });
+}
+
 enum KernelKind { K_DECODE = 0, K_TILE = 1, K_VERIFY = 2 };
+
+template <int GF>
+int launch_verify_mfma(hipStream_t st, const RecParams& p, int64_t B) {
+  const dim3 grid(static_cast<unsigned>((p.Dv + kVmRows - 1) / kVmRows), static_cast<unsigned>(p.Hv),
+                  static_cast<unsigned>(B));
+  if (p.T <= 4) hipLaunchKernelGGL((verify_mfma_kernel<GF, 4>), grid, dim3(256), 0, st, p);
+  else hipLaunchKernelGGL((verify_mfma_kernel<GF, kVerifyMaxT>), grid, dim3(256), 0, st, p);
+  return gdn_host::check_launch("gdn_recurrent");
+}
 
 template <int DK, int DT, int GF>
 int launch_pf(int kind, dim3 grid, dim3 block, hipStream_t st, const RecParams& p) {
@@ -646,6 +852,14 @@ int run_recurrent(const gdn_recurrent_args* a) {
   dim3 grid(static_cast<unsigned>((a->Dv + rows_per_wg - 1) / rows_per_wg),
             static_cast<unsigned>(a->Hv), static_cast<unsigned>(a->B));
   hipStream_t st = static_cast<hipStream_t>(a->stream);
+  // bf16 q/k at Dk = 128 (16-byte aligned rows): the verify's dot products
+  // on MFMA (verify_mfma_kernel, 64-row workgroups)
+  if (kind == K_VERIFY && a->Dk == 128 && a->qkv_dtype == GDN_DTYPE_BF16 && gdn_host::aligned(a->q, 16) &&
+      gdn_host::aligned(a->k, 16)) {
+    if (gf == GF_IO_F32) return launch_verify_mfma<GF_IO_F32>(st, p, a->B);
+    if (gf == GF_IO_IO) return launch_verify_mfma<GF_IO_IO>(st, p, a->B);
+    return launch_verify_mfma<GF_ANY>(st, p, a->B);
+  }
   switch (a->Dk) {
     case 64:
       return launch_dt<64>(a->qkv_dtype, gf, kind, grid, block, st, p);

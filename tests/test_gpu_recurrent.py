@@ -205,6 +205,32 @@ def test_verify_without_state_write_matches_oracle(T, dtype, Dk, Dv):
         assert torch.all(y.cpu()[off] == 0)
 
 
+def _offset_copy(x, shift=4):
+    """x in a buffer shifted by `shift` elements: 8-byte but not 16-byte aligned."""
+    buf = torch.empty(x.numel() + shift, dtype=x.dtype, device=x.device)
+    out = buf[shift:].view(x.shape)
+    out.copy_(x)
+    return out
+
+
+@pytest.mark.parametrize("T", [1, 3, 4, 6, 8])
+def test_verify_mfma_and_fma_kernels_agree(T):
+    """bf16 q/k at Dk=128 take the MFMA verify (state split hi/lo bf16);
+    q/k rows that are only 8-byte aligned take the FMA kernel.  Both against
+    the oracle, and against each other."""
+    d = draw(400 + T, 5, T, 2, 4, 128, 128, mask_p=0.25 if T > 2 else None)
+    t, r = to_torch(d, DEV)
+    args = (t["v"], t["a"], t["b"], t["A_log"], t["dt_bias"], t["state"], t["mask"])
+    y_mfma, _ = mx.gated_delta_verify(t["q"], t["k"], *args)
+    q8, k8 = _offset_copy(t["q"]), _offset_copy(t["k"])
+    assert q8.data_ptr() % 16 != 0 and k8.data_ptr() % 16 != 0
+    y_fma, _ = mx.gated_delta_verify(q8, k8, *args)
+    y_ref, _ = oracle_update(r)
+    assert row_errs_y(y_mfma.float().cpu().numpy(), y_ref).max() <= Y_TOL
+    assert row_errs_y(y_fma.float().cpu().numpy(), y_ref).max() <= Y_TOL
+    assert row_errs_y(y_mfma.float().cpu().numpy(), y_fma.float().cpu().numpy()).max() <= Y_TOL
+
+
 def test_verify_with_underflowing_decay_and_precomputed_gates():
     d = draw(77, 2, 4, 2, 4, 128, 128)
     d["A_log"][:] = 12.0          # exp(A_log) softplus(.) >> 100: g underflows to 0
