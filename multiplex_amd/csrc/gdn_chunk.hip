@@ -508,13 +508,15 @@ constexpr int kTiles = DV / DVT;  // state-row tiles per head (8)
 constexpr int kXcds = 8;
 
 __global__ __launch_bounds__(256) void chunk_scan_kernel(const ChunkParams p) {
-  // Block b runs on XCD b % 8.  Heads (over all sequences, longest sequence
-  // first) are dealt to XCDs round-robin, and the 8 tiles of a head go to
-  // the head's XCD, where they share its K/T/P stream in L2.
+  // Block b runs on XCD b % 8.  The v-heads of one k-head (a GQA group,
+  // which share its K, Q and K^T) form a unit; units (over all sequences,
+  // longest sequence first) are dealt to XCDs round-robin, and the 8 tiles of
+  // each head go to the unit's XCD, where they share its operands in L2.
   const int blk = blockIdx.x;
   const int xcd = blk % kXcds, r8 = blk / kXcds;
   const int tile = r8 % kTiles;
-  const int head_rank = (r8 / kTiles) * kXcds + xcd;
+  const int slot_x = r8 / kTiles;  // head slot on this XCD
+  const int head_rank = ((slot_x / p.group) * kXcds + xcd) * p.group + slot_x % p.group;
   if (head_rank >= p.n_seqs * p.Hv) return;
   const int seq = seq_by_rank(p, head_rank / p.Hv);
   int slot = seq;
@@ -787,7 +789,7 @@ extern "C" int gdn_chunk_fwd(const void* q, const void* k, const void* v, int qk
       !gdn_host::aligned(v, 16) || !gdn_host::aligned(state_in, 16) || !gdn_host::aligned(state_out, 16))
     return fail(GDN_ERR_INVALID, "gdn_chunk_fwd: misaligned pointer");
   if (n_tok > INT32_MAX / 2 || n_seqs > 65535 || Hv > 65535 || max_chunks(n_seqs, n_tok, packed) * Hv > INT32_MAX ||
-      (DV / DVT) * (Hv * n_seqs + 8) > INT32_MAX)
+      (DV / DVT) * (Hv * n_seqs + 8 * (Hv / Hk)) > INT32_MAX)
     return fail(GDN_ERR_UNSUPPORTED, "gdn_chunk_fwd: problem too large");
 
   ChunkParams p;
@@ -822,8 +824,9 @@ extern "C" int gdn_chunk_fwd(const void* q, const void* k, const void* v, int qk
     const int rc = gdn_host::check_launch("gdn_chunk_fwd/prep");
     if (rc != GDN_OK) return rc;
   }
-  const int64_t heads = n_seqs * Hv;
-  const int64_t scan_blocks = kTiles * kXcds * ((heads + kXcds - 1) / kXcds);
+  // whole GQA units per XCD (a unit never spans two sequences: Hv % group == 0)
+  const int64_t heads = n_seqs * Hv, unit = Hv / Hk;
+  const int64_t scan_blocks = kTiles * kXcds * unit * ((heads + kXcds * unit - 1) / (kXcds * unit));
   hipLaunchKernelGGL(chunk_scan_kernel, dim3(static_cast<unsigned>(scan_blocks)), dim3(256), 0, st, p);
   return gdn_host::check_launch("gdn_chunk_fwd/scan");
 }
