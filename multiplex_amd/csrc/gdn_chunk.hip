@@ -554,17 +554,28 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(const ChunkParams p) {
   const uint32_t off_g4 = rec_hv + kOffGam + (16 * wave + 4 * lq) * 4;
   const uint32_t off_g1 = rec_hv + kOffGam + (16 * wave + lr) * 4;
 
-  auto bufs_of = [&](int ci) {
-    const int64_t t0 = sr.tok0 + static_cast<int64_t>(ci) * CH;
-    const uint32_t last = static_cast<uint32_t>(min(CH, sr.len - ci * CH) - 1);
-    const size_t chunk = static_cast<size_t>(sr.chunk0 + ci);
+  // Bases of the chunk whose descriptors come next, advanced by one chunk at
+  // a time (a 64-bit add each) rather than recomputed from the chunk index.
+  const size_t vy_step = static_cast<size_t>(CH) * hv_row;
+  const size_t rec_step = static_cast<size_t>(p.Hv) * kRecBytes;
+  const unsigned char* vb = reinterpret_cast<const unsigned char*>(p.v + (sr.tok0 * p.Hv + hv) * DV + dv0);
+  const unsigned char* yb = reinterpret_cast<const unsigned char*>(p.y + (sr.tok0 * p.Hv + hv) * DV + dv0);
+  const unsigned char* rb = p.ws + static_cast<size_t>(sr.chunk0) * rec_step;
+  int left = sr.len;  // tokens from the chunk at vb to the sequence's end
+  auto bufs_here = [&]() {
+    const uint32_t last = static_cast<uint32_t>(min(CH, left) - 1);
     ChunkBufs c;
-    c.v = buf_rsrc(p.v + (t0 * p.Hv + hv) * DV + dv0, last * hv_row + DV * 2);
-    c.y = buf_rsrc(p.y + (t0 * p.Hv + hv) * DV + dv0, last * hv_row + DV * 2);
-    const unsigned char* recs = p.ws + chunk * p.Hv * kRecBytes;
-    c.rec = buf_rsrc(recs, static_cast<uint32_t>(p.Hv) * kRecBytes);
-    c.gam = reinterpret_cast<const float*>(recs + rec_hv + kOffGam);
+    c.v = buf_rsrc(vb, last * hv_row + DV * 2);
+    c.y = buf_rsrc(yb, last * hv_row + DV * 2);
+    c.rec = buf_rsrc(rb, static_cast<uint32_t>(rec_step));
+    c.gam = reinterpret_cast<const float*>(rb + rec_hv + kOffGam);
     return c;
+  };
+  auto advance = [&]() {
+    vb += vy_step;
+    yb += vy_step;
+    rb += rec_step;
+    left -= CH;
   };
 
   WaveOps o = {};
@@ -627,8 +638,8 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(const ChunkParams p) {
     for (int j = 0; j < 2; ++j) split4_store(sacc[j], &Sh[lr][32 * wave + 16 * j + 4 * lq], &Sl[lr][32 * wave + 16 * j + 4 * lq]);
   };
 
+  const ChunkBufs c0 = bufs_here();  // chunk 0 (only used when the sequence has chunks)
   if (nch > 0) {
-    const ChunkBufs c0 = bufs_of(0);
     load_kq(c0);
     load_vg(c0);
     load_t(c0);
@@ -639,11 +650,12 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(const ChunkParams p) {
   write_state();
   const f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
 
-  BufRsrc y_cur = bufs_of(0).y;  // (only used when the sequence has chunks)
+  BufRsrc y_cur = c0.y;
   for (int ci = 0; ci < nch; ++ci) {
     // the next chunk's operands (the last chunk reloads its own: no branches
     // around the loads, so their waits are not forced early)
-    const ChunkBufs cn = bufs_of(min(ci + 1, nch - 1));
+    if (ci + 1 < nch) advance();
+    const ChunkBufs cn = bufs_here();
     __syncthreads();  // state hi/lo of this chunk is in LDS
 
     // ---- X_K = K S0^T (tokens x rows) and X_Q^T = S0 Q^T (rows x tokens)
