@@ -337,11 +337,16 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(const ChunkParams p) {
   }
   __syncthreads();
 
-  // P planes out: a linear 16 KB copy (hi then lo, as in the record).
+  // P planes out: a linear 16 KB copy (hi then lo, as in the record).  The
+  // fragments above the diagonal that hold only zeros -- row blocks 0 and 1,
+  // column block 1 (fragments 1 and 3 of a plane) -- are not written: the
+  // scan never reads them.
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int i = tid + 256 * j;
-    *reinterpret_cast<u32x4*>(rec + kOffPh + 16 * i) = *reinterpret_cast<const u32x4*>(Pst + 8 * i);
+    const int frag = (i & 511) >> 6;
+    if (frag != 1 && frag != 3)
+      *reinterpret_cast<u32x4*>(rec + kOffPh + 16 * i) = *reinterpret_cast<const u32x4*>(Pst + 8 * i);
   }
   __syncthreads();  // the P planes are out: their buffer takes (I + A)^{-1}
 
@@ -419,11 +424,13 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(const ChunkParams p) {
   uint16_t* Th = reinterpret_cast<uint16_t*>(rec + kOffTh);
   uint16_t* Tl = reinterpret_cast<uint16_t*>(rec + kOffTl);
   // one 16-byte group (8 columns of a row) per thread and pass; blocks
-  // above the diagonal are zero (never written in Ti)
+  // above the diagonal are zero (never written in Ti), and the all-zero
+  // fragments (rows < 32, columns >= 32) are not stored, as for P
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     const int i = tid + 256 * j;
     const int r = i >> 3, cc = (i & 7) * 8;
+    if (r < 32 && cc >= 32) continue;
     const bool upper = (cc >> 4) > (r >> 4);
     const f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
     const f32x4 a = upper ? z : *reinterpret_cast<const f32x4*>(&Ti[r][cc]);
@@ -595,7 +602,8 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(const ChunkParams p) {
   };
   // T and P are lower triangular: the rows of waves 0 and 1 (tokens < 32)
   // have no entries in the second 32-column block, whose loads and products
-  // those waves skip (wave-uniform branches).
+  // those waves skip (wave-uniform branches; the prep does not write those
+  // fragments).
   const bool full_rows = wave >= 2;
   auto load_t = [&](const ChunkBufs& c) {
     static_for<2>([&](auto s) {
