@@ -198,7 +198,7 @@ def bench_verify(torch, mx, dev, timer, iters=50):
                 frac=credited / (t_commit * 1e-3) / 1e9 / HBM_PEAK_GBS)
 
 
-def bench_prefill(torch, mx, dev, timer, iters=10):
+def bench_prefill(torch, mx, dev, timer, iters=50):
     gen = torch.Generator().manual_seed(1003)
     T = 4096
     qkv = torch.randn(1, T, C_DIM, generator=gen).to(torch.bfloat16).to(dev)
@@ -237,7 +237,7 @@ def bench_prefill(torch, mx, dev, timer, iters=10):
                 flops=flops, finite=bool(torch.isfinite(out["S"]).all()))
 
 
-def bench_mixed(torch, mx, dev, timer, iters=10):
+def bench_mixed(torch, mx, dev, timer, iters=50):
     """One continuous-batching step: the packed prefills run on the current
     stream while the decode, verify and commit launches (independent rows
     and states) run beside them on a second stream; the step ends when both
