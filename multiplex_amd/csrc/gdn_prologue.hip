@@ -71,7 +71,7 @@ __global__ __launch_bounds__(256) void prologue_kernel(const ProParams p) {
   constexpr int HPW = 64 / LPH;  // heads per wavefront
   constexpr int WDT = W32 ? GDN_DTYPE_F32 : DT;
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
   int seq, len, run;
   int64_t start;
   if (!locate<R>(p, seq, start, len, run)) return;
@@ -119,9 +119,35 @@ __global__ __launch_bounds__(256) void prologue_kernel(const ProParams p) {
     }
     return;
   }
-  // Issue every load first: the run's tokens (rows past the end re-read the
-  // last row and are never stored), the window of the 3 inputs before the
-  // run, the taps.  A masked token reads as zero (mask byte as multiplier).
+  // Issue every load first, in the order they are needed (memory returns in
+  // issue order, so a wait for the taps or the window would otherwise also
+  // wait for every token row queued ahead of them): the taps, the window of
+  // the 3 inputs before the run, then the run's tokens (rows past the end
+  // re-read the last row and are never stored).  All are raw loads, unpacked
+  // only once every load is issued, so token u is computed as soon as its
+  // own row arrives.  A masked token reads as zero (mask byte as multiplier).
+  Raw8<WDT> wr[KT];  // taps of the lane's 8 channels: weight[c][tap], 32 consecutive values
+#pragma unroll
+  for (int i = 0; i < KT; ++i) wr[i] = load_raw8<WDT>(p.weight, static_cast<int64_t>(c0) * KT + 8 * i);
+  // window row i = X[t + i] for the run's first token t: a conv-state row
+  // for t + i < KT - 1, else a qkv row.  Without a conv state those rows are
+  // zeros: the sequence's first qkv row is read and multiplied by 0, so the
+  // load stays unconditional and in the global address space.
+  Raw8<DT> xw[KT - 1];
+  float wm[KT - 1];
+#pragma unroll
+  for (int i = 0; i < KT - 1; ++i) {
+    const int xi = t_begin + i;
+    const bool from_cs = xi < KT - 1;
+    const bool cs_row = from_cs && p.cs_in != nullptr;
+    const int64_t tok = from_cs ? start : start + xi - (KT - 1);
+    const int64_t off = cs_row ? (static_cast<int64_t>(seq) * (KT - 1) + xi) * C + c0 : tok * p.ld + c0;
+    xw[i] = load_raw8<DT>(cs_row ? p.cs_in : p.qkv, off);
+    wm[i] = from_cs ? (cs_row ? 1.0f : 0.0f) : 1.0f;
+    if constexpr (MASK) {
+      if (!from_cs) wm[i] = p.mask[tok] != 0 ? 1.0f : 0.0f;
+    }
+  }
   Raw8<DT> xs[R];
   float xm[R];
   const int t_last = t_end - 1;
@@ -131,22 +157,22 @@ __global__ __launch_bounds__(256) void prologue_kernel(const ProParams p) {
     xs[u] = load_raw8<DT>(p.qkv, tok * p.ld + c0);
     if constexpr (MASK) xm[u] = p.mask[tok] != 0 ? 1.0f : 0.0f;
   }
-  // window[i] = X[t + i] for the run's first token t
-  float win[KT - 1][CPL];
-#pragma unroll
-  for (int i = 0; i < KT - 1; ++i) load_x(t_begin + i, win[i]);
-  // taps of the lane's 8 channels: weight[c][tap], 32 consecutive values
   float w[KT][CPL];
   {
     float wv[CPL * KT];
-    unpack8<WDT>(load_raw8<WDT>(p.weight, static_cast<int64_t>(c0) * KT), *reinterpret_cast<float(*)[CPL]>(&wv[0]));
-    unpack8<WDT>(load_raw8<WDT>(p.weight, static_cast<int64_t>(c0) * KT + 8), *reinterpret_cast<float(*)[CPL]>(&wv[8]));
-    unpack8<WDT>(load_raw8<WDT>(p.weight, static_cast<int64_t>(c0) * KT + 16), *reinterpret_cast<float(*)[CPL]>(&wv[16]));
-    unpack8<WDT>(load_raw8<WDT>(p.weight, static_cast<int64_t>(c0) * KT + 24), *reinterpret_cast<float(*)[CPL]>(&wv[24]));
+#pragma unroll
+    for (int i = 0; i < KT; ++i) unpack8<WDT>(wr[i], *reinterpret_cast<float(*)[CPL]>(&wv[8 * i]));
 #pragma unroll
     for (int j = 0; j < CPL; ++j)
 #pragma unroll
       for (int i = 0; i < KT; ++i) w[i][j] = wv[j * KT + i];
+  }
+  float win[KT - 1][CPL];
+#pragma unroll
+  for (int i = 0; i < KT - 1; ++i) {
+    unpack8<DT>(xw[i], win[i]);
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) win[i][j] *= wm[i];
   }
 
   // Head role: 0 = q, 1 = k, 2 = v (lanes of one head agree).
