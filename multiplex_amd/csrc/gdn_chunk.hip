@@ -99,6 +99,23 @@ __device__ __forceinline__ bf16x8 lds8(const uint16_t* p) {
   return *reinterpret_cast<const bf16x8*>(p);
 }
 
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef short i16x8 __attribute__((ext_vector_type(8)));
+typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+
+// K^T as an MFMA A-fragment from K rows in LDS ([token][dk], row stride KP),
+// by two transposed reads (ds_read_b64_tr_b16).  Within each 16-lane group,
+// lane i of a transposed read receives element i % 4 of the 4 read by lane
+// 4e + i / 4, for e = 0..3.  Lane (r, q) here passes &K[t0 + r / 4][d0 + 4 (r % 4)]
+// (t0 = the fragment's first token + 8 q, d0 = its first dk), so it receives
+// K[t0 + e][d0 + r]: tokens t0 .. t0+3 of dk d0 + r, then t0+4 .. t0+7 from
+// the rows 4 further on -- the 8 k-slots of row d0 + r of the fragment.
+__device__ __forceinline__ bf16x8 kt_frag(const uint16_t* p) {
+  const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p));
+  const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p + 4 * KP));
+  return __builtin_bit_cast(bf16x8, i16x8(__builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7)));
+}
+
 
 // Component-wise "keep or zero" (a ternary on the u32x4 struct would be
 // lowered through memory).
@@ -192,6 +209,8 @@ __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// KT_LDS: the scan forms K^T from K in LDS, so the record carries no K^T.
+template <bool KT_LDS>
 __global__ __launch_bounds__(256) void chunk_prep_kernel(const ChunkParams p) {
   // work index = chunk * Hv + hv: both v-heads of a k-head (GQA) share an XCD
   const int w = xcd_work_index();
@@ -297,7 +316,7 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(const ChunkParams p) {
       kk[j] = mfma16(ak, bk, kk[j]);
       qk[j] = mfma16(aq, bk, qk[j]);
     }
-    if (first_v) {
+    if (!KT_LDS && first_v) {
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         const f32x4 t = mfma16(ak, eye[h], f32x4{0.0f, 0.0f, 0.0f, 0.0f});
@@ -513,7 +532,14 @@ __device__ __forceinline__ int seq_by_rank(const ChunkParams& p, int rank) {
 
 constexpr int kTiles = DV / DVT;  // state-row tiles per head (8)
 constexpr int kXcds = 8;
+constexpr int kCUs = 256;  // compute units of an MI355X (8 XCDs x 32)
 
+// KT_LDS: K^T comes from transposed LDS reads of the K rows the waves hold
+// (the record's K^T is then not written or read).  That trades 16 KB of
+// operand loads per chunk for 16 KB of LDS writes and reads: it pays when
+// several workgroups share a CU, and costs a little on the chain when one
+// workgroup has the CU to itself.
+template <bool KT_LDS>
 __global__ __launch_bounds__(256) void chunk_scan_kernel(const ChunkParams p) {
   // Block b runs on XCD b % 8.  The v-heads of one k-head (a GQA group,
   // which share its K, Q and K^T) form a unit; units (over all sequences,
@@ -545,6 +571,7 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(const ChunkParams p) {
   __shared__ __align__(16) uint16_t Rh[DVT][CP], Rl[DVT][CP];  // R^T [row][token]
   __shared__ __align__(16) uint16_t Uh[DVT][CP], Ul[DVT][CP];  // U^T
   __shared__ __align__(16) uint16_t Eh[DVT][CP], El[DVT][CP];  // (diag(e) U)^T
+  __shared__ __align__(16) uint16_t Kl[KT_LDS ? CH : 1][KP];   // K [token][dk] (KT_LDS)
 
   // Loop-invariant lane offsets (bytes) into the per-chunk descriptors:
   // fragment (rb, cb) of a record matrix is 1 KB at (rb * n_cb + cb) KB.
@@ -615,11 +642,13 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(const ChunkParams p) {
   };
   auto load_e = [&](const ChunkBufs& c) { o.e = buf_f32x4(c.rec, off_g4 + (kOffE - kOffGam)); };
   auto load_kt = [&](const ChunkBufs& c) {
-    static_for<2>([&](auto j) {
-      static_for<2>([&](auto s) {
-        o.kt[j.value][s.value] = buf_bf16x8(c.rec, off_kt + 2048 * j.value + 1024 * s.value, 0);
+    if constexpr (!KT_LDS) {
+      static_for<2>([&](auto j) {
+        static_for<2>([&](auto s) {
+          o.kt[j.value][s.value] = buf_bf16x8(c.rec, off_kt + 2048 * j.value + 1024 * s.value, 0);
+        });
       });
-    });
+    }
     o.gC = c.gam[CH - 1];
   };
   auto load_p = [&](const ChunkBufs& c) {
@@ -677,6 +706,13 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(const ChunkParams p) {
       xq0 = mfma16(sh, o.q[s.value], xq0);
       xq1 = mfma16(sl, o.q[s.value], xq1);
     });
+    if constexpr (KT_LDS) {
+      // this wave's K rows to LDS (read transposed after the next barrier),
+      // before their registers take the next chunk's K
+      static_for<4>([&](auto s) {
+        *reinterpret_cast<bf16x8*>(&Kl[16 * wave + lr][32 * s.value + lg8]) = o.k[s.value];
+      });
+    }
     load_kq(cn);
 
     // ---- R = beta (V - gamma X_K) -> R^T
@@ -690,6 +726,19 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(const ChunkParams p) {
     const float gy = o.gy;  // kept for Y
     load_vg(cn);
     __syncthreads();  // R^T complete
+
+    // K^T fragments of this wave's state columns (KT_LDS: from the K rows in
+    // LDS since the barrier above, read here so their latency is off the update)
+    bf16x8 kt[2][2];
+    static_for<2>([&](auto j) {
+      static_for<2>([&](auto s) {
+        if constexpr (KT_LDS)
+          kt[j.value][s.value] =
+              kt_frag(&Kl[32 * s.value + 8 * lq + (lr >> 2)][32 * wave + 16 * j.value + 4 * (lr & 3)]);
+        else
+          kt[j.value][s.value] = o.kt[j.value][s.value];
+      });
+    });
 
     // ---- U = T R for this wave's 16 tokens
     f32x4 u0 = z, u1 = z;
@@ -718,8 +767,8 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(const ChunkParams p) {
       const bf16x8 eh = lds8(&Eh[lr][kc]);
       const bf16x8 el = lds8(&El[lr][kc]);
       static_for<2>([&](auto j) {
-        sacc[j.value] = mfma16(o.kt[j.value][s.value], eh, sacc[j.value]);
-        sacc[j.value] = mfma16(o.kt[j.value][s.value], el, sacc[j.value]);
+        sacc[j.value] = mfma16(kt[j.value][s.value], eh, sacc[j.value]);
+        sacc[j.value] = mfma16(kt[j.value][s.value], el, sacc[j.value]);
       });
     });
     load_kt(cn);
@@ -839,14 +888,21 @@ extern "C" int gdn_chunk_fwd(const void* q, const void* k, const void* v, int qk
 
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int64_t chunks = max_chunks(n_seqs, n_tok, packed);
+  // More scan workgroups than CUs (several per CU): K^T from LDS (fewer
+  // operand bytes per CU); else the record's K^T (a shorter chain per chunk).
+  const bool kt_lds = static_cast<int64_t>(kTiles) * n_seqs * Hv > kCUs;
   if (chunks > 0) {
-    hipLaunchKernelGGL(chunk_prep_kernel, dim3(static_cast<unsigned>(chunks * Hv)), dim3(256), 0, st, p);
+    const dim3 grid(static_cast<unsigned>(chunks * Hv));
+    if (kt_lds) hipLaunchKernelGGL(chunk_prep_kernel<true>, grid, dim3(256), 0, st, p);
+    else hipLaunchKernelGGL(chunk_prep_kernel<false>, grid, dim3(256), 0, st, p);
     const int rc = gdn_host::check_launch("gdn_chunk_fwd/prep");
     if (rc != GDN_OK) return rc;
   }
   // whole GQA units per XCD (a unit never spans two sequences: Hv % group == 0)
   const int64_t heads = n_seqs * Hv, unit = Hv / Hk;
   const int64_t scan_blocks = kTiles * kXcds * unit * ((heads + kXcds * unit - 1) / (kXcds * unit));
-  hipLaunchKernelGGL(chunk_scan_kernel, dim3(static_cast<unsigned>(scan_blocks)), dim3(256), 0, st, p);
+  const dim3 sgrid(static_cast<unsigned>(scan_blocks));
+  if (kt_lds) hipLaunchKernelGGL(chunk_scan_kernel<true>, sgrid, dim3(256), 0, st, p);
+  else hipLaunchKernelGGL(chunk_scan_kernel<false>, sgrid, dim3(256), 0, st, p);
   return gdn_host::check_launch("gdn_chunk_fwd/scan");
 }

@@ -128,3 +128,18 @@ def test_prepared_launch_equals_call():
         plan.launch()
         y, S = plan.outputs
         assert torch.equal(y, y_ref) and torch.equal(S, S_ref)
+
+
+def test_kt_sources_agree_bitwise():
+    """With more scan workgroups than CUs the scan forms K^T by transposed LDS
+    reads of K; with at most one per CU it reads the record's K^T.  Two
+    Hv=32 sequences in one call (512 workgroups) against each alone (256):
+    the transposes are exact, so the results are bit-identical."""
+    d = draw(309, 2, 200, 16, 32, 128, 128)
+    t, _ = to_torch(d, DEV)
+    y2, S2 = chunked(t, t["state"])
+    for b in range(2):
+        one = {k: (v[b:b + 1] if k in ("q", "k", "v", "a", "b", "state") else v) for k, v in t.items()}
+        y1, S1 = chunked(one, one["state"])
+        assert torch.equal(y1[0], y2[b]), f"row {b}: y"
+        assert torch.equal(S1[0], S2[b]), f"row {b}: state"
