@@ -220,7 +220,8 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(const ChunkParams p) {
   int len;
   if (!chunk_at(p, c, tok0, len)) return;
   const int hk = hv / p.group;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
   const int lr = lane & 15, lq = lane >> 4, lg8 = lq * 8;
 
   // Two 17 KB buffers, each reused once (LDS stays under 53 KB, so three
@@ -240,11 +241,13 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(const ChunkParams p) {
   auto Ti = reinterpret_cast<float(*)[CH + 4]>(buf1);
   uint16_t* Pst = reinterpret_cast<uint16_t*>(buf1);
 
-  // Gate loads first (wave 0), so waiting for them does not wait for the
-  // K/Q rows queued behind; then the rows (rows past the chunk's end read its
-  // last row and are zeroed at the LDS store).
-  float lg = 0.0f, bt = 0.0f;
-  if (wave == 0) load_log_gates(p.ga, (tok0 + min(lane, len - 1)) * p.ga.ld + hv, hv, lg, bt);
+  // Gate loads first, raw (wave 0 uses them; every wave issues them, so no
+  // branch lets the compiler start converting them early, which would wait),
+  // so waiting for them does not wait for the K/Q rows queued behind; then
+  // the rows (rows past the chunk's end read its last row and are zeroed at
+  // the LDS store); the gate transforms only after every load is issued.
+  const GateRaw gr = load_gate_raw(p.ga, (tok0 + min(lane, len - 1)) * p.ga.ld + hv, hv);
+  asm volatile("" ::: "memory");  // keeps the gate loads issued ahead of the rows
   u32x4 kr[4], qr[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
@@ -256,6 +259,8 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(const ChunkParams p) {
   }
   unsigned char* rec = p.ws + (static_cast<size_t>(c) * p.Hv + hv) * kRecBytes;
   if (wave == 0) {
+    float lg, bt;
+    log_gates(p.ga, gr, lg, bt);
     // padding tokens: no decay, no write; g = 0 (pre-transformed) stays finite
     lg = lane < len ? fmaxf(lg, -1.0e30f) : 0.0f;
     bt = lane < len ? bt : 0.0f;

@@ -54,11 +54,18 @@ __device__ __forceinline__ uint16_t f32_to_f16(float f) {
   return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
 }
 
-// Scalar load of a runtime-typed element (gates, per-head parameters).
+// Scalar load of a runtime-typed element (gates, per-head parameters).  Two
+// unconditional 16-bit loads -- the halves of an fp32 element, or the 16-bit
+// element twice -- combined by selects: a per-dtype branch around the load
+// would force a wait for it (and for every load issued before it) right there.
 __device__ __forceinline__ float load_any(const void* p, int dt, int64_t i) {
-  if (dt == GDN_DTYPE_F32) return static_cast<const float*>(p)[i];
-  const uint16_t h = static_cast<const uint16_t*>(p)[i];
-  return dt == GDN_DTYPE_BF16 ? bf16_to_f32(h) : f16_to_f32(h);
+  const bool f32 = dt == GDN_DTYPE_F32;
+  const uint16_t* e = static_cast<const uint16_t*>(p) + (f32 ? 2 * i : i);
+  const uint16_t lo = e[0];
+  const uint16_t hi = e[f32 ? 1 : 0];
+  const float as_f32 = __uint_as_float((static_cast<uint32_t>(hi) << 16) | lo);
+  const float as_16 = dt == GDN_DTYPE_BF16 ? bf16_to_f32(lo) : f16_to_f32(lo);
+  return f32 ? as_f32 : as_16;
 }
 
 // Compile-time typed I/O for q/k/v/y: DT is one of the GDN_DTYPE_* codes.
@@ -206,17 +213,46 @@ __device__ __forceinline__ void gate_transform(int mode, float x, float y, float
   }
 }
 
+// Raw gate inputs of one token, loads only: the 16-bit halves of a (or g),
+// b (or beta) and the head's A_log and dt_bias, as load_any reads them.  Every
+// load is unconditional (pre-transformed gates read gx in place of the
+// absent parameters) and nothing is converted here, so a caller can issue
+// more loads before anything waits for these.
+struct GateRaw {
+  uint32_t lo[4], hi[4];  // 16-bit halves, one per register (no packing, which would wait)
+};
+__device__ __forceinline__ void load_raw_any(const void* p, int dt, int64_t i, uint32_t& lo, uint32_t& hi) {
+  const bool f32 = dt == GDN_DTYPE_F32;
+  const uint16_t* e = static_cast<const uint16_t*>(p) + (f32 ? 2 * i : i);
+  lo = e[0];
+  hi = e[f32 ? 1 : 0];
+}
+__device__ __forceinline__ float raw_any_value(int dt, uint32_t lo, uint32_t hi) {
+  const float as_f32 = __uint_as_float((hi << 16) | lo);
+  const uint16_t h = static_cast<uint16_t>(lo);
+  const float as_16 = dt == GDN_DTYPE_BF16 ? bf16_to_f32(h) : f16_to_f32(h);
+  return dt == GDN_DTYPE_F32 ? as_f32 : as_16;
+}
+__device__ __forceinline__ GateRaw load_gate_raw(const GateArgs& ga, int64_t gi, int hv) {
+  const bool raw = ga.mode != GDN_GATES_PRE;
+  GateRaw r;
+  load_raw_any(ga.gx, ga.gdt, gi, r.lo[0], r.hi[0]);
+  load_raw_any(ga.gy, ga.gdt, gi, r.lo[1], r.hi[1]);
+  load_raw_any(raw ? ga.A_log : ga.gx, raw ? ga.pdt : ga.gdt, raw ? hv : gi, r.lo[2], r.hi[2]);
+  load_raw_any(raw ? ga.dt_bias : ga.gx, raw ? ga.pdt : ga.gdt, raw ? hv : gi, r.lo[3], r.hi[3]);
+  return r;
+}
+
 // Log decay (chunked prefill): -exp(A_log) softplus(a + dt_bias), or log g.
-__device__ __forceinline__ void load_log_gates(const GateArgs& ga, int64_t gi, int hv, float& logg,
-                                               float& beta) {
-  const float x = load_any(ga.gx, ga.gdt, gi);
-  const float y = load_any(ga.gy, ga.gdt, gi);
+__device__ __forceinline__ void log_gates(const GateArgs& ga, const GateRaw& r, float& logg, float& beta) {
+  const float x = raw_any_value(ga.gdt, r.lo[0], r.hi[0]);
+  const float y = raw_any_value(ga.gdt, r.lo[1], r.hi[1]);
   if (ga.mode == GDN_GATES_PRE) {
     logg = logf(x);
     beta = y;
   } else {
-    const float al = load_any(ga.A_log, ga.pdt, hv);
-    const float db = load_any(ga.dt_bias, ga.pdt, hv);
+    const float al = raw_any_value(ga.pdt, r.lo[2], r.hi[2]);
+    const float db = raw_any_value(ga.pdt, r.lo[3], r.hi[3]);
     logg = -expf(al) * softplus_f(x + db);
     beta = sigmoid_f(y);
   }
