@@ -201,6 +201,30 @@ __device__ __forceinline__ bool chunk_at(const ChunkParams& p, int c, int64_t& t
 
 // ------------------------------------------------------------ chunk_prep
 
+// One DPP move of a double (both 32-bit halves with the same control);
+// lanes the move does not reach read 0.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ double dpp_d(double x) {
+  const uint64_t u = __builtin_bit_cast(uint64_t, x);
+  const uint32_t lo = __builtin_amdgcn_update_dpp(0, static_cast<int>(u), CTRL, ROW_MASK, 0xF, false);
+  const uint32_t hi = __builtin_amdgcn_update_dpp(0, static_cast<int>(u >> 32), CTRL, ROW_MASK, 0xF, false);
+  return __builtin_bit_cast(double, (static_cast<uint64_t>(hi) << 32) | lo);
+}
+
+// Inclusive prefix sum of a double over the 64 lanes: row shifts by 1, 2, 4
+// and 8 scan each 16-lane row, then the gfx9 row broadcasts carry the row
+// totals (lane 15 of a row to the next row, for rows 1 and 3; lane 31 to
+// rows 2 and 3).
+__device__ __forceinline__ double wave_scan_d(double x) {
+  x += dpp_d<0x111, 0xF>(x);  // row_shr:1
+  x += dpp_d<0x112, 0xF>(x);  // row_shr:2
+  x += dpp_d<0x114, 0xF>(x);  // row_shr:4
+  x += dpp_d<0x118, 0xF>(x);  // row_shr:8
+  x += dpp_d<0x142, 0xA>(x);  // row_bcast:15
+  x += dpp_d<0x143, 0xC>(x);  // row_bcast:31
+  return x;
+}
+
 // Orders this wave's LDS writes before its later LDS reads (no other wave
 // takes part).
 __device__ __forceinline__ void wave_lds_sync() {
@@ -247,6 +271,8 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(const ChunkParams p) {
   // the rows (rows past the chunk's end read its last row and are zeroed at
   // the LDS store); the gate transforms only after every load is issued.
   const GateRaw gr = load_gate_raw(p.ga, (tok0 + min(lane, len - 1)) * p.ga.ld + hv, hv);
+  double L_lane = 0.0;  // wave 0: L_t of token `lane` (its record entries are written last)
+  float b_lane = 0.0f;
   asm volatile("" ::: "memory");  // keeps the gate loads issued ahead of the rows
   u32x4 kr[4], qr[4];
 #pragma unroll
@@ -264,17 +290,10 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(const ChunkParams p) {
     // padding tokens: no decay, no write; g = 0 (pre-transformed) stays finite
     lg = lane < len ? fmaxf(lg, -1.0e30f) : 0.0f;
     bt = lane < len ? bt : 0.0f;
-    double L = lg;
-    for (int off = 1; off < 64; off <<= 1) {
-      const double o = __shfl_up(L, off, 64);
-      if (lane >= off) L += o;
-    }
-    Ld[lane] = L;
+    L_lane = wave_scan_d(lg);
+    Ld[lane] = L_lane;
     Bs[lane] = bt;
-    const double LC = __shfl(L, 63, 64);
-    reinterpret_cast<float*>(rec + kOffGam)[lane] = expf(static_cast<float>(L));
-    reinterpret_cast<float*>(rec + kOffE)[lane] = expf(static_cast<float>(LC - L));
-    reinterpret_cast<float*>(rec + kOffBeta)[lane] = bt;
+    b_lane = bt;
   }
   const bool first_v = hv % p.group == 0;  // writes the k-head's K^T, K and Q
 #pragma unroll
@@ -361,86 +380,80 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(const ChunkParams p) {
   }
   __syncthreads();
 
-  // P planes out: a linear 16 KB copy (hi then lo, as in the record).  The
-  // fragments above the diagonal that hold only zeros -- row blocks 0 and 1,
-  // column block 1 (fragments 1 and 3 of a plane) -- are not written: the
-  // scan never reads them.
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int i = tid + 256 * j;
-    const int frag = (i & 511) >> 6;
-    if (frag != 1 && frag != 3)
-      *reinterpret_cast<u32x4*>(rec + kOffPh + 16 * i) = *reinterpret_cast<const u32x4*>(Pst + 8 * i);
-  }
-  __syncthreads();  // the P planes are out: their buffer takes (I + A)^{-1}
-
-  // (I + A)^{-1}, A strictly lower.  Diagonal 16x16 blocks by forward
-  // substitution from registers (one lane per (block, column)).
+  // (I + A)^{-1}, A strictly lower.  Its diagonal 16x16 blocks by forward
+  // substitution (wave 0, one lane per (block, column)), into registers --
+  // only A is read -- while waves 1-3 copy the P planes out of the buffer the
+  // inverse takes next: a linear 16 KB copy (hi then lo, as in the record).
+  // The P fragments above the diagonal that hold only zeros -- row blocks 0
+  // and 1, column block 1 (fragments 1 and 3 of a plane) -- are not written:
+  // the scan never reads them.
+  const int dbase = 16 * (lane >> 4), dcol = lane & 15;
+  float x[16];
   if (wave == 0) {
-    const int base = 16 * (lane >> 4), j = lane & 15;
     float a[16][16];
 #pragma unroll
     for (int t = 1; t < 16; ++t)
 #pragma unroll
-      for (int i = 0; i < t; ++i) a[t][i] = As[base + t][base + i];
-    float x[16];
+      for (int i = 0; i < t; ++i) a[t][i] = As[dbase + t][dbase + i];
 #pragma unroll
     for (int t = 0; t < 16; ++t) {
-      float acc = t == j ? 1.0f : 0.0f;
+      float acc = t == dcol ? 1.0f : 0.0f;
 #pragma unroll
       for (int i = 0; i < t; ++i) acc = fmaf(-a[t][i], x[i], acc);
-      x[t] = t < j ? 0.0f : acc;
+      x[t] = t < dcol ? 0.0f : acc;
     }
+  } else {
+    for (int i = tid - 64; i < 1024; i += 192) {
+      const int frag = (i & 511) >> 6;
+      if (frag != 1 && frag != 3)
+        *reinterpret_cast<u32x4*>(rec + kOffPh + 16 * i) = *reinterpret_cast<const u32x4*>(Pst + 8 * i);
+    }
+  }
+  __syncthreads();  // the P planes are out: their buffer takes (I + A)^{-1}
+  if (wave == 0) {
 #pragma unroll
-    for (int t = 0; t < 16; ++t) Ti[base + t][base + j] = x[t];
+    for (int t = 0; t < 16; ++t) Ti[dbase + t][dbase + dcol] = x[t];
   }
   __syncthreads();
   // Off-diagonal blocks by distance d from the diagonal.  Block (I, J=I-d)
-  // belongs to wave J; a lane computes a 1x4 patch (row r, columns c4..c4+3):
+  // belongs to wave J:
   //   M = sum_{K=J}^{I-1} A_IK T_KJ,   T_IJ = -T_II M
+  // Each 16x16x16 block product is four fp32 MFMAs (16x16x4): lane l holds
+  // A[l % 16][4s + l / 16] and B[4s + l / 16][l % 16] for k-step s, and the
+  // accumulator rows 4 (l / 16) .. +3 of column l % 16.  M goes through LDS
+  // (this wave's Ms) to become the B operand of the second product.
   {
-    const int r = lane >> 2, c4 = (lane & 3) * 4;
+    const int ln = lane & 15, lk = lane >> 4;
     for (int d = 1; d < 4; ++d) {
       const int J = wave, I = wave + d;
       if (I < 4) {
-        // operands of a block product are loaded ahead of its FMAs (one LDS
-        // round trip per block instead of one per step)
-        f32x4 m0 = {0.0f, 0.0f, 0.0f, 0.0f}, m1 = m0;
+        f32x4 m = {0.0f, 0.0f, 0.0f, 0.0f};
         for (int Kb = J; Kb < I; ++Kb) {
-          f32x4 av[4], tb[16];
+          float a[4], b[4];
 #pragma unroll
-          for (int q = 0; q < 4; ++q) av[q] = *reinterpret_cast<const f32x4*>(&As[16 * I + r][16 * Kb + 4 * q]);
-#pragma unroll
-          for (int x = 0; x < 16; ++x) tb[x] = *reinterpret_cast<const f32x4*>(&Ti[16 * Kb + x][16 * J + c4]);
-#pragma unroll
-          for (int x = 0; x < 16; x += 2) {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              m0[e] = fmaf(av[x >> 2][x & 3], tb[x][e], m0[e]);
-              m1[e] = fmaf(av[(x + 1) >> 2][(x + 1) & 3], tb[x + 1][e], m1[e]);
-            }
+          for (int s4 = 0; s4 < 4; ++s4) {
+            a[s4] = As[16 * I + ln][16 * Kb + 4 * s4 + lk];
+            b[s4] = Ti[16 * Kb + 4 * s4 + lk][16 * J + ln];
           }
+#pragma unroll
+          for (int s4 = 0; s4 < 4; ++s4) m = __builtin_amdgcn_mfma_f32_16x16x4f32(a[s4], b[s4], m, 0, 0, 0);
         }
-        *reinterpret_cast<f32x4*>(&Ms[wave][r][c4]) = m0 + m1;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) Ms[wave][4 * lk + i][ln] = m[i];
         wave_lds_sync();  // Ms is written and read by this wave only
-        f32x4 tv0 = {0.0f, 0.0f, 0.0f, 0.0f}, tv1 = tv0;
+        f32x4 tv = {0.0f, 0.0f, 0.0f, 0.0f};
         {
-          f32x4 av[4], mb[16];
+          float a[4], b[4];
 #pragma unroll
-          for (int q = 0; q < 4; ++q) av[q] = *reinterpret_cast<const f32x4*>(&Ti[16 * I + r][16 * I + 4 * q]);
-#pragma unroll
-          for (int x = 0; x < 16; ++x) mb[x] = *reinterpret_cast<const f32x4*>(&Ms[wave][x][c4]);
-#pragma unroll
-          for (int x = 0; x < 16; x += 2) {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              tv0[e] = fmaf(-av[x >> 2][x & 3], mb[x][e], tv0[e]);
-              tv1[e] = fmaf(-av[(x + 1) >> 2][(x + 1) & 3], mb[x + 1][e], tv1[e]);
-            }
+          for (int s4 = 0; s4 < 4; ++s4) {
+            a[s4] = Ti[16 * I + ln][16 * I + 4 * s4 + lk];
+            b[s4] = Ms[wave][4 * s4 + lk][ln];
           }
+#pragma unroll
+          for (int s4 = 0; s4 < 4; ++s4) tv = __builtin_amdgcn_mfma_f32_16x16x4f32(a[s4], b[s4], tv, 0, 0, 0);
         }
-        const f32x4 tv = tv0 + tv1;
-        *reinterpret_cast<f32x4*>(&Ti[16 * I + r][16 * J + c4]) = tv;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) Ti[16 * I + 4 * lk + i][16 * J + ln] = -tv[i];
       }
       __syncthreads();
     }
@@ -461,6 +474,16 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(const ChunkParams p) {
     const f32x4 b = upper ? z : *reinterpret_cast<const f32x4*>(&Ti[r][cc + 4]);
     split4_store(a, Th + frag_elem(r, cc, CH / 32), Tl + frag_elem(r, cc, CH / 32));
     split4_store(b, Th + frag_elem(r, cc + 4, CH / 32), Tl + frag_elem(r, cc + 4, CH / 32));
+  }
+  // the gates' record entries (only the scan reads them)
+  if (wave == 0) {
+    const uint64_t u = __builtin_bit_cast(uint64_t, L_lane);
+    const uint32_t lo = __builtin_amdgcn_readlane(static_cast<int>(u), 63);
+    const uint32_t hi = __builtin_amdgcn_readlane(static_cast<int>(u >> 32), 63);
+    const double LC = __builtin_bit_cast(double, (static_cast<uint64_t>(hi) << 32) | lo);
+    reinterpret_cast<float*>(rec + kOffGam)[lane] = expf(static_cast<float>(L_lane));
+    reinterpret_cast<float*>(rec + kOffE)[lane] = expf(static_cast<float>(LC - L_lane));
+    reinterpret_cast<float*>(rec + kOffBeta)[lane] = b_lane;
   }
 }
 
