@@ -143,3 +143,29 @@ def test_kt_sources_agree_bitwise():
         y1, S1 = chunked(one, one["state"])
         assert torch.equal(y1[0], y2[b]), f"row {b}: y"
         assert torch.equal(S1[0], S2[b]), f"row {b}: state"
+
+
+@pytest.mark.parametrize("gate_dtype,param_dtype", [("f32", "f32"), ("f16", "bf16"), ("bf16", "f16")])
+def test_runtime_typed_gates(gate_dtype, param_dtype):
+    """a / b and A_log / dt_bias in other dtypes than the bf16 / fp32 pair
+    (runtime-typed gate loads), against the oracle."""
+    d = draw(310, 2, 150, 2, 4, 128, 128)
+    t, r = to_torch(d, DEV, gate_dtype=gate_dtype, param_dtype=param_dtype)
+    y, S = chunked(t, t["state"])
+    y_ref, S_ref = oracle_heads(r, [0, 1, 2, 3], 4, 2, r["state"])
+    assert row_errs_y(y.float().cpu().numpy(), y_ref).max() <= Y_TOL
+    assert head_errs_state(S.cpu().numpy(), S_ref).max() <= STATE_TOL
+
+
+def test_precomputed_gates():
+    """g and beta given (fp32), through a prepared chunked launch."""
+    d = draw(311, 2, 150, 2, 4, 128, 128)
+    t, r = to_torch(d, DEV)
+    g = mx.compute_g(t["A_log"], t["a"], t["dt_bias"]).float()
+    beta = mx.compute_beta(t["b"]).float()
+    plan = mx.prepare_chunked(t["q"], t["k"], t["v"], g, beta, None, None, t["state"], gates_precomputed=True)
+    plan.launch()
+    y, S = plan.outputs
+    y_ref, S_ref = oracle_heads(r, [0, 1, 2, 3], 4, 2, r["state"])
+    assert row_errs_y(y.float().cpu().numpy(), y_ref).max() <= Y_TOL
+    assert head_errs_state(S.cpu().numpy(), S_ref).max() <= STATE_TOL
