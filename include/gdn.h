@@ -170,6 +170,37 @@ int gdn_chunk_fwd(const void* q, const void* k, const void* v, int qkv_dtype,
                   void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * The two phases of gdn_chunk_fwd, enqueued separately (same arguments, same
+ * checks): gdn_chunk_prep writes the per-chunk records into the workspace
+ * (every chunk in parallel; reads q, k and the gates, not the state), and
+ * gdn_chunk_scan runs the state chain over them and writes y and state_out.
+ * A scan must follow the prep of the same arguments and workspace on the
+ * caller's streams.  The split lets a serving step place HBM-bound work (the
+ * decode / verify / commit launches of other rows) beside the scan, which
+ * leaves HBM mostly idle, instead of beside the prep, which is itself bound
+ * by HBM.  No reference counterpart beyond gdn_chunk_fwd's: only where the
+ * caller places the two launches changes.
+ */
+int gdn_chunk_prep(const void* q, const void* k, const void* v, int qkv_dtype,
+                   int gate_mode, const void* gx, const void* gy, int gate_dtype,
+                   int64_t gate_stride,
+                   const void* A_log, const void* dt_bias, int param_dtype,
+                   const float* state_in, void* y, float* state_out,
+                   const int32_t* state_index, int64_t n_slots,
+                   const int32_t* cu_seqlens, int64_t n_seqs, int64_t n_tok,
+                   int64_t Hk, int64_t Hv, int64_t Dk, int64_t Dv, int64_t chunk,
+                   void* workspace, size_t workspace_bytes, void* stream);
+int gdn_chunk_scan(const void* q, const void* k, const void* v, int qkv_dtype,
+                   int gate_mode, const void* gx, const void* gy, int gate_dtype,
+                   int64_t gate_stride,
+                   const void* A_log, const void* dt_bias, int param_dtype,
+                   const float* state_in, void* y, float* state_out,
+                   const int32_t* state_index, int64_t n_slots,
+                   const int32_t* cu_seqlens, int64_t n_seqs, int64_t n_tok,
+                   int64_t Hk, int64_t Hv, int64_t Dk, int64_t Dv, int64_t chunk,
+                   void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * Fused mixer prologue of GatedDeltaNet (dflash.py:351-370): mask zeroing,
  * concat(conv_state, qkv), depthwise causal conv1d with Kt taps (no bias),
  * SiLU, split into q | k | v, q = rms_norm(q)/Dk, k = rms_norm(k)/sqrt(Dk)

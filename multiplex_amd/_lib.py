@@ -36,6 +36,8 @@ EXPORTS = (
     "gdn_recurrent",
     "gdn_chunk_workspace_bytes",
     "gdn_chunk_fwd",
+    "gdn_chunk_prep",
+    "gdn_chunk_scan",
     "gdn_conv_prologue",
     "gdn_conv_state_commit",
     "gdn_gated_rmsnorm",
@@ -107,6 +109,16 @@ _SIGNATURES = {
     "gdn_recurrent": (c_int, [POINTER(RecurrentArgs)]),
     "gdn_chunk_workspace_bytes": (c_size_t, [_I64, _I64, _I64, _I64, _I64, _I64]),
     "gdn_chunk_fwd": (
+        c_int,
+        [_P, _P, _P, c_int, c_int, _P, _P, c_int, _I64, _P, _P, c_int, _P, _P, _P, _P, _I64, _P,
+         _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P, c_size_t, _P],
+    ),
+    "gdn_chunk_prep": (
+        c_int,
+        [_P, _P, _P, c_int, c_int, _P, _P, c_int, _I64, _P, _P, c_int, _P, _P, _P, _P, _I64, _P,
+         _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P, c_size_t, _P],
+    ),
+    "gdn_chunk_scan": (
         c_int,
         [_P, _P, _P, c_int, c_int, _P, _P, c_int, _I64, _P, _P, c_int, _P, _P, _P, _P, _I64, _P,
          _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P, c_size_t, _P],

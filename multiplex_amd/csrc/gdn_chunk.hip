@@ -843,15 +843,19 @@ extern "C" size_t gdn_chunk_workspace_bytes(int64_t n_seqs, int64_t n_tok, int64
   return static_cast<size_t>(chunks) * static_cast<size_t>(Hv) * kRecBytes;
 }
 
-extern "C" int gdn_chunk_fwd(const void* q, const void* k, const void* v, int qkv_dtype,
-                             int gate_mode, const void* gx, const void* gy, int gate_dtype,
-                             int64_t gate_stride,
-                             const void* A_log, const void* dt_bias, int param_dtype,
-                             const float* state_in, void* y, float* state_out,
-                             const int32_t* state_index, int64_t n_slots,
-                             const int32_t* cu_seqlens, int64_t n_seqs, int64_t n_tok, int64_t Hk,
-                             int64_t Hv, int64_t Dk, int64_t Dv, int64_t chunk, void* workspace,
-                             size_t workspace_bytes, void* stream) {
+namespace {
+
+constexpr unsigned kPhasePrep = 1, kPhaseScan = 2;
+
+// Validates the arguments and enqueues the phases selected by `phases`
+// (the same checks for every phase, so a prep and a scan issued separately
+// with the same arguments see the same records).
+int chunk_fwd(const void* q, const void* k, const void* v, int qkv_dtype, int gate_mode, const void* gx,
+              const void* gy, int gate_dtype, int64_t gate_stride, const void* A_log, const void* dt_bias,
+              int param_dtype, const float* state_in, void* y, float* state_out, const int32_t* state_index,
+              int64_t n_slots, const int32_t* cu_seqlens, int64_t n_seqs, int64_t n_tok, int64_t Hk, int64_t Hv,
+              int64_t Dk, int64_t Dv, int64_t chunk, void* workspace, size_t workspace_bytes, void* stream,
+              unsigned phases) {
   using gdn_host::fail;
   if (chunk != CH) return fail(GDN_ERR_UNSUPPORTED, "gdn_chunk_fwd: chunk must be 64 (got %lld)", (long long)chunk);
   if (qkv_dtype != GDN_DTYPE_BF16) return fail(GDN_ERR_UNSUPPORTED, "gdn_chunk_fwd: q/k/v must be bf16");
@@ -919,7 +923,7 @@ extern "C" int gdn_chunk_fwd(const void* q, const void* k, const void* v, int qk
   // More scan workgroups than CUs (several per CU): K^T from LDS (fewer
   // operand bytes per CU); else the record's K^T (a shorter chain per chunk).
   const bool kt_lds = static_cast<int64_t>(kTiles) * n_seqs * Hv > kCUs;
-  if (chunks > 0) {
+  if ((phases & kPhasePrep) && chunks > 0) {
     const dim3 grid(static_cast<unsigned>(chunks * Hv));
     if (kt_lds) hipLaunchKernelGGL(chunk_prep_kernel<true>, grid, dim3(256), 0, st, p);
     else hipLaunchKernelGGL(chunk_prep_kernel<false>, grid, dim3(256), 0, st, p);
@@ -929,8 +933,28 @@ extern "C" int gdn_chunk_fwd(const void* q, const void* k, const void* v, int qk
   // whole GQA units per XCD (a unit never spans two sequences: Hv % group == 0)
   const int64_t heads = n_seqs * Hv, unit = Hv / Hk;
   const int64_t scan_blocks = kTiles * kXcds * unit * ((heads + kXcds * unit - 1) / (kXcds * unit));
+  if (!(phases & kPhaseScan)) return GDN_OK;
   const dim3 sgrid(static_cast<unsigned>(scan_blocks));
   if (kt_lds) hipLaunchKernelGGL(chunk_scan_kernel<true>, sgrid, dim3(256), 0, st, p);
   else hipLaunchKernelGGL(chunk_scan_kernel<false>, sgrid, dim3(256), 0, st, p);
   return gdn_host::check_launch("gdn_chunk_fwd/scan");
 }
+
+}  // namespace
+
+#define GDN_CHUNK_PARAMS                                                                                        \
+  const void *q, const void *k, const void *v, int qkv_dtype, int gate_mode, const void *gx, const void *gy,   \
+      int gate_dtype, int64_t gate_stride, const void *A_log, const void *dt_bias, int param_dtype,             \
+      const float *state_in, void *y, float *state_out, const int32_t *state_index, int64_t n_slots,            \
+      const int32_t *cu_seqlens, int64_t n_seqs, int64_t n_tok, int64_t Hk, int64_t Hv, int64_t Dk, int64_t Dv, \
+      int64_t chunk, void *workspace, size_t workspace_bytes, void *stream
+#define GDN_CHUNK_ARGS                                                                                        \
+  q, k, v, qkv_dtype, gate_mode, gx, gy, gate_dtype, gate_stride, A_log, dt_bias, param_dtype, state_in, y,   \
+      state_out, state_index, n_slots, cu_seqlens, n_seqs, n_tok, Hk, Hv, Dk, Dv, chunk, workspace,           \
+      workspace_bytes, stream
+
+extern "C" int gdn_chunk_fwd(GDN_CHUNK_PARAMS) { return chunk_fwd(GDN_CHUNK_ARGS, kPhasePrep | kPhaseScan); }
+
+extern "C" int gdn_chunk_prep(GDN_CHUNK_PARAMS) { return chunk_fwd(GDN_CHUNK_ARGS, kPhasePrep); }
+
+extern "C" int gdn_chunk_scan(GDN_CHUNK_PARAMS) { return chunk_fwd(GDN_CHUNK_ARGS, kPhaseScan); }

@@ -38,6 +38,7 @@ __all__ = [
     "prepare_chunked",
     "PreparedRecurrent",
     "PreparedCall",
+    "PreparedChunked",
     "CHUNK_MIN_TOKENS",
 ]
 
@@ -444,6 +445,32 @@ class PreparedCall:
             _lib.check(self._fn_name, st)
 
 
+class PreparedChunked(PreparedCall):
+    """A prepared chunked prefill: ``launch()`` enqueues both phases; the
+    phases can also be enqueued apart (``launch_prep`` then ``launch_scan``,
+    in that order on the caller's streams), so a serving step can run
+    HBM-bound launches of other rows beside the scan rather than beside the
+    HBM-bound prep."""
+
+    def __init__(self, fn: str, args: tuple, keep: dict, outputs: tuple, dev):
+        super().__init__(fn, args, keep, outputs, dev)
+        lib = _lib.load()
+        self._prep = lib.gdn_chunk_prep
+        self._scan = lib.gdn_chunk_scan
+
+    def _issue(self, fn, name, stream):
+        args = self._args if stream is None else self._args[:-1] + (_stream_handle(stream),)
+        st = fn(*args)
+        if st != _lib.OK:
+            _lib.check(name, st)
+
+    def launch_prep(self, stream=None):
+        self._issue(self._prep, "gdn_chunk_prep", stream)
+
+    def launch_scan(self, stream=None):
+        self._issue(self._scan, "gdn_chunk_scan", stream)
+
+
 def _chunk_args(q, k, v, gx, gy, gate_mode, A_log, dt_bias, state, *, cu_seqlens=None,
                 state_out=None, workspace=None, state_index=None):
     names = ["q", "k", "v", "a/g", "b/beta", "A_log", "dt_bias", "state", "state_out"]
@@ -487,7 +514,7 @@ def _chunked(q, k, v, gx, gy, gate_mode, A_log, dt_bias, state, *, cu_seqlens=No
 
 
 def prepare_chunked(q, k, v, a, b, A_log, dt_bias, state=None, *, cu_seqlens=None, state_out=None,
-                    workspace=None, gates_precomputed=False, state_index=None) -> PreparedCall:
+                    workspace=None, gates_precomputed=False, state_index=None) -> "PreparedChunked":
     """Validates a chunked prefill once; ``launch()`` re-issues it.
 
     Same arguments as :func:`gated_delta_update` with ``chunked=True``;
@@ -502,7 +529,7 @@ def prepare_chunked(q, k, v, a, b, A_log, dt_bias, state=None, *, cu_seqlens=Non
         if keep[name].data_ptr() != {"q": q, "k": k, "v": v, "gx": a, "gy": b}[name].data_ptr():
             raise ValueError(f"{name} must be contiguous (gates: or one-stride column slices) for a prepared launch")
     keep.update(y=y_t, state_out=out_state)
-    return PreparedCall("gdn_chunk_fwd", args, keep, (y_t, out_state), dev)
+    return PreparedChunked("gdn_chunk_fwd", args, keep, (y_t, out_state), dev)
 
 
 def _use_chunked(chunked, k, mask, cu_seqlens, T):

@@ -169,3 +169,26 @@ def test_precomputed_gates():
     y_ref, S_ref = oracle_heads(r, [0, 1, 2, 3], 4, 2, r["state"])
     assert row_errs_y(y.float().cpu().numpy(), y_ref).max() <= Y_TOL
     assert head_errs_state(S.cpu().numpy(), S_ref).max() <= STATE_TOL
+
+
+def test_prep_and_scan_launched_apart():
+    """The two phases enqueued separately (the scan on another stream, after
+    an event) equal the one-call launch bit for bit."""
+    d = draw(312, 1, 300, 2, 4, 128, 128)
+    t, _ = to_torch(d, DEV)
+    cu = torch.tensor([0, 70, 70, 300], dtype=torch.int32)
+    st = torch.tensor(np.random.default_rng(10).normal(0.0, 0.02, (3, 4, 128, 128)), dtype=torch.float32,
+                      device=DEV)
+    y_ref, S_ref = chunked(t, st, cu=cu)
+    plan = mx.prepare_chunked(t["q"], t["k"], t["v"], t["a"], t["b"], t["A_log"], t["dt_bias"], st,
+                              cu_seqlens=cu)
+    main, side = torch.cuda.current_stream(), torch.cuda.Stream()
+    done = torch.cuda.Event()
+    plan.launch_prep(main)
+    done.record(main)
+    side.wait_event(done)
+    plan.launch_scan(side)
+    main.wait_stream(side)
+    torch.cuda.synchronize()
+    y, S = plan.outputs
+    assert torch.equal(y, y_ref) and torch.equal(S, S_ref)
