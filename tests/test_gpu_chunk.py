@@ -47,6 +47,20 @@ def test_short_sequences_match_oracle(T):
     assert head_errs_state(S.cpu().numpy(), S_ref).max() <= STATE_TOL
 
 
+@pytest.mark.parametrize("B,Hk,Hv", [(2, 4, 4), (2, 2, 6), (2, 1, 4), (3, 12, 12), (3, 4, 12), (3, 3, 12)])
+def test_gqa_groups_match_oracle(B, Hk, Hv):
+    """GQA groups of 1, 3 and 4 v-heads per k-head (the other tests use 2).
+    The scan deals whole groups to an XCD and the prep writes a k-head's K, Q
+    and K^T records once per group; B=3 with Hv=12 is 288 scan workgroups,
+    so K^T then comes from transposed LDS reads."""
+    d = draw(320 + 16 * B + Hk + Hv, B, 150, Hk, Hv, 128, 128)
+    t, r = to_torch(d, DEV)
+    y, S = chunked(t, t["state"])
+    y_ref, S_ref = oracle_heads(r, list(range(Hv)), Hv, Hk, r["state"])
+    assert row_errs_y(y.float().cpu().numpy(), y_ref).max() <= Y_TOL
+    assert head_errs_state(S.cpu().numpy(), S_ref).max() <= STATE_TOL
+
+
 def test_prefill_4096_full_heads_subset_oracle():
     # One long sequence at the prefill shape: B=1, T=4096, Hk=16, Hv=32, zero state.
     d = draw(1003, 1, 4096, 16, 32, 128, 128, state=False)
@@ -79,14 +93,17 @@ def test_packed_prefills_with_prefix_states():
     assert head_errs_state(S[:, heads].cpu().numpy(), S_ref).max() <= STATE_TOL
 
 
-def test_ragged_packed_small():
+@pytest.mark.parametrize("Hk,Hv", [(2, 4), (2, 6), (3, 12)])
+def test_ragged_packed_small(Hk, Hv):
+    """Five packed sequences (one empty, one of a single token); GQA groups 2,
+    3 and 4 (Hv=12: 480 scan workgroups, K^T from transposed LDS reads)."""
     lens = [70, 0, 1, 128, 63]
     cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
-    d = draw(305, 1, int(cu[-1]), 2, 4, 128, 128, state=False)
+    d = draw(305 + Hv, 1, int(cu[-1]), Hk, Hv, 128, 128, state=False)
     t, r = to_torch(d, DEV)
-    S0 = np.random.default_rng(6).normal(0, 0.02, (len(lens), 4, 128, 128)).astype(np.float32)
+    S0 = np.random.default_rng(6).normal(0, 0.02, (len(lens), Hv, 128, 128)).astype(np.float32)
     y, S = chunked(t, torch.tensor(S0, device=DEV), cu=cu)
-    y_ref, S_ref = oracle_heads(r, [0, 1, 2, 3], 4, 2, S0.astype(np.float64), cu=cu)
+    y_ref, S_ref = oracle_heads(r, list(range(Hv)), Hv, Hk, S0.astype(np.float64), cu=cu)
     assert rel_err(y.float().cpu().numpy(), y_ref) <= Y_TOL
     assert head_errs_state(S.cpu().numpy(), S_ref).max() <= STATE_TOL
     np.testing.assert_array_equal(S[1].cpu().numpy(), S0[1])
