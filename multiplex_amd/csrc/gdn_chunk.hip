@@ -234,8 +234,12 @@ __device__ __forceinline__ void wave_lds_sync() {
 }
 
 // KT_LDS: the scan forms K^T from K in LDS, so the record carries no K^T.
+// Four workgroups per CU: 40.7 KB of LDS each and at most 128 VGPRs (four
+// waves per SIMD; left to itself the compiler takes 137-138, which leaves
+// three).  At 4096 tokens x 32 heads the 2048 workgroups then run in two
+// full rounds instead of two and two thirds.
 template <bool KT_LDS>
-__global__ __launch_bounds__(256) void chunk_prep_kernel(const ChunkParams p) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void chunk_prep_kernel(const ChunkParams p) {
   // work index = chunk * Hv + hv: both v-heads of a k-head (GQA) share an XCD
   const int w = xcd_work_index();
   const int c = w / p.Hv;
@@ -248,7 +252,7 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(const ChunkParams p) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
   const int lr = lane & 15, lq = lane >> 4, lg8 = lq * 8;
 
-  // Two 17 KB buffers, each reused once (LDS stays under 53 KB, so three
+  // Two 17 KB buffers, each reused once (LDS stays under 40 KB, so four
   // workgroups fit on a CU):  buf0 = K rows, then A;  buf1 = Q rows, then
   // the P hi/lo planes in fragment order, then (I + A)^{-1}.
   constexpr int kBuf = CH * KP * 2;
