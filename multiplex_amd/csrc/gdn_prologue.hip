@@ -14,7 +14,10 @@ namespace {
 
 using namespace gdn;
 
-constexpr int kRun = 16;   // tokens per wavefront (prefill)
+// Tokens per wavefront (prefill).  8 keeps the kernel at 109 VGPRs, four
+// waves per SIMD (16 took 142, three), and re-reads the 3-row window once
+// per 8 tokens (from L2).
+constexpr int kRun = 8;
 constexpr int kWaves = 4;  // wavefronts per workgroup (consecutive runs)
 constexpr int KT = 4;      // conv taps
 
