@@ -84,7 +84,12 @@ struct ChunkParams {
   int T;              // tokens per sequence when cu == null
   int Hk, Hv, group;
   unsigned char* ws;
+  int32_t* order;     // [n_seqs] packed sequences longest first (in the workspace), or null
 };
+
+// Packed calls of 2..kOrderMax sequences order them by length, so the scan
+// deals the longest chains out first; above that, sequence order.
+constexpr int kOrderMax = 1024;
 
 __device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
@@ -148,15 +153,25 @@ struct SeqRange {
 __device__ __forceinline__ int n_chunks(int len) { return (len + CH - 1) / CH; }
 
 // Workgroups are dispatched to the 8 XCDs round-robin by linear block id.
-// This maps block id -> work index so that each XCD gets one contiguous
-// range of work indices (whose consumers of the same data then share that
-// XCD's L2).  Identity when the grid does not split evenly.
-__device__ __forceinline__ int xcd_work_index() {
+// This maps block id (below n, the number of work blocks) -> work index so
+// that each XCD gets one contiguous range of work indices (whose consumers
+// of the same data then share that XCD's L2).  Identity when n does not
+// split evenly.
+__device__ __forceinline__ int xcd_work_index(int n) {
   constexpr int kXcds = 8;
-  const int n = gridDim.x, b = blockIdx.x;
+  const int b = blockIdx.x;
   if (n % kXcds != 0) return b;
   return (b % kXcds) * (n / kXcds) + b / kXcds;
 }
+
+// Chunk slots of packed sequences.  Sequence n owns the slots from
+// cu[n] / CH + n on: with cu[n] = aC + r and a length of bC + s,
+// a + ceil((bC + s) / C) <= floor(((a + b)C + r + s) / C) + 1, so the slots
+// of consecutive sequences never overlap, and the last one is below
+// n_tok / CH + n_seqs (the workspace bound).  A sequence's first slot is
+// then one load away, with no sum over the sequences before it; the slots
+// a sequence leaves unused hold no record.
+__device__ __forceinline__ int first_slot(const ChunkParams& p, int n) { return p.cu[n] / CH + n; }
 
 __device__ __forceinline__ SeqRange seq_range(const ChunkParams& p, int n) {
   SeqRange r;
@@ -166,11 +181,9 @@ __device__ __forceinline__ SeqRange seq_range(const ChunkParams& p, int n) {
     r.chunk0 = n * n_chunks(p.T);
     return r;
   }
-  int base = 0;
-  for (int m = 0; m < n; ++m) base += n_chunks(p.cu[m + 1] - p.cu[m]);
   r.tok0 = p.cu[n];
   r.len = p.cu[n + 1] - p.cu[n];
-  r.chunk0 = base;
+  r.chunk0 = first_slot(p, n);
   return r;
 }
 
@@ -184,19 +197,39 @@ __device__ __forceinline__ bool chunk_at(const ChunkParams& p, int c, int64_t& t
     len = min(CH, p.T - i * CH);
     return true;
   }
-  int base = 0;
-  for (int n = 0; n < p.n_seqs; ++n) {
-    const int l = p.cu[n + 1] - p.cu[n];
-    const int nc = n_chunks(l);
-    if (c < base + nc) {
-      const int i = c - base;
-      tok0 = p.cu[n] + static_cast<int64_t>(i) * CH;
-      len = min(CH, l - i * CH);
-      return true;
-    }
-    base += nc;
+  // the last sequence whose first slot is at or below c (first slots
+  // increase with n), by bisection
+  int lo = 0, hi = p.n_seqs - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (first_slot(p, mid) <= c) lo = mid;
+    else hi = mid - 1;
   }
-  return false;
+  const int l = p.cu[lo + 1] - p.cu[lo];
+  const int i = c - first_slot(p, lo);
+  if (i < 0 || i >= n_chunks(l)) return false;  // a slot no sequence uses
+  tok0 = p.cu[lo] + static_cast<int64_t>(i) * CH;
+  len = min(CH, l - i * CH);
+  return true;
+}
+
+// Writes p.order: the packed sequences by length, longest first (ties by
+// index).  One workgroup: each thread ranks sequences tid, tid + 256, ...
+// against all the others, whose lengths it reads from LDS (`lens`, room for
+// kOrderMax).
+__device__ void order_sequences(const ChunkParams& p, int* lens) {
+  const int n = p.n_seqs;
+  for (int i = threadIdx.x; i < n; i += blockDim.x) lens[i] = p.cu[i + 1] - p.cu[i];
+  __syncthreads();
+  for (int i = threadIdx.x; i < n; i += blockDim.x) {
+    const int li = lens[i];
+    int r = 0;
+    for (int m = 0; m < n; ++m) {
+      const int lm = lens[m];
+      r += (lm > li) || (lm == li && m < i);
+    }
+    p.order[r] = i;
+  }
 }
 
 // ------------------------------------------------------------ chunk_prep
@@ -240,8 +273,22 @@ __device__ __forceinline__ void wave_lds_sync() {
 // full rounds instead of two and two thirds.
 template <bool KT_LDS>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void chunk_prep_kernel(const ChunkParams p) {
+  // Two 17 KB buffers, each reused once (LDS stays under 40 KB, so four
+  // workgroups fit on a CU):  buf0 = K rows, then A;  buf1 = Q rows, then
+  // the P hi/lo planes in fragment order, then (I + A)^{-1}.  The extra last
+  // workgroup of a packed call orders the sequences in buf0 instead.
+  constexpr int kBuf = CH * KP * 2;
+  static_assert(kBuf == CH * (CH + 4) * 4, "A and T must fill the K / Q buffers exactly");
+  static_assert(kBuf >= 2 * CH * CH * 2, "P staging must fit in the Q buffer");
+  static_assert(kBuf >= kOrderMax * 4, "the sequence lengths must fit in buf0");
+  __shared__ __align__(16) unsigned char buf0[kBuf];
+  __shared__ __align__(16) unsigned char buf1[kBuf];
+  if (p.order != nullptr && blockIdx.x == gridDim.x - 1) {
+    order_sequences(p, reinterpret_cast<int*>(buf0));
+    return;
+  }
   // work index = chunk * Hv + hv: both v-heads of a k-head (GQA) share an XCD
-  const int w = xcd_work_index();
+  const int w = xcd_work_index(gridDim.x - (p.order != nullptr ? 1 : 0));
   const int c = w / p.Hv;
   const int hv = w % p.Hv;
   int64_t tok0;
@@ -252,14 +299,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void c
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
   const int lr = lane & 15, lq = lane >> 4, lg8 = lq * 8;
 
-  // Two 17 KB buffers, each reused once (LDS stays under 40 KB, so four
-  // workgroups fit on a CU):  buf0 = K rows, then A;  buf1 = Q rows, then
-  // the P hi/lo planes in fragment order, then (I + A)^{-1}.
-  constexpr int kBuf = CH * KP * 2;
-  static_assert(kBuf == CH * (CH + 4) * 4, "A and T must fill the K / Q buffers exactly");
-  static_assert(kBuf >= 2 * CH * CH * 2, "P staging must fit in the Q buffer");
-  __shared__ __align__(16) unsigned char buf0[kBuf];
-  __shared__ __align__(16) unsigned char buf1[kBuf];
   __shared__ __align__(16) float Ms[4][16][20];
   __shared__ double Ld[CH];
   __shared__ float Bs[CH];
@@ -546,22 +585,6 @@ struct ChunkBufs {
   const float* gam;      // gamma of this head's record
 };
 
-// Rank of sequence n when sequences are ordered by length, longest first
-// (ties by index); used to start the longest chains first.
-__device__ __forceinline__ int seq_by_rank(const ChunkParams& p, int rank) {
-  if (p.cu == nullptr || p.n_seqs > 256) return rank;
-  for (int n = 0; n < p.n_seqs; ++n) {
-    const int ln = p.cu[n + 1] - p.cu[n];
-    int r = 0;
-    for (int m = 0; m < p.n_seqs; ++m) {
-      const int lm = p.cu[m + 1] - p.cu[m];
-      r += (lm > ln) || (lm == ln && m < n);
-    }
-    if (r == rank) return n;
-  }
-  return rank;
-}
-
 constexpr int kTiles = DV / DVT;  // state-row tiles per head (8)
 constexpr int kXcds = 8;
 constexpr int kCUs = 256;  // compute units of an MI355X (8 XCDs x 32)
@@ -583,7 +606,7 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(const ChunkParams p) {
   const int slot_x = r8 / kTiles;  // head slot on this XCD
   const int head_rank = ((slot_x / p.group) * kXcds + xcd) * p.group + slot_x % p.group;
   if (head_rank >= p.n_seqs * p.Hv) return;
-  const int seq = seq_by_rank(p, head_rank / p.Hv);
+  const int seq = p.order != nullptr ? p.order[head_rank / p.Hv] : head_rank / p.Hv;
   int slot = seq;
   if (p.state_index != nullptr) {
     slot = p.state_index[seq];
@@ -830,6 +853,12 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(const ChunkParams p) {
     *reinterpret_cast<f32x4*>(p.state_out + srow * DK + 32 * wave + 16 * j + 4 * lq) = sacc[j];
 }
 
+// Bytes of the records (every chunk slot of a packed call, which bounds the
+// unpacked count too); the sequence order follows them.
+size_t record_bytes(int64_t n_seqs, int64_t n_tok, int64_t Hv);
+
+bool ordered(int64_t n_seqs) { return n_seqs > 1 && n_seqs <= kOrderMax; }
+
 int64_t max_chunks(int64_t n_seqs, int64_t n_tok, bool packed) {
   if (packed) return (n_tok + CH - 1) / CH + n_seqs;
   if (n_seqs == 0) return 0;
@@ -843,11 +872,15 @@ extern "C" size_t gdn_chunk_workspace_bytes(int64_t n_seqs, int64_t n_tok, int64
                                             int64_t Dv, int64_t chunk) {
   if (chunk != CH || Dk != DK || Dv != DV || n_seqs < 0 || n_tok < 0 || Hv <= 0) return 0;
   // Sized for packed sequences (an upper bound of the unpacked count too).
-  const int64_t chunks = max_chunks(n_seqs, n_tok, true);
-  return static_cast<size_t>(chunks) * static_cast<size_t>(Hv) * kRecBytes;
+  const size_t order = ordered(n_seqs) ? (static_cast<size_t>(n_seqs) * 4 + 255) / 256 * 256 : 0;
+  return record_bytes(n_seqs, n_tok, Hv) + order;
 }
 
 namespace {
+
+size_t record_bytes(int64_t n_seqs, int64_t n_tok, int64_t Hv) {
+  return static_cast<size_t>(max_chunks(n_seqs, n_tok, true)) * static_cast<size_t>(Hv) * kRecBytes;
+}
 
 constexpr unsigned kPhasePrep = 1, kPhaseScan = 2;
 
@@ -893,7 +926,7 @@ int chunk_fwd(const void* q, const void* k, const void* v, int qkv_dtype, int ga
   if (!gdn_host::aligned(workspace, 256) || !gdn_host::aligned(q, 16) || !gdn_host::aligned(k, 16) ||
       !gdn_host::aligned(v, 16) || !gdn_host::aligned(state_in, 16) || !gdn_host::aligned(state_out, 16))
     return fail(GDN_ERR_INVALID, "gdn_chunk_fwd: misaligned pointer");
-  if (n_tok > INT32_MAX / 2 || n_seqs > 65535 || Hv > 65535 || max_chunks(n_seqs, n_tok, packed) * Hv > INT32_MAX ||
+  if (n_tok > INT32_MAX / 2 || n_seqs > 65535 || Hv > 65535 || max_chunks(n_seqs, n_tok, packed) * Hv >= INT32_MAX ||
       (DV / DVT) * (Hv * n_seqs + 8 * (Hv / Hk)) > INT32_MAX)
     return fail(GDN_ERR_UNSUPPORTED, "gdn_chunk_fwd: problem too large");
 
@@ -921,6 +954,7 @@ int chunk_fwd(const void* q, const void* k, const void* v, int qkv_dtype, int ga
   p.Hv = static_cast<int>(Hv);
   p.group = static_cast<int>(Hv / Hk);
   p.ws = static_cast<unsigned char*>(workspace);
+  p.order = packed && ordered(n_seqs) ? reinterpret_cast<int32_t*>(p.ws + record_bytes(n_seqs, n_tok, Hv)) : nullptr;
 
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int64_t chunks = max_chunks(n_seqs, n_tok, packed);
@@ -928,7 +962,8 @@ int chunk_fwd(const void* q, const void* k, const void* v, int qkv_dtype, int ga
   // operand bytes per CU); else the record's K^T (a shorter chain per chunk).
   const bool kt_lds = static_cast<int64_t>(kTiles) * n_seqs * Hv > kCUs;
   if ((phases & kPhasePrep) && chunks > 0) {
-    const dim3 grid(static_cast<unsigned>(chunks * Hv));
+    // one workgroup per (chunk slot, v-head), and one more that orders packed sequences
+    const dim3 grid(static_cast<unsigned>(chunks * Hv + (p.order != nullptr ? 1 : 0)));
     if (kt_lds) hipLaunchKernelGGL(chunk_prep_kernel<true>, grid, dim3(256), 0, st, p);
     else hipLaunchKernelGGL(chunk_prep_kernel<false>, grid, dim3(256), 0, st, p);
     const int rc = gdn_host::check_launch("gdn_chunk_fwd/prep");

@@ -154,6 +154,24 @@ def test_workspace_size_is_monotone(lib):
     assert lib.gdn_chunk_workspace_bytes(1, 64, 32, 128, 128, 32) == 0  # unsupported chunk
 
 
+def test_workspace_holds_records_and_sequence_order(lib):
+    """One record per (chunk slot, v-head): a packed call numbers sequence n's
+    slots from cu[n] / 64 + n, so n_tok / 64 + n_seqs slots bound every
+    packing.  2..1024 packed sequences add their longest-first order (int32,
+    rounded up to 256 B) after the records."""
+    rec = lib.gdn_chunk_workspace_bytes(1, 64, 4, 128, 128, 64) // (4 * 2)  # 1 + 1 slots
+    assert rec % 256 == 0
+
+    def slots(n_seqs, n_tok):
+        return -(-n_tok // 64) + n_seqs
+
+    assert lib.gdn_chunk_workspace_bytes(1, 4096, 4, 128, 128, 64) == slots(1, 4096) * 4 * rec
+    assert lib.gdn_chunk_workspace_bytes(3, 300, 4, 128, 128, 64) == slots(3, 300) * 4 * rec + 256
+    assert lib.gdn_chunk_workspace_bytes(100, 300, 4, 128, 128, 64) == slots(100, 300) * 4 * rec + 512
+    assert lib.gdn_chunk_workspace_bytes(1024, 2048, 4, 128, 128, 64) == slots(1024, 2048) * 4 * rec + 4096
+    assert lib.gdn_chunk_workspace_bytes(1025, 2048, 4, 128, 128, 64) == slots(1025, 2048) * 4 * rec
+
+
 def test_python_rejects_host_tensors():
     import multiplex_amd as mx
 

@@ -109,6 +109,33 @@ def test_ragged_packed_small(Hk, Hv):
     np.testing.assert_array_equal(S[1].cpu().numpy(), S0[1])
 
 
+def test_many_ragged_packed_sequences():
+    """96 packed sequences of 0-200 tokens: the prep's extra workgroup orders
+    them longest first for the scan, and each sequence's chunk slots start at
+    cu[n] / 64 + n; against the oracle."""
+    lens = np.random.default_rng(11).integers(0, 201, 96)
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    d = draw(331, 1, int(cu[-1]), 1, 2, 128, 128, state=False)
+    t, r = to_torch(d, DEV)
+    S0 = np.random.default_rng(12).normal(0, 0.02, (len(lens), 2, 128, 128)).astype(np.float32)
+    y, S = chunked(t, torch.tensor(S0, device=DEV), cu=cu)
+    y_ref, S_ref = oracle_heads(r, [0, 1], 2, 1, S0.astype(np.float64), cu=cu)
+    assert rel_err(y.float().cpu().numpy(), y_ref) <= Y_TOL
+    assert head_errs_state(S.cpu().numpy(), S_ref).max() <= STATE_TOL
+
+
+def test_packed_beyond_ordering_limit_matches_unpacked():
+    """1100 packed sequences (above the 1024 that are ordered by length, so in
+    sequence order) against the same rows unpacked: bit-identical."""
+    n, L = 1100, 3
+    d = draw(332, n, L, 1, 2, 128, 128)
+    t, _ = to_torch(d, DEV)
+    y_u, S_u = chunked(t, t["state"])
+    flat = {k: (v.reshape(1, n * L, *v.shape[2:]) if k in ("q", "k", "v", "a", "b") else v) for k, v in t.items()}
+    y_p, S_p = chunked(flat, t["state"], cu=torch.arange(0, n * L + 1, L, dtype=torch.int32))
+    assert torch.equal(y_p.reshape(y_u.shape), y_u) and torch.equal(S_p, S_u)
+
+
 def test_strong_decay_is_finite_and_exact():
     d = draw(306, 1, 256, 2, 4, 128, 128)
     d["a"][:] = 4.0
