@@ -38,7 +38,11 @@ struct ProParams {
 };
 
 // Locates (sequence, first token, length, run) of this workgroup.  Packed
-// mode walks cu_seqlens: sequence n owns max(1, ceil(len/(R*4))) run slots.
+// mode: sequence n owns max(1, ceil(len / RW)) run slots (one even when
+// empty: its wave passes the conv state through), from cu[n] / RW + n on.
+// With cu[n] = a RW + r, those end at or below floor(cu[n+1] / RW) + n + 1,
+// the next sequence's first slot, and all lie below n_tok / RW + n_seqs (the
+// grid); a workgroup finds its sequence by bisection.
 template <int R>
 __device__ __forceinline__ bool locate(const ProParams& p, int& seq, int64_t& start, int& len,
                                        int& run) {
@@ -50,18 +54,21 @@ __device__ __forceinline__ bool locate(const ProParams& p, int& seq, int64_t& st
     len = p.S;
     return true;
   }
-  for (int n = 0; n < p.n_seqs; ++n) {
-    const int l = p.cu_seqlens[n + 1] - p.cu_seqlens[n];
-    const int runs = l > 0 ? (l + RW - 1) / RW : 1;
-    if (run < runs) {
-      seq = n;
-      start = p.cu_seqlens[n];
-      len = l;
-      return true;
-    }
-    run -= runs;
+  auto first_run = [&](int n) { return p.cu_seqlens[n] / RW + n; };
+  int lo = 0, hi = p.n_seqs - 1;  // the last sequence whose first slot is at or below run
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (first_run(mid) <= run) lo = mid;
+    else hi = mid - 1;
   }
-  return false;
+  const int l = p.cu_seqlens[lo + 1] - p.cu_seqlens[lo];
+  const int i = run - first_run(lo);
+  if (i < 0 || i >= (l > 0 ? (l + RW - 1) / RW : 1)) return false;  // a slot no sequence uses
+  seq = lo;
+  start = p.cu_seqlens[lo];
+  len = l;
+  run = i;
+  return true;
 }
 
 // W32: conv taps are fp32 (else they share the io dtype DT).  MASK: a token

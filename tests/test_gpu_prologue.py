@@ -87,6 +87,17 @@ def test_packed_sequences():
     check(qkv, w, cs, None, 2, 4, 128, cu=cu)
 
 
+def test_many_packed_sequences():
+    """300 packed sequences of 0-40 tokens (empty ones too): each workgroup
+    finds its sequence by bisection over cu_seqlens; against the oracle."""
+    lens = np.random.default_rng(27).integers(0, 41, 300)
+    lens[[0, 150, 299]] = 0
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    qkv, w, _, _ = draw_prologue(28, 1, int(cu[-1]), 1, 2, 64)
+    cs = torch.tensor(np.random.default_rng(3).standard_normal((len(lens), 3, qkv.shape[-1]))).to(torch.bfloat16)
+    check(qkv, w, cs, None, 1, 2, 64, cu=cu)
+
+
 @pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
 def test_io_dtypes_with_fp32_taps_and_partial_head_group(dtype):
     # 2*1 + 1 = 3 heads of 128 channels: a wavefront covers 4 heads, so one
