@@ -181,6 +181,16 @@ def bench_verify(torch, mx, dev, timer, iters=50):
                                   y=False, commit_len=n_b, state_out=torch.empty_like(d["state"]))
     snap = mx.prepare_recurrent(d["q"], d["k"], d["v"], d["a"], d["b"], d["A_log"], d["dt_bias"], d["state"],
                                 write_state=False, snapshots=True)
+    # The commit folded into the next round (gated_delta_commit_verify): one
+    # launch over [this round's drafts, the next round's drafts], the rejected
+    # drafts masked, the state written after this round's tokens.
+    nxt = draw(gen, B, T, torch, dev, state=False)
+    cat = {n: torch.cat([d[n], nxt[n]], dim=1).contiguous() for n in ("q", "k", "v", "a", "b")}
+    keep = torch.cat([torch.arange(T, device=dev)[None, :] < n_b[:, None],
+                      torch.ones(B, T, dtype=torch.bool, device=dev)], dim=1)
+    fused = mx.prepare_recurrent(cat["q"], cat["k"], cat["v"], cat["a"], cat["b"], d["A_log"], d["dt_bias"],
+                                 d["state"], keep, commit_len=torch.full((B,), T, dtype=torch.int32, device=dev),
+                                 state_out=torch.empty_like(d["state"]))
 
     def round_commit(i):
         verify.launch()
@@ -189,13 +199,17 @@ def bench_verify(torch, mx, dev, timer, iters=50):
     for _ in range(5):
         round_commit(0)
         snap.launch()
+        fused.launch()
     t_commit = timer.total_ms(round_commit, iters) / iters
     t_verify, _ = timer.per_launch_ms(lambda i: verify.launch(), iters)
     t_snap = timer.total_ms(lambda i: snap.launch(), iters) / iters
+    t_fused = timer.total_ms(lambda i: fused.launch(), iters) / iters
     credited = 2 * state_bytes(B) + io_bytes(B, T)
     return dict(ms_verify_plus_commit=t_commit, ms_verify=t_verify, ms_snapshot_verify=t_snap,
                 credited_bytes=credited, gbs=credited / (t_commit * 1e-3) / 1e9,
-                frac=credited / (t_commit * 1e-3) / 1e9 / HBM_PEAK_GBS)
+                frac=credited / (t_commit * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                ms_commit_verify_one_pass=t_fused, gbs_one_pass=credited / (t_fused * 1e-3) / 1e9,
+                frac_one_pass=credited / (t_fused * 1e-3) / 1e9 / HBM_PEAK_GBS)
 
 
 def bench_prefill(torch, mx, dev, timer, iters=50):

@@ -12,6 +12,7 @@ from .gated_delta import (
     compute_beta,
     compute_g,
     gated_delta_commit,
+    gated_delta_commit_verify,
     gated_delta_kernel,
     gated_delta_ops,
     gated_delta_update,
@@ -45,6 +46,7 @@ __all__ = [
     "compute_g",
     "conv_state_commit",
     "gated_delta_commit",
+    "gated_delta_commit_verify",
     "gated_delta_kernel",
     "gated_delta_ops",
     "gated_delta_update",

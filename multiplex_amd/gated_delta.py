@@ -33,6 +33,7 @@ __all__ = [
     "gated_delta_update",
     "gated_delta_verify",
     "gated_delta_commit",
+    "gated_delta_commit_verify",
     "chunk_workspace_bytes",
     "prepare_recurrent",
     "prepare_chunked",
@@ -632,3 +633,38 @@ def gated_delta_commit(k, v, a, b, A_log, dt_bias, state, n_commit: IntSeq, mask
                          y=False, state_out=state_out, cu_seqlens=cu_seqlens, commit_len=commit,
                          state_index=state_index)
     return s
+
+
+def gated_delta_commit_verify(prev, n_prev: IntSeq, q, k, v, a, b, A_log, dt_bias, state, mask=None, *,
+                              state_out=None, state_index=None):
+    """Commit of the previous verify round and verify of the next, in one pass over the state.
+
+    ``prev`` is ``(q, k, v, a, b)`` of the previous round's T_p draft tokens
+    (``[B, T_p, ...]``), of which ``n_prev[b]`` were accepted (clamped to
+    ``[0, T_p]``).  The result equals :func:`gated_delta_commit` of ``prev``
+    with ``n_prev`` followed by :func:`gated_delta_verify` of the new tokens
+    from the committed state -- the rollback replay of ``engine.py:337-359``
+    folded into the next round -- but the state is read once and the committed
+    state written once, where a verify and a commit read it twice.  One launch
+    steps ``[prev tokens, new tokens]`` per row with the rejected previous
+    tokens masked (a masked token leaves the state unchanged, the mlx-lm rule)
+    and writes the state after the previous round's tokens.  ``mask``
+    (``[B, T]``) masks new tokens.  ``state_out`` may be ``state``.
+
+    Returns ``(y [B, T, Hv, Dv] of the new tokens, committed state)``.
+    """
+    qp, kp, vp, ap, bp = prev
+    dev = _require_device([q, k, v, a, b, qp, kp, vp, ap, bp, state], ["q", "k", "v", "a", "b", "prev q",
+                                                                       "prev k", "prev v", "prev a", "prev b",
+                                                                       "state"])
+    B, Tp = kp.shape[0], kp.shape[1]
+    if k.shape[0] != B:
+        raise ValueError(f"the new round has {k.shape[0]} rows, the previous one {B}")
+    n = _int_rows(n_prev, B, dev, "n_prev").clamp(0, Tp)
+    keep = torch.arange(Tp, device=dev)[None, :] < n[:, None]
+    new = torch.ones(B, k.shape[1], dtype=torch.bool, device=dev) if mask is None else mask.to(dev, torch.bool)
+    cat = [torch.cat([x0, x1], dim=1) for x0, x1 in ((qp, q), (kp, k), (vp, v), (ap, a), (bp, b))]
+    commit = torch.full((B,), Tp, dtype=torch.int32, device=dev)
+    y, s, _ = _recurrent(*cat, _lib.GATES_RAW, A_log, dt_bias, state, torch.cat([keep, new], dim=1),
+                         state_out=state_out, commit_len=commit, state_index=state_index)
+    return y[:, Tp:], s

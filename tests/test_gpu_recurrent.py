@@ -296,3 +296,35 @@ def test_ops_path_on_device_matches_kernel():
     y_ref, S_ref = oracle_update(r)
     assert_close(y2, S2, y_ref, S_ref)
     assert rel_err(S1.cpu().numpy(), S2.cpu().numpy()) < 1e-5
+
+
+@pytest.mark.parametrize("Tp,T", [(4, 4), (3, 5)])
+def test_commit_verify_is_commit_then_verify(Tp, T):
+    """One pass over the state: the commit of the previous round's accepted
+    drafts (n_prev clamped to [0, Tp]) and the verify of the next round's."""
+    d = draw(90 + Tp, 6, Tp + T, 2, 4, 128, 128)
+    t, r = to_torch(d, DEV)
+    part = lambda lo, hi: tuple(t[n][:, lo:hi].contiguous() for n in ("q", "k", "v", "a", "b"))
+    prev, new = part(0, Tp), part(Tp, Tp + T)
+    n_prev = [0, 1, Tp, 2, -1, Tp + 3]
+    y, S = mx.gated_delta_commit_verify(prev, n_prev, *new, t["A_log"], t["dt_bias"], t["state"])
+    S_c = mx.gated_delta_commit(*prev[1:], t["A_log"], t["dt_bias"], t["state"],
+                                [min(max(n, 0), Tp) for n in n_prev])
+    assert torch.equal(S, S_c)
+    y_v, _ = mx.gated_delta_verify(*new, t["A_log"], t["dt_bias"], S_c)
+    assert row_errs_y(y.float().cpu().numpy(), y_v.float().cpu().numpy()).max() <= Y_TOL
+    # the same against the oracle: the committed prefix, then the new tokens
+    g = gdn.compute_g(r["A_log"], r["a"], r["dt_bias"])
+    beta = gdn.compute_beta(r["b"])
+    for b_, n in enumerate(n_prev):
+        n = min(max(n, 0), Tp)
+        idx = list(range(n)) + list(range(Tp, Tp + T))
+        hk = [h // 2 for h in range(4)]
+        y_ref, S_ref = gdn.recurrent(r["q"][b_:b_ + 1, idx][:, :, hk], r["k"][b_:b_ + 1, idx][:, :, hk],
+                                     r["v"][b_:b_ + 1, idx], g[b_:b_ + 1, idx], beta[b_:b_ + 1, idx],
+                                     r["state"][b_:b_ + 1])
+        assert row_errs_y(y[b_:b_ + 1].float().cpu().numpy(), y_ref[:, n:]).max() <= Y_TOL
+    assert head_errs_state(S_c.cpu().numpy()[5:6], gdn.recurrent(
+        r["q"][5:6, :Tp][:, :, [0, 0, 1, 1]], r["k"][5:6, :Tp][:, :, [0, 0, 1, 1]], r["v"][5:6, :Tp],
+        g[5:6, :Tp], beta[5:6, :Tp], r["state"][5:6])[1]).max() <= STATE_TOL
+
