@@ -298,10 +298,12 @@ def test_ops_path_on_device_matches_kernel():
     assert rel_err(S1.cpu().numpy(), S2.cpu().numpy()) < 1e-5
 
 
-@pytest.mark.parametrize("Tp,T", [(4, 4), (3, 5)])
+@pytest.mark.parametrize("Tp,T", [(4, 4), (3, 5), (1, 1), (4, 6)])
 def test_commit_verify_is_commit_then_verify(Tp, T):
     """One pass over the state: the commit of the previous round's accepted
-    drafts (n_prev clamped to [0, Tp]) and the verify of the next round's."""
+    drafts (n_prev clamped to [0, Tp]) and the verify of the next round's.
+    The launch steps the tile kernel, as the commit does, so the committed
+    state is bit-identical to the commit's."""
     d = draw(90 + Tp, 6, Tp + T, 2, 4, 128, 128)
     t, r = to_torch(d, DEV)
     part = lambda lo, hi: tuple(t[n][:, lo:hi].contiguous() for n in ("q", "k", "v", "a", "b"))
@@ -324,6 +326,9 @@ def test_commit_verify_is_commit_then_verify(Tp, T):
                                      r["v"][b_:b_ + 1, idx], g[b_:b_ + 1, idx], beta[b_:b_ + 1, idx],
                                      r["state"][b_:b_ + 1])
         assert row_errs_y(y[b_:b_ + 1].float().cpu().numpy(), y_ref[:, n:]).max() <= Y_TOL
+    st = t["state"].clone()
+    y2, S2 = mx.gated_delta_commit_verify(prev, n_prev, *new, t["A_log"], t["dt_bias"], st, state_out=st)
+    assert S2.data_ptr() == st.data_ptr() and torch.equal(S2, S) and torch.equal(y2, y)
     assert head_errs_state(S_c.cpu().numpy()[5:6], gdn.recurrent(
         r["q"][5:6, :Tp][:, :, [0, 0, 1, 1]], r["k"][5:6, :Tp][:, :, [0, 0, 1, 1]], r["v"][5:6, :Tp],
         g[5:6, :Tp], beta[5:6, :Tp], r["state"][5:6])[1]).max() <= STATE_TOL
