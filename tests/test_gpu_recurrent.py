@@ -329,6 +329,13 @@ def test_commit_verify_is_commit_then_verify(Tp, T):
     st = t["state"].clone()
     y2, S2 = mx.gated_delta_commit_verify(prev, n_prev, *new, t["A_log"], t["dt_bias"], st, state_out=st)
     assert S2.data_ptr() == st.data_ptr() and torch.equal(S2, S) and torch.equal(y2, y)
+    # pooled states: row b in slot idx[b], updated in place
+    idx = torch.tensor([5, 0, 7, 2, 3, 6], dtype=torch.int32, device=DEV)
+    pool = torch.zeros(8, *t["state"].shape[1:], device=DEV)
+    pool[idx.long()] = t["state"]
+    y3, _ = mx.gated_delta_commit_verify(prev, n_prev, *new, t["A_log"], t["dt_bias"], pool, state_index=idx)
+    assert torch.equal(pool[idx.long()], S) and torch.equal(y3, y)
+    assert not pool[[1, 4]].any()
     assert head_errs_state(S_c.cpu().numpy()[5:6], gdn.recurrent(
         r["q"][5:6, :Tp][:, :, [0, 0, 1, 1]], r["k"][5:6, :Tp][:, :, [0, 0, 1, 1]], r["v"][5:6, :Tp],
         g[5:6, :Tp], beta[5:6, :Tp], r["state"][5:6])[1]).max() <= STATE_TOL
