@@ -539,7 +539,7 @@ def main():
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
-        print("bench.py measures one GPU: this build's path runs on a single MI355X "
+        print("bench.py measures one GPU: the GDN path runs on a single MI355X "
               "(multi-GPU sharding is design-only); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
     if args.steps < 1:
