@@ -138,6 +138,10 @@ def test_chunk_rejects_bad_arguments(lib):
     assert call(n_seqs=0, n_tok=0) == _lib.OK
     assert call(index=FAKE, n_slots=-1) == _lib.ERR_INVALID
     assert call(g_ld=16) == _lib.ERR_INVALID       # below Hv
+    # packed sequences: the workspace must also hold their order after the records
+    need = lib.gdn_chunk_workspace_bytes(3, 4096, 32, 128, 128, 64)
+    assert call(cu=FAKE, n_seqs=3, ws_bytes=need - 256) == _lib.ERR_INVALID
+    assert "workspace" in _lib.last_error()
 
 
 def test_recurrent_rejects_bad_pool_size(lib):
