@@ -326,6 +326,14 @@ def test_commit_verify_is_commit_then_verify(Tp, T):
                                      r["v"][b_:b_ + 1, idx], g[b_:b_ + 1, idx], beta[b_:b_ + 1, idx],
                                      r["state"][b_:b_ + 1])
         assert row_errs_y(y[b_:b_ + 1].float().cpu().numpy(), y_ref[:, n:]).max() <= Y_TOL
+    # a mask on the new drafts: masked ones leave the state alone and give y = 0
+    m = torch.rand(6, T, generator=torch.Generator().manual_seed(Tp + T)) >= 0.3
+    y_m, S_m = mx.gated_delta_commit_verify(prev, n_prev, *new, t["A_log"], t["dt_bias"], t["state"],
+                                            m.to(DEV))
+    assert torch.equal(S_m, S)
+    y_vm, _ = mx.gated_delta_verify(*new, t["A_log"], t["dt_bias"], S_c, m.to(DEV))
+    assert not y_m[~m.to(DEV)].any()
+    assert row_errs_y(y_m.float().cpu().numpy(), y_vm.float().cpu().numpy()).max() <= Y_TOL
     st = t["state"].clone()
     y2, S2 = mx.gated_delta_commit_verify(prev, n_prev, *new, t["A_log"], t["dt_bias"], st, state_out=st)
     assert S2.data_ptr() == st.data_ptr() and torch.equal(S2, S) and torch.equal(y2, y)
