@@ -566,6 +566,15 @@ __device__ __forceinline__ f32x4 buf_f32x4(BufRsrc r, uint32_t voff) {
   return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, 0, 0));
 }
 
+// Lane I of each group of four lanes, to all four (DPP quad_perm [I,I,I,I]).
+// The lanes of a quad need the same four per-token values: one 4-byte load
+// per lane (value lr % 4) and these moves replace a 16-byte load per lane,
+// which would fetch each value 16 times.
+template <int I>
+__device__ __forceinline__ float quad_bcast(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), I * 0x55, 0xF, 0xF, false));
+}
+
 // One wave's operands of one chunk (all in MFMA operand layouts).
 struct WaveOps {
   bf16x8 k[4], q[4];     // K / Q rows 16w + lr, columns 32s + 8lq ..
@@ -573,7 +582,7 @@ struct WaveOps {
   bf16x8 ph[2], pl[2];   // P rows, same layout
   bf16x8 kt[2][2];       // K^T rows 32w + 16j + lr, columns 32s + 8lq ..
   uint16_t v[4];         // V[16w + 4lq + i][dv0 + lr] (bf16 bits)
-  f32x4 g, b, e;         // gamma / beta / e of tokens 16w + 4lq + i
+  f32x4 g, b, e;         // gamma / beta / e of tokens 16w + 4lq + i (KT_LDS: .x of token 16w + 4lq + lr % 4)
   float gy;              // gamma of token 16w + lr
   float gC;              // gamma of the chunk's last token
 };
@@ -641,6 +650,7 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(const ChunkParams p) {
   const uint32_t off_rows = rec_hv + (2 * wave * 64 + lane) * 16;        // T, P rows 16w + lr
   const uint32_t off_kt = rec_hk + kOffKT + (4 * wave * 64 + lane) * 16;  // K^T rows 32w + 16j + lr
   const uint32_t off_g4 = rec_hv + kOffGam + (16 * wave + 4 * lq) * 4;
+  const uint32_t off_gq = off_g4 + (lr & 3) * 4;
   const uint32_t off_g1 = rec_hv + kOffGam + (16 * wave + lr) * 4;
 
   // Bases of the chunk whose descriptors come next, advanced by one chunk at
@@ -678,8 +688,13 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(const ChunkParams p) {
     static_for<4>([&](auto i) {
       o.v[i.value] = __builtin_amdgcn_raw_buffer_load_b16(c.v, off_v[i.value], 0, 0);
     });
-    o.g = buf_f32x4(c.rec, off_g4);
-    o.b = buf_f32x4(c.rec, off_g4 + (kOffBeta - kOffGam));
+    if constexpr (KT_LDS) {
+      o.g.x = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(c.rec, off_gq, 0, 0));
+      o.b.x = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(c.rec, off_gq + (kOffBeta - kOffGam), 0, 0));
+    } else {
+      o.g = buf_f32x4(c.rec, off_g4);
+      o.b = buf_f32x4(c.rec, off_g4 + (kOffBeta - kOffGam));
+    }
     o.gy = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(c.rec, off_g1, 0, 0));
   };
   // T and P are lower triangular: the rows of waves 0 and 1 (tokens < 32)
@@ -695,7 +710,19 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(const ChunkParams p) {
       }
     });
   };
-  auto load_e = [&](const ChunkBufs& c) { o.e = buf_f32x4(c.rec, off_g4 + (kOffE - kOffGam)); };
+  auto load_e = [&](const ChunkBufs& c) {
+    if constexpr (KT_LDS)
+      o.e.x = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(c.rec, off_gq + (kOffE - kOffGam), 0, 0));
+    else
+      o.e = buf_f32x4(c.rec, off_g4 + (kOffE - kOffGam));
+  };
+  // Value i of a per-token gate vector: with several workgroups per CU the
+  // texture path is the bottleneck and the quad broadcasts pay; with one,
+  // they lengthen the chain.
+  auto tok4 = [&](const f32x4& x, auto i) {
+    if constexpr (KT_LDS) return quad_bcast<decltype(i)::value>(x.x);
+    else return x[i.value];
+  };
   auto load_kt = [&](const ChunkBufs& c) {
     if constexpr (!KT_LDS) {
       static_for<2>([&](auto j) {
@@ -774,7 +801,7 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(const ChunkParams p) {
     {
       f32x4 r;
       static_for<4>([&](auto i) {
-        r[i.value] = o.b[i.value] * (bf16_to_f32(o.v[i.value]) - o.g[i.value] * (xk0[i.value] + xk1[i.value]));
+        r[i.value] = tok4(o.b, i) * (bf16_to_f32(o.v[i.value]) - tok4(o.g, i) * (xk0[i.value] + xk1[i.value]));
       });
       split4_store(r, &Rh[lr][16 * wave + 4 * lq], &Rl[lr][16 * wave + 4 * lq]);
     }
@@ -809,7 +836,9 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(const ChunkParams p) {
     {
       const f32x4 uv = u0 + u1;
       split4_store(uv, &Uh[lr][16 * wave + 4 * lq], &Ul[lr][16 * wave + 4 * lq]);
-      split4_store(o.e * uv, &Eh[lr][16 * wave + 4 * lq], &El[lr][16 * wave + 4 * lq]);
+      const f32x4 ev = {tok4(o.e, std::integral_constant<int, 0>{}), tok4(o.e, std::integral_constant<int, 1>{}),
+                        tok4(o.e, std::integral_constant<int, 2>{}), tok4(o.e, std::integral_constant<int, 3>{})};
+      split4_store(ev * uv, &Eh[lr][16 * wave + 4 * lq], &El[lr][16 * wave + 4 * lq]);
     }
     load_e(cn);
     __syncthreads();  // U^T, (eU)^T complete
