@@ -128,6 +128,22 @@ def read_traffic(name):
     return vals["fetch_bytes_per_launch"] + vals["write_bytes_per_launch"]
 
 
+def read_kernel_avg_us(name, kernel_prefix):
+    """Average duration (us) of a kernel in a committed rocprofv3 summary
+    table (``| kernel | calls | average (ns) | ...``), or None."""
+    p = ROOT / "profiles" / name
+    if not p.exists():
+        return None
+    for line in p.read_text().splitlines():
+        cells = [c.strip() for c in line.strip().strip("|").split("|")]
+        if len(cells) >= 3 and cells[0].startswith(kernel_prefix):
+            try:
+                return float(cells[2]) / 1e3
+            except ValueError:
+                continue
+    return None
+
+
 # ------------------------------------------------------------- workloads
 
 def bench_decode_b64(torch, mx, dev, steps, warmup, timer):
@@ -253,11 +269,20 @@ def bench_prefill(torch, mx, dev, timer, iters=50):
                 flops=flops, finite=bool(torch.isfinite(out["S"]).all()))
 
 
+def mixed_bytes(lens, n_dec=48, n_ver=16, t_ver=4):
+    """Credited HBM bytes of the mixed step: the packed prefills' I/O and
+    prefix states (read + written), the decode rows' states and I/O, and the
+    verify rows' state read + one committed write and I/O."""
+    n_seq = len(lens)
+    prefill = io_bytes(1, sum(lens)) + 2 * state_bytes(n_seq)
+    return prefill, decode_bytes(n_dec) + 2 * state_bytes(n_ver) + io_bytes(n_ver, t_ver)
+
+
 def bench_mixed(torch, mx, dev, timer, iters=50):
-    """One continuous-batching step: the packed prefills run on the current
-    stream; the decode, verify and commit launches (independent rows and
-    states) run on a second stream beside the prefill's scan, once its prep
-    is done; the step ends when both streams are done."""
+    """One continuous-batching step (``multiplex_amd.MixedStep``): the packed
+    prefills' prep and scan on the current stream; the decode, verify and
+    commit launches (independent rows and states) on a second stream beside
+    the scan, once the prep is done; the step ends when both are done."""
     gen = torch.Generator().manual_seed(1004)
     lens = [1024, 2560, 7168]
     n_tok = sum(lens)
@@ -268,41 +293,47 @@ def bench_mixed(torch, mx, dev, timer, iters=50):
     ver = draw(gen, 16, 4, torch, dev)
     n_b = torch.randint(1, 5, (16,), generator=gen, dtype=torch.int32).to(dev)
     ws = torch.empty(mx.chunk_workspace_bytes(3, n_tok, Hv, Dk, Dv), dtype=torch.uint8, device=dev)
-    main = torch.cuda.current_stream(dev)
-    side = torch.cuda.Stream(dev)  # default priority
-    with torch.cuda.stream(side):
-        dplan = mx.prepare_recurrent(dec["q"], dec["k"], dec["v"], dec["a"], dec["b"], dec["A_log"],
-                                     dec["dt_bias"], dec["state"], state_out=dec["state"])
-        vplan = mx.prepare_recurrent(ver["q"], ver["k"], ver["v"], ver["a"], ver["b"], ver["A_log"],
-                                     ver["dt_bias"], ver["state"], write_state=False)
-        cplan = mx.prepare_recurrent(None, ver["k"], ver["v"], ver["a"], ver["b"], ver["A_log"], ver["dt_bias"],
-                                     ver["state"], y=False, commit_len=n_b, state_out=torch.empty_like(ver["state"]))
-    st_out = torch.empty_like(pf_state)
+    dplan = mx.prepare_recurrent(dec["q"], dec["k"], dec["v"], dec["a"], dec["b"], dec["A_log"],
+                                 dec["dt_bias"], dec["state"], state_out=dec["state"])
+    vplan = mx.prepare_recurrent(ver["q"], ver["k"], ver["v"], ver["a"], ver["b"], ver["A_log"],
+                                 ver["dt_bias"], ver["state"], write_state=False)
+    cplan = mx.prepare_recurrent(None, ver["k"], ver["v"], ver["a"], ver["b"], ver["A_log"], ver["dt_bias"],
+                                 ver["state"], y=False, commit_len=n_b, state_out=torch.empty_like(ver["state"]))
     pplan = mx.prepare_chunked(pf["q"], pf["k"], pf["v"], pf["a"], pf["b"], pf["A_log"], pf["dt_bias"], pf_state,
-                               cu_seqlens=cu, workspace=ws, state_out=st_out)
-
-    prep_done = torch.cuda.Event()
-
-    def step(i):
-        # the HBM-bound decode / verify / commit launches run beside the scan,
-        # which leaves HBM mostly idle, not beside the HBM-bound prep
-        pplan.launch_prep(main)
-        prep_done.record(main)
-        pplan.launch_scan(main)
-        side.wait_event(prep_done)
-        dplan.launch(side)
-        vplan.launch(side)
-        cplan.launch(side)
-        main.wait_stream(side)
+                               cu_seqlens=cu, workspace=ws, state_out=torch.empty_like(pf_state))
+    step = mx.MixedStep(pplan, [dplan, vplan, cplan])
 
     for _ in range(3):
-        step(0)
-    t = timer.total_ms(step, iters) / iters
+        step.launch()
+    t = timer.total_ms(lambda i: step.launch(), iters) / iters
+    t_serial = timer.total_ms(lambda i: step.launch_serial(), iters) / iters
     flops = prefill_flops(lens)
-    hbm = decode_bytes(48) + 2 * state_bytes(16) + io_bytes(16, 4)
+    pf_bytes, dv_bytes = mixed_bytes(lens)
+    hbm = pf_bytes + dv_bytes
+    bound_ms = max(flops / (MFMA_BF16_PEAK_TFLOPS * 1e12), hbm / (HBM_PEAK_GBS * 1e9)) * 1e3
     toks = n_tok + 48 + 64
-    return dict(ms=t, tokens_per_s=toks / (t * 1e-3), prefill_gflop=flops / 1e9, decode_verify_bytes=hbm,
-                streams=2)
+    return dict(ms=t, ms_one_stream=t_serial, tokens_per_s=toks / (t * 1e-3), prefill_gflop=flops / 1e9,
+                prefill_bytes=pf_bytes, decode_verify_bytes=dv_bytes,
+                mfma_frac=round(flops / (t * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
+                hbm_frac=round(hbm / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                lower_bound_ms=round(bound_ms, 5), bound_frac=round(bound_ms / t, 4), streams=2)
+
+
+def bench_decode_past_mall(torch, mx, dev, timer, B=256, steps=50):
+    """Decode at B=256: a 512 MiB state, twice the 256 MB last-level cache
+    (MALL), so no step can be served from it; GB/s as for B=64."""
+    gen = torch.Generator().manual_seed(1011)
+    d = draw(gen, B, 1, torch, dev)
+    plan = mx.prepare_recurrent(d["q"], d["k"], d["v"], d["a"], d["b"], d["A_log"], d["dt_bias"], d["state"],
+                                state_out=d["state"])
+    for _ in range(5):
+        plan.launch()
+    t = timer.total_ms(lambda i: plan.launch(), steps) / steps
+    gbs = decode_bytes(B) / (t * 1e-3) / 1e9
+    del d, plan
+    torch.cuda.empty_cache()
+    return dict(B=B, state_bytes=state_bytes(B), ms_per_step=round(t, 5), gbs=round(gbs, 1),
+                hbm_frac=round(gbs / HBM_PEAK_GBS, 4))
 
 
 def bench_epilogue(torch, mx, dev, timer, iters=50):
@@ -451,17 +482,32 @@ def bench_mixer_layer(torch, mx, dev, timer, iters=20, hidden=2048):
 
 # ------------------------------------------------------------ CPU baseline
 
-def cpu_baseline(torch, budget_s=12.0):
-    """The reference's ops path (fp32 port, oracle/ops_path.py) on host cores.
+def cpu_model_name():
+    """The host CPU's model name (as ``lscpu`` reports it), from /proc/cpuinfo."""
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
 
-    Bounded sample: decode steps at B=64 until ``budget_s`` seconds have
-    passed (at least 2), reported as algorithmic GB/s like ``value``; plus one
-    512-token prefill chunk (the reference's chunk size) for tokens/s.
+
+def cpu_baseline(torch, budget_s=10.0):
+    """The reference's ops path (fp32 port, oracle/ops_path.py) on host cores,
+    with ``os.cpu_count()`` threads.
+
+    Samples: decode steps at B=64 until ``budget_s`` seconds have passed (at
+    least 2), reported as algorithmic GB/s like ``value``; the T=4096 prefill
+    with its conv prologue; 20 decode steps at B=1; one B=32, T=4 verify with
+    the reference's restore + replay rollback; and the mixed step (the three
+    packed prefills run one sequence at a time, since the ops path has no
+    packed form, plus 48 decode rows and 16 verify rows with rollback).
     """
     sys.path.insert(0, str(ROOT))
     from oracle import ops_path
 
-    threads = max(1, min(16, os.cpu_count() or 1))
+    threads = os.cpu_count() or 1
     torch.set_num_threads(threads)
     gen = torch.Generator().manual_seed(1001)
     d = draw(gen, 64, 1, torch, "cpu")
@@ -471,18 +517,23 @@ def cpu_baseline(torch, budget_s=12.0):
         _, S = ops_path.gated_delta_update(d["q"], d["k"], d["v"], d["a"], d["b"], d["A_log"], d["dt_bias"], S)
         done += 1
     dt = (time.perf_counter() - t0) / done
-    gen = torch.Generator().manual_seed(1003)
-    T = 512
-    qkv = torch.randn(1, T, C_DIM, generator=gen).to(torch.bfloat16)
-    w = (torch.randn(C_DIM, KT, generator=gen) * 0.1).to(torch.bfloat16)
-    a = torch.randn(1, T, Hv, generator=gen).to(torch.bfloat16)
-    b = torch.randn(1, T, Hv, generator=gen).to(torch.bfloat16)
-    A_log = torch.rand(Hv, generator=gen) * math.log(16.0)
-    dt_bias = torch.rand(Hv, generator=gen) * 2 - 1
-    t1 = time.perf_counter()
-    q, k, v, _ = ops_path.conv_prologue(qkv, w, Hk, Hv, Dk, Dv, torch.zeros(1, KT - 1, C_DIM))
-    ops_path.gated_delta_update(q, k, v, a, b, A_log, dt_bias, torch.zeros(1, Hv, Dv, Dk))
-    tp = time.perf_counter() - t1
+
+    def prefill(T, seed, state=None):
+        g = torch.Generator().manual_seed(seed)
+        qkv = torch.randn(1, T, C_DIM, generator=g).to(torch.bfloat16)
+        w = (torch.randn(C_DIM, KT, generator=g) * 0.1).to(torch.bfloat16)
+        a = torch.randn(1, T, Hv, generator=g).to(torch.bfloat16)
+        b = torch.randn(1, T, Hv, generator=g).to(torch.bfloat16)
+        A_log = torch.rand(Hv, generator=g) * math.log(16.0)
+        dt_bias = torch.rand(Hv, generator=g) * 2 - 1
+        s0 = torch.zeros(1, Hv, Dv, Dk) if state is None else state
+        t1 = time.perf_counter()
+        q, k, v, _ = ops_path.conv_prologue(qkv, w, Hk, Hv, Dk, Dv, torch.zeros(1, KT - 1, C_DIM))
+        ops_path.gated_delta_update(q, k, v, a, b, A_log, dt_bias, s0)
+        return time.perf_counter() - t1
+
+    T = 4096
+    tp = prefill(T, 1003)
     # decode B=1: median of 20 steps
     gen = torch.Generator().manual_seed(1000)
     d1 = draw(gen, 1, 1, torch, "cpu")
@@ -492,27 +543,42 @@ def cpu_baseline(torch, budget_s=12.0):
         _, S1 = ops_path.gated_delta_update(d1["q"], d1["k"], d1["v"], d1["a"], d1["b"], d1["A_log"], d1["dt_bias"], S1)
         times.append(time.perf_counter() - t2)
     t_b1 = sorted(times)[len(times) // 2]
-    # MTP verify B=32, T=4, then the reference's rollback: restore the
-    # snapshot and replay each row's accepted prefix (engine.py:337-359)
-    gen = torch.Generator().manual_seed(1002)
-    dv = draw(gen, 32, 4, torch, "cpu")
-    n_b = torch.randint(1, 5, (32,), generator=gen)
-    t3 = time.perf_counter()
-    S0 = dv["state"].float().clone()
-    ops_path.gated_delta_update(dv["q"], dv["k"], dv["v"], dv["a"], dv["b"], dv["A_log"], dv["dt_bias"], S0)
-    for n in sorted(set(n_b.tolist())):
-        rows = (n_b == n).nonzero().flatten()
-        sl = lambda t: t[rows][:, :n]
-        ops_path.gated_delta_update(sl(dv["q"]), sl(dv["k"]), sl(dv["v"]), sl(dv["a"]), sl(dv["b"]), dv["A_log"],
-                                    dv["dt_bias"], S0[rows])
-    t_ver = time.perf_counter() - t3
+
+    def verify_rollback(B, seed):
+        # MTP verify at T=4, then the reference's rollback: restore the
+        # snapshot and replay each row's accepted prefix (engine.py:337-359)
+        g = torch.Generator().manual_seed(seed)
+        dv = draw(g, B, 4, torch, "cpu")
+        n_b = torch.randint(1, 5, (B,), generator=g)
+        t3 = time.perf_counter()
+        S0 = dv["state"].float().clone()
+        ops_path.gated_delta_update(dv["q"], dv["k"], dv["v"], dv["a"], dv["b"], dv["A_log"], dv["dt_bias"], S0)
+        for n in sorted(set(n_b.tolist())):
+            rows = (n_b == n).nonzero().flatten()
+            sl = lambda t: t[rows][:, :n]
+            ops_path.gated_delta_update(sl(dv["q"]), sl(dv["k"]), sl(dv["v"]), sl(dv["a"]), sl(dv["b"]), dv["A_log"],
+                                        dv["dt_bias"], S0[rows])
+        return time.perf_counter() - t3
+
+    t_ver = verify_rollback(32, 1002)
+    # the mixed step: prefills of 1024, 2560 and 7168 tokens from prefix
+    # states, 48 decode rows, 16 verify rows with rollback
+    g = torch.Generator().manual_seed(1004)
+    t_mix = sum(prefill(n, 2000 + n, torch.randn(1, Hv, Dv, Dk, generator=g) * 0.02) for n in (1024, 2560, 7168))
+    dd = draw(g, 48, 1, torch, "cpu")
+    t4 = time.perf_counter()
+    ops_path.gated_delta_update(dd["q"], dd["k"], dd["v"], dd["a"], dd["b"], dd["A_log"], dd["dt_bias"],
+                                dd["state"].float())
+    t_mix += time.perf_counter() - t4 + verify_rollback(16, 1005)
+    model = cpu_model_name()
     return dict(value=decode_bytes(64) / dt / 1e9, unit="GB/s", cores=threads, kind="port",
                 sample=f"{done} decode steps at B=64 (ops-path port, fp32, torch CPU), "
-                       f"{dt * 1e3:.1f} ms/step; prefill 512 tokens with conv prologue: {T / tp:.0f} tokens/s; "
+                       f"{dt * 1e3:.1f} ms/step; prefill T=4096 with conv prologue: {T / tp:.0f} tokens/s; "
                        f"decode B=1 {t_b1 * 1e6:.0f} us/step; verify B=32 T=4 + replay rollback {t_ver * 1e3:.1f} ms; "
-                       f"host {platform.processor() or platform.machine()}, {os.cpu_count()} logical cpus",
+                       f"mixed step (1024+2560+7168 prefill, 48 decode, 16 verify + rollback) {t_mix * 1e3:.0f} ms; "
+                       f"{threads} threads on {model}",
                 ms_per_step=dt * 1e3, prefill_tokens_per_s=T / tp, decode_b1_us=t_b1 * 1e6, verify_ms=t_ver * 1e3,
-                cpu=platform.processor() or platform.machine())
+                mixed_ms=t_mix * 1e3, cpu=model)
 
 
 # ------------------------------------------------------------------- main
@@ -611,6 +677,7 @@ def main():
         configs["verify_b32_t4"] = bench_verify(torch, mx, dev, timer)
         configs["prefill_t4096"] = bench_prefill(torch, mx, dev, timer)
         configs["mixed"] = bench_mixed(torch, mx, dev, timer)
+        configs["decode_b256_past_mall"] = bench_decode_past_mall(torch, mx, dev, timer)
         configs["epilogue_gated_rmsnorm"] = bench_epilogue(torch, mx, dev, timer)
         configs["state_pool"] = bench_pool(torch, mx, dev, timer)
         configs["prefix_state"] = bench_prefix_state(torch, mx, dev)
@@ -638,8 +705,11 @@ def main():
         "roofline": {
             "bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": read_traffic("decode_b64_traffic.txt"),
-            "kernel": "recurrent_kernel<128,bf16,GF_IO_F32>", "kernel_ms": round(dec["ms_per_step"], 5),
-            "kernel_ms_event_pairs": round(dec["kernel_ms"], 5),
+            "kernel": "recurrent_kernel<128, bf16, GF_IO_F32>",
+            # achieved = bytes per launch / (event-timed span of the back-to-back launches / launches)
+            "ms_per_launch_event_span": round(dec["ms_per_step"], 5),
+            "ms_per_launch_event_pairs": round(dec["kernel_ms"], 5),
+            "kernel_us_rocprof_committed": read_kernel_avg_us("decode_b64_kernel_trace.md", "recurrent_kernel"),
         },
         "cpu_baseline": None if base is None else {k: base[k] for k in ("value", "unit", "cores", "kind", "sample")},
         "prefill": None,
@@ -650,6 +720,8 @@ def main():
             configs["decode_b1"]["cpu_us_per_step"] = round(base["decode_b1_us"], 1)
         if "verify_b32_t4" in configs:
             configs["verify_b32_t4"]["cpu_ms_verify_plus_rollback"] = round(base["verify_ms"], 2)
+        if "mixed" in configs:
+            configs["mixed"]["cpu_ms"] = round(base["mixed_ms"], 1)
     if "prefill_t4096" in configs:
         p = configs["prefill_t4096"]
         line["prefill"] = {"tokens_per_s": round(p["tokens_per_s"], 1), "ms": round(p["ms_total"], 4),

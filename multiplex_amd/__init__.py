@@ -26,10 +26,12 @@ from .state_pool import PooledBatch, StatePool
 from . import prefix_state
 from .epilogue import gated_rms_norm, prepare_gated_rms_norm
 from .mixer import GatedDeltaNet, commit_verified
+from .mixed_step import MixedStep
 
 __all__ = [
     "ArraysCache",
     "GatedDeltaNet",
+    "MixedStep",
     "PooledBatch",
     "StatePool",
     "clone_ssm",

@@ -81,6 +81,7 @@ struct ChunkParams {
   int n_slots;
   const int32_t* cu;  // [n_seqs + 1] or null
   int n_seqs;
+  int n_tok;          // tokens in all sequences
   int T;              // tokens per sequence when cu == null
   int Hk, Hv, group;
   unsigned char* ws;
@@ -171,7 +172,18 @@ __device__ __forceinline__ int xcd_work_index(int n) {
 // n_tok / CH + n_seqs (the workspace bound).  A sequence's first slot is
 // then one load away, with no sum over the sequences before it; the slots
 // a sequence leaves unused hold no record.
-__device__ __forceinline__ int first_slot(const ChunkParams& p, int n) { return p.cu[n] / CH + n; }
+//
+// Offsets from a device tensor are not validated on the host, so every read
+// of the table clamps: sequence n spans [start(n), end(n)) with
+// start(n) = clamp(cu[n], 0, n_tok) and end(n) = clamp(cu[n+1], start(n), n_tok).
+// A bad table then gives wrong rows, but every token, record and slot index
+// stays within the bounds above.
+__device__ __forceinline__ int cu_start(const ChunkParams& p, int n) { return min(max(p.cu[n], 0), p.n_tok); }
+__device__ __forceinline__ int cu_len(const ChunkParams& p, int n) {
+  const int s = cu_start(p, n);
+  return min(max(p.cu[n + 1], s), p.n_tok) - s;
+}
+__device__ __forceinline__ int first_slot(const ChunkParams& p, int n) { return cu_start(p, n) / CH + n; }
 
 __device__ __forceinline__ SeqRange seq_range(const ChunkParams& p, int n) {
   SeqRange r;
@@ -181,8 +193,8 @@ __device__ __forceinline__ SeqRange seq_range(const ChunkParams& p, int n) {
     r.chunk0 = n * n_chunks(p.T);
     return r;
   }
-  r.tok0 = p.cu[n];
-  r.len = p.cu[n + 1] - p.cu[n];
+  r.tok0 = cu_start(p, n);
+  r.len = cu_len(p, n);
   r.chunk0 = first_slot(p, n);
   return r;
 }
@@ -205,10 +217,10 @@ __device__ __forceinline__ bool chunk_at(const ChunkParams& p, int c, int64_t& t
     if (first_slot(p, mid) <= c) lo = mid;
     else hi = mid - 1;
   }
-  const int l = p.cu[lo + 1] - p.cu[lo];
+  const int l = cu_len(p, lo);
   const int i = c - first_slot(p, lo);
   if (i < 0 || i >= n_chunks(l)) return false;  // a slot no sequence uses
-  tok0 = p.cu[lo] + static_cast<int64_t>(i) * CH;
+  tok0 = cu_start(p, lo) + static_cast<int64_t>(i) * CH;
   len = min(CH, l - i * CH);
   return true;
 }
@@ -219,7 +231,7 @@ __device__ __forceinline__ bool chunk_at(const ChunkParams& p, int c, int64_t& t
 // kOrderMax).
 __device__ void order_sequences(const ChunkParams& p, int* lens) {
   const int n = p.n_seqs;
-  for (int i = threadIdx.x; i < n; i += blockDim.x) lens[i] = p.cu[i + 1] - p.cu[i];
+  for (int i = threadIdx.x; i < n; i += blockDim.x) lens[i] = cu_len(p, i);
   __syncthreads();
   for (int i = threadIdx.x; i < n; i += blockDim.x) {
     const int li = lens[i];
@@ -978,6 +990,7 @@ int chunk_fwd(const void* q, const void* k, const void* v, int qkv_dtype, int ga
   p.n_slots = state_index != nullptr ? static_cast<int>(n_slots) : 0;
   p.cu = cu_seqlens;
   p.n_seqs = static_cast<int>(n_seqs);
+  p.n_tok = static_cast<int>(n_tok);
   p.T = packed ? 0 : static_cast<int>(n_tok / n_seqs);
   p.Hk = static_cast<int>(Hk);
   p.Hv = static_cast<int>(Hv);

@@ -54,18 +54,23 @@ __device__ __forceinline__ bool locate(const ProParams& p, int& seq, int64_t& st
     len = p.S;
     return true;
   }
-  auto first_run = [&](int n) { return p.cu_seqlens[n] / RW + n; };
+  // Offsets from a device tensor are not validated on the host: each
+  // sequence is clamped into [0, S] (S = the packed token count), so a bad
+  // table gives wrong rows but every run slot and token stays in bounds.
+  auto cu_start = [&](int n) { return min(max(p.cu_seqlens[n], 0), p.S); };
+  auto first_run = [&](int n) { return cu_start(n) / RW + n; };
   int lo = 0, hi = p.n_seqs - 1;  // the last sequence whose first slot is at or below run
   while (lo < hi) {
     const int mid = (lo + hi + 1) >> 1;
     if (first_run(mid) <= run) lo = mid;
     else hi = mid - 1;
   }
-  const int l = p.cu_seqlens[lo + 1] - p.cu_seqlens[lo];
+  const int s0 = cu_start(lo);
+  const int l = min(max(p.cu_seqlens[lo + 1], s0), p.S) - s0;
   const int i = run - first_run(lo);
   if (i < 0 || i >= (l > 0 ? (l + RW - 1) / RW : 1)) return false;  // a slot no sequence uses
   seq = lo;
-  start = p.cu_seqlens[lo];
+  start = s0;
   len = l;
   run = i;
   return true;

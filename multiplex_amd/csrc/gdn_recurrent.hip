@@ -112,8 +112,13 @@ __device__ __forceinline__ RowCtx row_ctx(const RecParams& p) {
   c.row = blockIdx.z;
   c.hk = c.hv / p.group;
   if (p.cu_seqlens != nullptr) {
-    c.tok0 = p.cu_seqlens[c.row];
-    c.L = p.cu_seqlens[c.row + 1] - p.cu_seqlens[c.row];
+    // Offsets from a device tensor are not validated on the host: each
+    // sequence is clamped into [0, T] (T = the packed token count), so a bad
+    // table gives wrong rows but never an access outside the buffers.
+    const int start = min(max(p.cu_seqlens[c.row], 0), p.T);
+    const int end = min(max(p.cu_seqlens[c.row + 1], start), p.T);
+    c.tok0 = start;
+    c.L = end - start;
   } else {
     c.tok0 = static_cast<int64_t>(c.row) * p.T;
     c.L = p.T;
@@ -121,8 +126,11 @@ __device__ __forceinline__ RowCtx row_ctx(const RecParams& p) {
   c.write_state = p.state_out != nullptr;
   c.commit = c.L;
   if (p.commit_len != nullptr) {
+    // A negative length skips the row: in place (state_out == state_in) it
+    // is not written at all; into a separate state_out it is copied
+    // unchanged (commit 0), so no output row is left unwritten.
     const int cl = p.commit_len[c.row];
-    if (cl < 0) c.write_state = false;
+    if (cl < 0 && p.state_out == p.state_in) c.write_state = false;
     c.commit = cl < 0 ? 0 : (cl < c.L ? cl : c.L);
   }
   c.want_y = p.y != nullptr;

@@ -179,18 +179,44 @@ def _state_operands(state, state_out, write_state, n_rows, Hv, Dv, Dk, dev, stat
     out_state = None
     if write_state:
         out_state = _out_state(state_out if state_out is not None else state, st_shape, dev, "state_out pool")
-    idx = _int_rows(state_index, n_rows, dev, "state_index")
+    idx = _int_rows(state_index, n_rows, dev, "state_index", unique_slots=write_state)
     return state, out_state, idx, st_shape[0]
 
 
-def _cu_seqlens(cu: Optional[IntSeq], n_tok: int, dev) -> Optional[torch.Tensor]:
-    """Validates packed-sequence offsets on the host and returns them on ``dev``.
+def _upload_i32(host: torch.Tensor, dev) -> torch.Tensor:
+    """An int32 copy of a host tensor on ``dev``, enqueued on the current
+    stream through pinned memory: the host does not wait for the device."""
+    t = host.to(torch.int32).contiguous()
+    if t.numel() == 0:
+        return torch.empty(0, dtype=torch.int32, device=dev)
+    return t.pin_memory().to(dev, non_blocking=True)
 
-    Offsets must start at 0, be non-decreasing and end at ``n_tok``; a device
-    tensor is copied to the host for the check (one synchronisation).
+
+def _is_device(x, dev) -> bool:
+    return isinstance(x, torch.Tensor) and x.device.type == "cuda"
+
+
+def _cu_seqlens(cu: Optional[IntSeq], n_tok: int, dev) -> Optional[torch.Tensor]:
+    """Packed-sequence offsets on ``dev``.
+
+    Host offsets (a list or a CPU tensor) are validated -- they must start at
+    0, be non-decreasing and end at ``n_tok`` -- and uploaded asynchronously.
+    A device tensor is used as it is, with no host copy and so no
+    synchronisation; the kernels clamp every sequence into ``[0, n_tok]``, so
+    a bad device table yields wrong rows but no access outside the buffers.
     """
     if cu is None:
         return None
+    if n_tok >= 2**31:
+        raise ValueError("too many packed tokens")
+    if _is_device(cu, dev):
+        if cu.device != dev:
+            raise ValueError(f"cu_seqlens is on {cu.device}, expected {dev}")
+        if cu.dim() != 1 or cu.numel() < 2:
+            raise ValueError("cu_seqlens must be a 1-D sequence of at least 2 offsets")
+        if cu.dtype != torch.int32 or not cu.is_contiguous():
+            cu = cu.to(torch.int32).contiguous()
+        return cu
     host = torch.as_tensor(cu).to("cpu", torch.int64)
     if host.dim() != 1 or host.numel() < 2:
         raise ValueError("cu_seqlens must be a 1-D sequence of at least 2 offsets")
@@ -198,20 +224,41 @@ def _cu_seqlens(cu: Optional[IntSeq], n_tok: int, dev) -> Optional[torch.Tensor]
         raise ValueError(f"cu_seqlens must start at 0 and end at {n_tok}")
     if bool((host[1:] < host[:-1]).any()):
         raise ValueError("cu_seqlens must be non-decreasing")
-    if n_tok >= 2**31:
-        raise ValueError("too many packed tokens")
-    if isinstance(cu, torch.Tensor) and cu.device == dev and cu.dtype == torch.int32 and cu.is_contiguous():
-        return cu
-    return host.to(torch.int32).to(dev, non_blocking=False)
+    return _upload_i32(host, dev)
 
 
-def _int_rows(x: IntSeq, n: int, dev, what: str) -> torch.Tensor:
-    t = torch.as_tensor(x)
+def _packed_max_len(cu: IntSeq, n_tok: int, max_seqlen: Optional[int]) -> int:
+    """Longest packed sequence, for choosing a kernel: exact for host
+    offsets; for a device table ``max_seqlen`` when given, else the mean
+    length (no device read, so no synchronisation)."""
+    if _is_device(cu, None):
+        if max_seqlen is not None:
+            return int(max_seqlen)
+        n_seqs = cu.numel() - 1
+        return -(-n_tok // n_seqs) if n_seqs > 0 else 0
+    host = torch.as_tensor(cu).to("cpu", torch.int64)
+    return int((host[1:] - host[:-1]).max()) if host.numel() > 1 else 0
+
+
+def _int_rows(x: IntSeq, n: int, dev, what: str, unique_slots: bool = False) -> torch.Tensor:
+    """An int32 ``[n]`` row table on ``dev``.  Host tables are uploaded
+    asynchronously; with ``unique_slots`` (the state slots of a launch that
+    writes them) a host table may not name one slot twice, since two rows
+    writing one slot would race.  Device tables are used as they are."""
+    if _is_device(x, dev):
+        if x.device != dev:
+            raise ValueError(f"{what} is on {x.device}, expected {dev}")
+        if x.dim() != 1 or x.numel() != n:
+            raise ValueError(f"{what} must have {n} entries")
+        return x.contiguous() if x.dtype == torch.int32 else x.to(torch.int32).contiguous()
+    t = torch.as_tensor(x).to("cpu", torch.int64)
     if t.dim() != 1 or t.numel() != n:
         raise ValueError(f"{what} must have {n} entries")
-    if t.device == dev and t.dtype == torch.int32:
-        return t.contiguous()
-    return t.to(torch.int32).to(dev)
+    if unique_slots and n > 1:
+        live = t[t >= 0]
+        if live.numel() != torch.unique(live).numel():
+            raise ValueError(f"{what} names a state slot twice; rows that write one slot would race")
+    return _upload_i32(t, dev)
 
 
 class _Shapes:
@@ -533,10 +580,20 @@ def prepare_chunked(q, k, v, a, b, A_log, dt_bias, state=None, *, cu_seqlens=Non
     return PreparedChunked("gdn_chunk_fwd", args, keep, (y_t, out_state), dev)
 
 
-def _use_chunked(chunked, k, mask, cu_seqlens, T):
+def _aligned16(t: torch.Tensor) -> bool:
+    # a non-contiguous operand is copied (and so aligned) before the launch
+    return (not t.is_contiguous()) or t.data_ptr() % 16 == 0
+
+
+def _use_chunked(chunked, q, k, v, mask, T):
+    """The chunked kernel by default for long unmasked bf16 rows at
+    Dk = Dv = 128 with 16-byte aligned q/k/v; everything else steps the
+    recurrent kernel, which takes any of those."""
     if chunked is not None:
         return bool(chunked)
-    if mask is not None or k.dtype != torch.bfloat16 or k.shape[-1] != 128:
+    if mask is not None or k.dtype != torch.bfloat16 or k.shape[-1] != 128 or v.shape[-1] != 128:
+        return False
+    if not all(_aligned16(t) for t in (q, k, v)):
         return False
     return T >= CHUNK_MIN_TOKENS
 
@@ -556,7 +613,8 @@ def gated_delta_kernel(q, k, v, g, beta, state, mask=None, *, state_out=None, st
 
 def gated_delta_update(q, k, v, a, b, A_log, dt_bias, state=None, mask=None, use_kernel=True, *,
                        cu_seqlens: Optional[IntSeq] = None, state_out=None,
-                       chunked: Optional[bool] = None, workspace=None, state_index=None):
+                       chunked: Optional[bool] = None, workspace=None, state_index=None,
+                       max_seqlen: Optional[int] = None):
     """mlx-lm ``gated_delta_update`` on MI355X.
 
     Args (as mlx-lm): q, k ``[B,T,Hk,Dk]``; v ``[B,T,Hv,Dv]``; a, b ``[B,T,Hv]``;
@@ -565,7 +623,10 @@ def gated_delta_update(q, k, v, a, b, A_log, dt_bias, state=None, mask=None, use
     (:func:`gated_delta_ops`) on the device.
 
     Keyword-only additions: ``cu_seqlens`` packs ragged sequences in a
-    ``[1, N_tok, ...]`` layout (state then has one row per sequence);
+    ``[1, N_tok, ...]`` layout (state then has one row per sequence); host
+    offsets are validated, a device tensor is used without a host copy (the
+    call never synchronises; ``max_seqlen``, when given, is its longest
+    sequence, which picks the kernel -- by default the mean length does);
     ``state_out`` receives the new state (may be ``state``); ``chunked``
     forces the chunked MFMA prefill kernel on/off (default: long unmasked
     bf16 rows with Dk = 128); ``workspace`` is a reusable uint8 buffer for it.
@@ -586,9 +647,8 @@ def gated_delta_update(q, k, v, a, b, A_log, dt_bias, state=None, mask=None, use
         return y, s
     T = k.shape[1]
     if cu_seqlens is not None:
-        cu_host = torch.as_tensor(cu_seqlens).to("cpu", torch.int64)
-        T = int((cu_host[1:] - cu_host[:-1]).max()) if cu_host.numel() > 1 else 0
-    if _use_chunked(chunked, k, mask, cu_seqlens, T):
+        T = _packed_max_len(cu_seqlens, k.shape[1], max_seqlen)
+    if _use_chunked(chunked, q, k, v, mask, T):
         if mask is not None:
             raise ValueError("the chunked kernel does not take a mask")
         return _chunked(q, k, v, a, b, _lib.GATES_RAW, A_log, dt_bias, state,
@@ -623,8 +683,9 @@ def gated_delta_commit(k, v, a, b, A_log, dt_bias, state, n_commit: IntSeq, mask
     on ``[:, :n]`` from the pre-verify state (``dflash.py:403-426``,
     ``engine.py:337-359``), but ragged per row and in one launch that reads
     each state once and writes it once.  ``n_commit[b]`` in ``[0, T]``
-    (0 keeps the state; a negative value skips row b).  ``state_out`` may be
-    ``state`` (in place).  Returns the new state.
+    (0 keeps the state; a negative value skips row b: in place it is not
+    written, into a separate ``state_out`` its state is copied unchanged).
+    ``state_out`` may be ``state`` (in place).  Returns the new state.
     """
     n_rows = (len(torch.as_tensor(cu_seqlens)) - 1) if cu_seqlens is not None else k.shape[0]
     dev = _require_device([k], ["k"])

@@ -1,0 +1,79 @@
+"""One continuous-batching step of one GDN layer as one launch set.
+
+multiplex's scheduler runs, in one engine step, prefill chunks of new
+sequences next to decode and speculative-verify rounds of running ones
+(``multiplex/kernel/scheduler.py:299-363`` for the prefill chunks,
+``:463-608`` for a decode / verify round and its rollback).  On one MI355X
+those rows are independent launches of the same layer:
+
+* the packed prefills are one chunked launch (``prepare_chunked`` with
+  ``cu_seqlens``), whose two phases differ in what they load: the prep is
+  HBM-bound (it streams q, k and writes the chunk records), the scan is a
+  sequential chain per head that leaves HBM mostly idle;
+* the decode, verify and commit launches of the other rows
+  (``prepare_recurrent``) are HBM-bound state streams.
+
+:class:`MixedStep` issues the prep on the caller's stream, records an event,
+issues the scan behind it, and runs the other launches on a second stream
+(default priority) that waits for that event, so the HBM-bound launches
+overlap the scan rather than the prep.  The caller's stream then waits for
+the second stream, so work issued after ``launch()`` sees every output.
+Every launch writes disjoint outputs (separate rows and states), so the
+order between the two streams does not change any result:
+``launch_serial()`` issues the same launches on one stream, bit-identically.
+"""
+
+from __future__ import annotations
+
+from typing import Optional, Sequence
+
+import torch
+
+from .gated_delta import PreparedChunked, PreparedRecurrent
+
+__all__ = ["MixedStep"]
+
+
+class MixedStep:
+    """A prepared prefill plus prepared recurrent launches, issued as one step.
+
+    ``prefill``: a :class:`PreparedChunked` (the packed prefills), or None.
+    ``others``: prepared recurrent launches (decode, verify, commit), issued
+    in order on the side stream.  ``side``: the second stream (created with
+    default priority when not given).
+    """
+
+    def __init__(self, prefill: Optional[PreparedChunked], others: Sequence[PreparedRecurrent],
+                 side: Optional[torch.cuda.Stream] = None):
+        self.prefill = prefill
+        self.others = list(others)
+        devs = {p.device for p in self.others} | ({prefill.device} if prefill is not None else set())
+        if len(devs) != 1:
+            raise ValueError("a mixed step runs on one device")
+        self.device = devs.pop()
+        self.side = side if side is not None else torch.cuda.Stream(self.device)
+        self._prep_done = torch.cuda.Event()
+
+    def launch(self, stream=None):
+        """Enqueues the step: prep, then scan on ``stream`` (default: the
+        current stream); the other launches on the side stream once the prep
+        is done; ``stream`` waits for the side stream at the end."""
+        main = stream if stream is not None else torch.cuda.current_stream(self.device)
+        if self.prefill is not None:
+            self.prefill.launch_prep(main)
+            self._prep_done.record(main)
+            self.prefill.launch_scan(main)
+            self.side.wait_event(self._prep_done)
+        else:
+            self.side.wait_stream(main)
+        for p in self.others:
+            p.launch(self.side)
+        main.wait_stream(self.side)
+
+    def launch_serial(self, stream=None):
+        """The same launches, in the same order, on one stream."""
+        main = stream if stream is not None else torch.cuda.current_stream(self.device)
+        if self.prefill is not None:
+            self.prefill.launch(main)
+        for p in self.others:
+            p.launch(main)

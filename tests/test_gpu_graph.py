@@ -102,3 +102,44 @@ def test_prepared_launches_replay_in_a_graph():
         torch.cuda.synchronize()
         assert torch.equal(state, ref), f"replay {r}"
         assert torch.equal(plan.outputs[0], eager.outputs[0]), f"replay {r}: y"
+
+
+@torch.no_grad()
+def test_packed_calls_with_device_offsets_capture_in_a_graph():
+    """Packed calls whose ``cu_seqlens`` (and commit lengths) are device
+    tensors read nothing back to the host, so they can be captured: the
+    chunked and the recurrent packed updates and a packed commit, replayed
+    with the offsets and inputs changed between replays."""
+    g = torch.Generator().manual_seed(47)
+    n_tok, n_seqs = 300, 3
+    q = torch.nn.functional.normalize(torch.randn(1, n_tok, Hk, D, generator=g), dim=-1).to(torch.bfloat16).to(DEV)
+    k = torch.nn.functional.normalize(torch.randn(1, n_tok, Hk, D, generator=g), dim=-1).to(torch.bfloat16).to(DEV)
+    v = torch.randn(1, n_tok, Hv, D, generator=g).to(torch.bfloat16).to(DEV)
+    a = torch.randn(1, n_tok, Hv, generator=g).to(torch.bfloat16).to(DEV)
+    b = torch.randn(1, n_tok, Hv, generator=g).to(torch.bfloat16).to(DEV)
+    A_log = (torch.rand(Hv, generator=g) * 2.7).to(DEV)
+    dt_bias = (torch.rand(Hv, generator=g) * 2 - 1).to(DEV)
+    state = (torch.randn(n_seqs, Hv, D, D, generator=g) * 0.02).to(DEV)
+    cu = torch.tensor([0, 100, 130, 300], dtype=torch.int32, device=DEV)
+    n_commit = torch.tensor([5, 0, 64], dtype=torch.int32, device=DEV)
+
+    def calls():
+        yc, Sc = mx.gated_delta_update(q, k, v, a, b, A_log, dt_bias, state, cu_seqlens=cu, chunked=True)
+        yr, Sr = mx.gated_delta_update(q, k, v, a, b, A_log, dt_bias, state, cu_seqlens=cu, chunked=False)
+        Sm = mx.gated_delta_commit(k, v, a, b, A_log, dt_bias, state, n_commit, cu_seqlens=cu)
+        return yc, Sc, yr, Sr, Sm
+
+    calls()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        outs = calls()
+    for r, offsets in enumerate(([0, 100, 130, 300], [0, 64, 64, 300], [0, 1, 299, 300])):
+        cu.copy_(torch.tensor(offsets, dtype=torch.int32))
+        v.mul_(-1.0)
+        eager = calls()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for i, (x, y) in enumerate(zip(outs, eager)):
+            assert torch.equal(x, y), f"replay {r}: output {i}"

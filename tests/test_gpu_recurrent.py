@@ -348,3 +348,36 @@ def test_commit_verify_is_commit_then_verify(Tp, T):
         r["q"][5:6, :Tp][:, :, [0, 0, 1, 1]], r["k"][5:6, :Tp][:, :, [0, 0, 1, 1]], r["v"][5:6, :Tp],
         g[5:6, :Tp], beta[5:6, :Tp], r["state"][5:6])[1]).max() <= STATE_TOL
 
+
+
+def test_skipped_commit_row_into_a_fresh_state():
+    """A negative commit length skips the row; with no ``state_out`` (a
+    fresh output tensor) the row is the unchanged input state, not
+    uninitialised memory."""
+    d = draw(2003, 4, 3, 2, 4, 128, 128)
+    t, r = to_torch(d, DEV)
+    n = np.array([2, -1, 3, -5], dtype=np.int32)
+    S = mx.gated_delta_commit(t["k"], t["v"], t["a"], t["b"], t["A_log"], t["dt_bias"], t["state"],
+                              torch.tensor(n))
+    assert torch.equal(S[1], t["state"][1]) and torch.equal(S[3], t["state"][3])
+    g, beta = gdn.compute_g(r["A_log"], r["a"], r["dt_bias"]), gdn.compute_beta(r["b"])
+    S_ref = gdn.commit(r["q"], r["k"], r["v"], g, beta, r["state"], np.maximum(n, 0))
+    assert head_errs_state(S.cpu().numpy(), S_ref).max() <= STATE_TOL
+
+
+def test_default_path_for_shapes_the_chunked_kernel_does_not_take():
+    """Long bf16 rows at Dk=128 with Dv=96, or with 8-byte aligned q/k, go to
+    the recurrent kernel by default instead of failing in the chunked one."""
+    d = draw(2004, 1, 80, 2, 4, 128, 96)
+    t, r = to_torch(d, DEV)
+    y, S = run_update(t)
+    y_ref, S_ref = oracle_update(r)
+    assert row_errs_y(y.float().cpu().numpy(), y_ref).max() <= Y_TOL
+    assert head_errs_state(S.cpu().numpy(), S_ref).max() <= STATE_TOL
+    d = draw(2005, 1, 80, 2, 4, 128, 128)
+    t, r = to_torch(d, DEV)
+    t["q"], t["k"] = _offset_copy(t["q"]), _offset_copy(t["k"])
+    y, S = run_update(t)
+    y_ref, S_ref = oracle_update(r)
+    assert row_errs_y(y.float().cpu().numpy(), y_ref).max() <= Y_TOL
+    assert head_errs_state(S.cpu().numpy(), S_ref).max() <= STATE_TOL
