@@ -201,6 +201,30 @@ int gdn_chunk_scan(const void* q, const void* k, const void* v, int qkv_dtype,
                    void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * gdn_chunk_fwd without a workspace argument: the chunk records go to a
+ * static device array of 64 MiB (67,108,864 bytes) inside the library,
+ * one per GPU, held until the process ends.  No reference counterpart: it
+ * is for callers that cannot allocate device memory (code under HIP graph
+ * capture, serving loops that forbid allocation).  Calls whose
+ * gdn_chunk_workspace_bytes(...) exceed 64 MiB return GDN_ERR_UNSUPPORTED
+ * before any HIP call (at Hv = 32: one sequence of up to 1536 tokens, or
+ * packed sequences with ceil(n_tok / 64) + n_seqs <= 25).  The array's
+ * address on the current device (which must be the stream's) is taken on
+ * the first call there.  Every call on one GPU shares the array: calls that
+ * overlap on one GPU (on different streams) race.  Other arguments as in
+ * gdn_chunk_fwd.
+ */
+int gdn_chunk_fwd_noalloc(const void* q, const void* k, const void* v, int qkv_dtype,
+                          int gate_mode, const void* gx, const void* gy, int gate_dtype,
+                          int64_t gate_stride,
+                          const void* A_log, const void* dt_bias, int param_dtype,
+                          const float* state_in, void* y, float* state_out,
+                          const int32_t* state_index, int64_t n_slots,
+                          const int32_t* cu_seqlens, int64_t n_seqs, int64_t n_tok,
+                          int64_t Hk, int64_t Hv, int64_t Dk, int64_t Dv, int64_t chunk,
+                          void* stream);
+
+/*
  * Fused mixer prologue of GatedDeltaNet (dflash.py:351-370): mask zeroing,
  * concat(conv_state, qkv), depthwise causal conv1d with Kt taps (no bias),
  * SiLU, split into q | k | v, q = rms_norm(q)/Dk, k = rms_norm(k)/sqrt(Dk)

@@ -38,6 +38,7 @@ EXPORTS = (
     "gdn_chunk_fwd",
     "gdn_chunk_prep",
     "gdn_chunk_scan",
+    "gdn_chunk_fwd_noalloc",
     "gdn_conv_prologue",
     "gdn_conv_state_commit",
     "gdn_gated_rmsnorm",
@@ -122,6 +123,11 @@ _SIGNATURES = {
         c_int,
         [_P, _P, _P, c_int, c_int, _P, _P, c_int, _I64, _P, _P, c_int, _P, _P, _P, _P, _I64, _P,
          _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P, c_size_t, _P],
+    ),
+    "gdn_chunk_fwd_noalloc": (
+        c_int,
+        [_P, _P, _P, c_int, c_int, _P, _P, c_int, _I64, _P, _P, c_int, _P, _P, _P, _P, _I64, _P,
+         _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P],
     ),
     "gdn_conv_prologue": (
         c_int,

@@ -27,6 +27,8 @@
 // the fp32 state meets a 1e-4 norm-wise tolerance.  Log-decay prefix sums
 // are accumulated in fp64 so exp(L_t - L_i) keeps its digits when |L| is
 // large.
+#include <mutex>
+
 #include "gdn_common.hpp"
 
 namespace {
@@ -917,6 +919,54 @@ extern "C" size_t gdn_chunk_workspace_bytes(int64_t n_seqs, int64_t n_tok, int64
   return record_bytes(n_seqs, n_tok, Hv) + order;
 }
 
+// ------------------------------------------------ no-allocation entry point
+//
+// gdn_chunk_fwd with the chunk records in a file-scope device array instead
+// of a caller's workspace, for callers that cannot allocate device memory
+// (code under HIP graph capture, serving loops that forbid allocation).  The
+// array is kScratchBytes; every GPU the library runs on holds its own copy
+// (at its own address) until the process ends.  Its address is taken once
+// per device, on the entry point's first call there with that device
+// current, by hipGetSymbolAddress; the name `scratch` itself is a host-side
+// stand-in and is never passed to a kernel.  The records need no clearing:
+// the prep writes every record entry the scan reads.  All calls on one GPU
+// share the array, so calls that overlap on one GPU (different streams, or
+// an unfinished call's scan) race on it.
+
+constexpr size_t kScratchBytes = size_t(64) << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+}  // namespace
+
+static int scratch_on_current_device(void** out) {
+  using gdn_host::fail;
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(GDN_ERR_LAUNCH, "gdn_chunk_fwd_noalloc: hipGetDevice: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices)
+    return fail(GDN_ERR_UNSUPPORTED, "gdn_chunk_fwd_noalloc: device %d above %d", dev, kMaxDevices - 1);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || ptr == nullptr)
+      return fail(GDN_ERR_LAUNCH, "gdn_chunk_fwd_noalloc: hipGetSymbolAddress(scratch) on device %d: %s", dev,
+                  hipGetErrorString(e));
+    if (!gdn_host::aligned(ptr, 256))
+      return fail(GDN_ERR_LAUNCH, "gdn_chunk_fwd_noalloc: scratch on device %d is not 256-byte aligned", dev);
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return GDN_OK;
+}
+
+
 namespace {
 
 size_t record_bytes(int64_t n_seqs, int64_t n_tok, int64_t Hv) {
@@ -927,13 +977,15 @@ constexpr unsigned kPhasePrep = 1, kPhaseScan = 2;
 
 // Validates the arguments and enqueues the phases selected by `phases`
 // (the same checks for every phase, so a prep and a scan issued separately
-// with the same arguments see the same records).
+// with the same arguments see the same records).  With `use_scratch` the
+// records go to the library's static scratch array on the current device
+// instead of `workspace` (checked against its size before any HIP call).
 int chunk_fwd(const void* q, const void* k, const void* v, int qkv_dtype, int gate_mode, const void* gx,
               const void* gy, int gate_dtype, int64_t gate_stride, const void* A_log, const void* dt_bias,
               int param_dtype, const float* state_in, void* y, float* state_out, const int32_t* state_index,
               int64_t n_slots, const int32_t* cu_seqlens, int64_t n_seqs, int64_t n_tok, int64_t Hk, int64_t Hv,
               int64_t Dk, int64_t Dv, int64_t chunk, void* workspace, size_t workspace_bytes, void* stream,
-              unsigned phases) {
+              unsigned phases, bool use_scratch = false) {
   using gdn_host::fail;
   if (chunk != CH) return fail(GDN_ERR_UNSUPPORTED, "gdn_chunk_fwd: chunk must be 64 (got %lld)", (long long)chunk);
   if (qkv_dtype != GDN_DTYPE_BF16) return fail(GDN_ERR_UNSUPPORTED, "gdn_chunk_fwd: q/k/v must be bf16");
@@ -961,15 +1013,27 @@ int chunk_fwd(const void* q, const void* k, const void* v, int qkv_dtype, int ga
     return fail(GDN_ERR_INVALID, "gdn_chunk_fwd: n_slots=%lld out of range", (long long)n_slots);
   if (n_seqs == 0) return GDN_OK;
   const size_t need = gdn_chunk_workspace_bytes(n_seqs, n_tok, Hv, Dk, Dv, chunk);
-  if (workspace == nullptr || workspace_bytes < need)
+  if (use_scratch) {
+    if (need > kScratchBytes)
+      return fail(GDN_ERR_UNSUPPORTED,
+                  "gdn_chunk_fwd_noalloc: %zu bytes of chunk records exceed the static scratch of %zu bytes "
+                  "(n_seqs=%lld, n_tok=%lld, Hv=%lld); use gdn_chunk_fwd with a workspace",
+                  need, kScratchBytes, (long long)n_seqs, (long long)n_tok, (long long)Hv);
+  } else if (workspace == nullptr || workspace_bytes < need) {
     return fail(GDN_ERR_INVALID, "gdn_chunk_fwd: workspace of %zu bytes is below the %zu needed", workspace_bytes,
                 need);
-  if (!gdn_host::aligned(workspace, 256) || !gdn_host::aligned(q, 16) || !gdn_host::aligned(k, 16) ||
-      !gdn_host::aligned(v, 16) || !gdn_host::aligned(state_in, 16) || !gdn_host::aligned(state_out, 16))
+  }
+  if ((!use_scratch && !gdn_host::aligned(workspace, 256)) || !gdn_host::aligned(q, 16) ||
+      !gdn_host::aligned(k, 16) || !gdn_host::aligned(v, 16) || !gdn_host::aligned(state_in, 16) ||
+      !gdn_host::aligned(state_out, 16))
     return fail(GDN_ERR_INVALID, "gdn_chunk_fwd: misaligned pointer");
   if (n_tok > INT32_MAX / 2 || n_seqs > 65535 || Hv > 65535 || max_chunks(n_seqs, n_tok, packed) * Hv >= INT32_MAX ||
       (DV / DVT) * (Hv * n_seqs + 8 * (Hv / Hk)) > INT32_MAX)
     return fail(GDN_ERR_UNSUPPORTED, "gdn_chunk_fwd: problem too large");
+  if (use_scratch) {
+    const int rc = scratch_on_current_device(&workspace);
+    if (rc != GDN_OK) return rc;
+  }
 
   ChunkParams p;
   p.q = static_cast<const uint16_t*>(q);
@@ -1039,3 +1103,14 @@ extern "C" int gdn_chunk_fwd(GDN_CHUNK_PARAMS) { return chunk_fwd(GDN_CHUNK_ARGS
 extern "C" int gdn_chunk_prep(GDN_CHUNK_PARAMS) { return chunk_fwd(GDN_CHUNK_ARGS, kPhasePrep); }
 
 extern "C" int gdn_chunk_scan(GDN_CHUNK_PARAMS) { return chunk_fwd(GDN_CHUNK_ARGS, kPhaseScan); }
+
+extern "C" int gdn_chunk_fwd_noalloc(const void* q, const void* k, const void* v, int qkv_dtype, int gate_mode,
+                                     const void* gx, const void* gy, int gate_dtype, int64_t gate_stride,
+                                     const void* A_log, const void* dt_bias, int param_dtype, const float* state_in,
+                                     void* y, float* state_out, const int32_t* state_index, int64_t n_slots,
+                                     const int32_t* cu_seqlens, int64_t n_seqs, int64_t n_tok, int64_t Hk,
+                                     int64_t Hv, int64_t Dk, int64_t Dv, int64_t chunk, void* stream) {
+  return chunk_fwd(q, k, v, qkv_dtype, gate_mode, gx, gy, gate_dtype, gate_stride, A_log, dt_bias, param_dtype,
+                   state_in, y, state_out, state_index, n_slots, cu_seqlens, n_seqs, n_tok, Hk, Hv, Dk, Dv, chunk,
+                   nullptr, 0, stream, kPhasePrep | kPhaseScan, true);
+}

@@ -189,3 +189,17 @@ def test_python_rejects_host_tensors():
         mx.gated_delta_ops(q, q, v, g, g)
     with pytest.raises(ValueError, match="ROCm device"):
         mx.gdn_conv_prologue(torch.zeros(1, 1, 8192), torch.zeros(8192, 4), 16, 32, 128, 128)
+
+
+def test_noalloc_chunk_rejects_calls_beyond_its_scratch(lib):
+    """gdn_chunk_fwd_noalloc refuses, before any HIP call, a call whose chunk
+    records exceed its 64 MiB static scratch (2048 tokens at Hv=32 need
+    (32 + 1) * 32 records of 82,688 B), and takes no workspace argument."""
+    P, I = FAKE, _lib.DTYPE_BF16
+    st = lib.gdn_chunk_fwd_noalloc(P, P, P, I, _lib.GATES_RAW, P, P, I, 0, P, P, _lib.DTYPE_F32, P, P, P,
+                                   None, 0, None, 1, 2048, 16, 32, 128, 128, 64, None)
+    assert st == _lib.ERR_UNSUPPORTED
+    msg = lib.gdn_last_error().decode()
+    assert "static scratch" in msg and "67108864" in msg
+    assert lib.gdn_chunk_workspace_bytes(1, 2048, 32, 128, 128, 64) > 64 << 20
+    assert lib.gdn_chunk_workspace_bytes(1, 1536, 32, 128, 128, 64) <= 64 << 20
