@@ -34,6 +34,32 @@ def test_staged_copy_sees_the_preceding_kernel():
     assert torch.equal(host[0][1], new_state.cpu())
 
 
+def test_staged_clone_survives_a_later_in_place_update_and_reuse():
+    """Stage a clone, drop it, then queue an in-place decode of the live
+    state and an allocation of the same size: the snapshot still holds the
+    pre-update state (the source is marked used on the copy stream, so its
+    memory is not handed out while the copy is pending)."""
+    g = torch.Generator().manual_seed(4)
+    B = 64
+    q = (torch.randn(B, 1, HK, D, generator=g) / 16).to(torch.bfloat16).to(DEV)
+    k = torch.nn.functional.normalize(torch.randn(B, 1, HK, D, generator=g), dim=-1).to(torch.bfloat16).to(DEV)
+    v = torch.randn(B, 1, HV, D, generator=g).to(torch.bfloat16).to(DEV)
+    a = torch.randn(B, 1, HV, generator=g).to(torch.bfloat16).to(DEV)
+    b = torch.randn(B, 1, HV, generator=g).to(torch.bfloat16).to(DEV)
+    A_log, dt_bias = torch.rand(HV).to(DEV), torch.rand(HV).to(DEV)
+    state = (torch.randn(B, HV, D, D, generator=g) * 0.02).to(DEV)
+    expect = state.cpu()
+    snap = state.clone()
+    staged = ps.stage_to_host([snap])
+    del snap
+    for _ in range(4):
+        mx.gated_delta_update(q, k, v, a, b, A_log, dt_bias, state, state_out=state)
+    junk = torch.full_like(state, 7.0)
+    host = staged.wait()
+    assert torch.equal(host[0], expect)
+    assert not torch.equal(state.cpu(), expect) and bool((junk == 7.0).all())
+
+
 @torch.no_grad()
 def test_record_round_trip_restores_a_mixer(tmp_path):
     m = mx.GatedDeltaNet(HID, HK, HV, D, D, device=DEV)

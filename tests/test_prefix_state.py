@@ -74,14 +74,15 @@ def test_round_trip_through_the_blob_store(tmp_path):
     snap = snapshot(1)
     tree = (7, snap, [None, True])
     spec, blobs = ps.encode_tree(tree)
-    store = ps.BlobStore(tmp_path)
-    wrote, dedup = store.write_blobs(blobs)
-    assert wrote == len(blobs) and dedup == 0
-    assert store.write_blobs(blobs) == (0, len(blobs))
-    assert not list(tmp_path.rglob("*.tmp-*"))
+    store = ps.ContentStore(tmp_path)
+    wrote, present = store.put_many(blobs)
+    assert wrote == len(blobs) and present == 0
+    assert store.put_many(blobs) == (0, len(blobs))
+    assert not [p for p in tmp_path.rglob("*") if p.name.startswith(".")]
     for d in blobs:
-        assert store.path(d) == tmp_path / "blobs" / d[:2] / f"{d}.bin"
-    back = ps.decode_tree(json.loads(json.dumps(spec)), store.read_blob)
+        assert store.blob_path(d) == tmp_path / "blobs" / d[:2] / f"{d}.bin"
+        assert hashlib.sha256(store.blob_path(d).read_bytes()).hexdigest() == d
+    back = ps.decode_tree(json.loads(json.dumps(spec)), store.get)
     assert back[0] == 7 and back[2] == [None, 1]
     for a, b in zip(back[1], snap):
         if b is None:
@@ -106,15 +107,74 @@ def test_writer_records_host_snapshots(tmp_path):
     snap = snapshot(2)
     w = ps.AsyncStateWriter(tmp_path)
     try:
-        w.submit("ab" * 32, snap, parent=None, tokens=[1, 2, 3], start=0, pos=3, touch=5)
+        w.submit("ab" * 32, snap, parent=None, tokens=[1, 2, 3], start=0, pos=3, touch=5).result()
         w.flush()
-        rec = w.read_record("ab" * 32)
+        path = w.record_path("ab" * 32)
+        assert path == tmp_path / "records" / "ab" / f"{'ab' * 32}.json"
+        rec = json.loads(path.read_text(encoding="utf-8"))
+        assert list(rec) == ["version", "key", "parent", "tokens", "start", "pos", "pool", "source", "touch",
+                             "attn", "ssm", "cached_h"]
         assert rec["version"] == ps.RECORD_FORMAT_VERSION == 1
         assert (rec["key"], rec["tokens"], rec["pos"], rec["touch"], rec["pool"]) == ("ab" * 32, [1, 2, 3], 3, 5,
                                                                                        "default")
-        assert w.record_path("ab" * 32) == tmp_path / "records" / "ab" / f"{'ab' * 32}.json"
+        assert path.read_text(encoding="utf-8") == json.dumps(rec, ensure_ascii=False, separators=(",", ":"))
+        # every blob the record names is in the store, under its own digest
+        shas = []
+        stack = [rec["ssm"]]
+        while stack:
+            x = stack.pop()
+            if isinstance(x, dict):
+                shas += [x["sha"]] if "sha" in x else []
+                stack += list(x.values())
+            elif isinstance(x, list):
+                stack += x
+        for d in shas:
+            assert hashlib.sha256((tmp_path / "blobs" / d[:2] / f"{d}.bin").read_bytes()).hexdigest() == d
         back = w.load_ssm("ab" * 32)
         assert torch.equal(back[0][1], snap[0][1]) and back[1] is None
+        assert back[0][0].dtype == torch.bfloat16 and torch.equal(back[0][0], snap[0][0])
         assert ps.spec_nbytes(rec["ssm"]) == 2 * (3 * 8192 * 2 + 32 * 128 * 128 * 4)
+    finally:
+        w.close()
+
+
+@pytest.mark.parametrize("dtype", [torch.bool, torch.uint8, torch.int16, torch.int32, torch.int64, torch.float16,
+                                   torch.float64, torch.bfloat16])
+def test_every_dtype_round_trips_with_numpy_bytes(dtype):
+    g = torch.Generator().manual_seed(5)
+    t = (torch.randn(2, 3, 600, generator=g) * 100).to(dtype)
+    spec, blobs = ps.encode_tree(t, block_size=256)
+    assert spec["k"] == "blocks" and [(b["start"], b["end"]) for b in spec["blocks"]] == [(0, 256), (256, 512),
+                                                                                           (512, 600)]
+    for b in spec["blocks"]:
+        part = t[:, :, b["start"]:b["end"]]
+        ref = (part.view(torch.int16) if dtype == torch.bfloat16 else part).numpy()
+        raw = np.ascontiguousarray(ref).tobytes()
+        assert blobs[b["sha"]] == raw and b["sha"] == hashlib.sha256(raw).hexdigest()
+    assert torch.equal(ps.decode_tree(spec, blobs.__getitem__), t)
+
+
+def test_record_reader_checks_the_version(tmp_path):
+    w = ps.AsyncStateWriter(tmp_path)
+    try:
+        w.submit("cd" * 32, [None]).result()
+        p = w.record_path("cd" * 32)
+        obj = json.loads(p.read_text())
+        obj["version"] = 2
+        p.write_text(json.dumps(obj))
+        with pytest.raises(ValueError):
+            w.read_record("cd" * 32)
+    finally:
+        w.close()
+
+
+def test_writer_reports_failures_on_flush(tmp_path):
+    w = ps.AsyncStateWriter(tmp_path)
+    try:
+        w.submit("ef" * 32, [object()])
+        with pytest.raises(RuntimeError):
+            w.flush()
+        w.submit("ef" * 32, [None]).result()
+        w.flush()
     finally:
         w.close()
