@@ -13,7 +13,10 @@ therefore computed by implementations independent of ``oracle/gdn.py``:
 * the prologue: ``torch.nn.functional.conv1d(groups=C)``, ``silu`` and
   ``rms_norm`` in float64;
 * the epilogue's gated RMSNorm: transformers' ``Qwen3NextRMSNormGated``
-  module, run in bfloat16 (bf16 and fp32 weight) and in float32.
+  module, run in bfloat16 (bf16 and fp32 weight) and in float32;
+* the whole mixer: transformers' ``Qwen3_5GatedDeltaNet`` module, run from
+  given conv and recurrent states in float32 (prefill and single-token
+  decode) and in bfloat16.
 
 Inputs are drawn from ``numpy.random.default_rng`` with fixed seeds.
 Run: ``python tests/golden/make_golden.py [case ...]`` (needs transformers;
@@ -145,12 +148,104 @@ def gated_norm_case(name, seed, rows, D, eps=1e-6):
     )
 
 
+class _OneLayerCache:
+    """The part of a transformers ``Cache`` that ``Qwen3_5GatedDeltaNet.forward``
+    uses, for layer 0: a conv state ``[B, C, K]`` (transformers keeps K
+    columns; the last K-1 are the previous inputs) and a recurrent state
+    ``[B, H, Dk, Dv]``, both present (a continued sequence)."""
+
+    def __init__(self, conv, rec):
+        import types
+
+        self.layers = [types.SimpleNamespace(conv_states={0: conv}, recurrent_states={0: rec}, record_past=False)]
+
+    def has_previous_state(self, idx):
+        return True
+
+    def update_conv_state(self, x, idx, conv_kernel_size):
+        layer = self.layers[idx]
+        full = torch.cat([layer.conv_states[0], x], dim=-1)
+        layer.conv_states[0] = full[..., -conv_kernel_size:].clone()
+        return full
+
+    def update_recurrent_state(self, st, idx):
+        self.layers[idx].recurrent_states[0] = st.clone()
+
+
+def mixer_case(name, seed, B, S, hidden, Hk, Hv, D, dtype, Kt=4, eps=1e-6):
+    """transformers' ``Qwen3_5GatedDeltaNet`` (the GatedDeltaNet mixer of the
+    Qwen3.5 family, whose layout -- in_proj_qkv / in_proj_z / in_proj_b /
+    in_proj_a, depthwise conv1d, gated RMSNorm, out_proj -- is the one
+    ``multiplex/kernel/dflash.py:343-381`` restates), run on the CPU from
+    given conv and recurrent states: with S > 1 through its chunked path,
+    with S = 1 through its single-token update."""
+    import types
+
+    from transformers.models.qwen3_5.modeling_qwen3_5 import Qwen3_5GatedDeltaNet
+
+    rng = np.random.default_rng(seed)
+    C = 2 * Hk * D + Hv * D
+    cfg = types.SimpleNamespace(hidden_size=hidden, linear_num_value_heads=Hv, linear_num_key_heads=Hk,
+                                linear_key_head_dim=D, linear_value_head_dim=D, linear_conv_kernel_dim=Kt,
+                                hidden_act="silu", rms_norm_eps=eps, layer_types=["linear_attention"])
+    prm = {
+        "in_proj_qkv": rng.normal(0.0, hidden ** -0.5, (C, hidden)),
+        "in_proj_z": rng.normal(0.0, hidden ** -0.5, (Hv * D, hidden)),
+        "in_proj_b": rng.normal(0.0, hidden ** -0.5, (Hv, hidden)),
+        "in_proj_a": rng.normal(0.0, hidden ** -0.5, (Hv, hidden)),
+        "conv1d": rng.normal(0.0, 0.3, (C, Kt)),
+        "A_log": rng.uniform(0.0, np.log(16.0), Hv),
+        "dt_bias": rng.uniform(-1.0, 1.0, Hv),
+        "norm": rng.normal(1.0, 0.2, D),
+        "out_proj": rng.normal(0.0, (Hv * D) ** -0.5, (hidden, Hv * D)),
+    }
+    x = rng.standard_normal((B, S, hidden))
+    conv_state = rng.standard_normal((B, Kt - 1, C))
+    state = rng.normal(0.0, 0.05, (B, Hv, D, D))                 # [B, Hv, Dv, Dk]
+    tdt = {"f32": torch.float32, "bf16": torch.bfloat16}[dtype]
+    with torch.no_grad():
+        m = Qwen3_5GatedDeltaNet(cfg, 0).to(tdt)
+        for n, w in (("in_proj_qkv", "in_proj_qkv"), ("in_proj_z", "in_proj_z"), ("in_proj_b", "in_proj_b"),
+                     ("in_proj_a", "in_proj_a"), ("out_proj", "out_proj")):
+            getattr(m, n).weight.copy_(torch.tensor(prm[w]))
+        m.conv1d.weight.copy_(torch.tensor(prm["conv1d"])[:, None, :])
+        m.A_log.copy_(torch.tensor(prm["A_log"]))
+        m.dt_bias.copy_(torch.tensor(prm["dt_bias"]))
+        m.norm.weight.copy_(torch.tensor(prm["norm"]))
+        # round every parameter / input to the module's dtype, and store the rounded values
+        prm = {"in_proj_qkv": m.in_proj_qkv.weight, "in_proj_z": m.in_proj_z.weight, "in_proj_b": m.in_proj_b.weight,
+               "in_proj_a": m.in_proj_a.weight, "conv1d": m.conv1d.weight[:, 0, :], "A_log": m.A_log,
+               "dt_bias": m.dt_bias, "norm": m.norm.weight, "out_proj": m.out_proj.weight}
+        prm = {k: v.double().numpy() for k, v in prm.items()}
+        xt = torch.tensor(x).to(tdt)
+        cst = torch.tensor(conv_state).to(tdt)
+        conv_hf = torch.cat([torch.zeros(B, 1, C, dtype=tdt), cst], dim=1).transpose(1, 2).contiguous()
+        st = torch.tensor(state, dtype=torch.float32)
+        cache = _OneLayerCache(conv_hf, st.transpose(-1, -2).contiguous())
+        out = m(xt, cache_params=cache)
+        cs_out = cache.layers[0].conv_states[0][..., 1:].transpose(1, 2)
+        st_out = cache.layers[0].recurrent_states[0].transpose(-1, -2)
+    np.savez_compressed(
+        HERE / f"{name}.npz",
+        x=xt.double().numpy(), conv_state=cst.double().numpy(), state=st.double().numpy(),
+        out=out.double().numpy(), conv_state_out=cs_out.double().numpy(), state_out=st_out.double().numpy(),
+        dims=np.array([B, S, hidden, Hk, Hv, D, Kt], dtype=np.float64), eps=np.array(eps),
+        **{f"p_{k}": v for k, v in prm.items()},
+    )
+
+
 CASES = {
     "recurrent_small": lambda: recurrent_case("recurrent_small", 11, B=2, T=6, Hk=2, Hv=4, Dk=16, Dv=8),
     "recurrent_hd128": lambda: recurrent_case("recurrent_hd128", 12, B=1, T=3, Hk=2, Hv=4, Dk=128, Dv=128),
     "chunked_t100": lambda: chunked_case("chunked_t100", 13, B=1, T=100, Hk=1, Hv=2, Dk=32, Dv=16, chunk=64),
     "prologue_small": lambda: prologue_case("prologue_small", 14, B=2, S=7, Hk=2, Hv=4, D=16),
     "gated_norm_small": lambda: gated_norm_case("gated_norm_small", 15, rows=48, D=128),
+    "mixer_prefill_f32": lambda: mixer_case("mixer_prefill_f32", 16, B=2, S=6, hidden=48, Hk=2, Hv=4, D=16,
+                                            dtype="f32"),
+    "mixer_decode_f32": lambda: mixer_case("mixer_decode_f32", 17, B=3, S=1, hidden=48, Hk=2, Hv=4, D=16,
+                                           dtype="f32"),
+    "mixer_prefill_bf16": lambda: mixer_case("mixer_prefill_bf16", 18, B=2, S=6, hidden=48, Hk=2, Hv=4, D=16,
+                                             dtype="bf16"),
 }
 
 

@@ -323,3 +323,80 @@ def test_planted_mistakes(kind):
     assert rel_err(y, d["y"]) < 2e-6 and rel_err(S, d["state_out"]) < 2e-6
     ym, Sm = _mutant(kind)(d["q"], d["k"], d["v"], g, beta, d["state"])
     assert max(rel_err(ym, d["y"]), rel_err(Sm, d["state_out"])) > 1e-2
+
+
+# ------------------------------------------------------------------ mixer
+
+def _mixer_fixture(name):
+    d = load(name)
+    B, S, H, Hk, Hv, D, Kt = (int(x) for x in d["dims"])
+    p = {k[2:]: v for k, v in d.items() if k.startswith("p_")}
+    return d, p, (Hk, Hv, D, D)
+
+
+def _run_mixer(d, p, dims, round_bf16=False):
+    return gdn.mixer_forward(p, d["x"], *dims, conv_state=d["conv_state"], state=d["state"],
+                             eps=float(d["eps"]), round_bf16=round_bf16)
+
+
+@pytest.mark.parametrize("name", ["mixer_prefill_f32", "mixer_decode_f32"])
+def test_mixer_matches_library_module(name):
+    """``mixer_forward`` against transformers' Qwen3_5GatedDeltaNet in float32
+    (prefill through its chunked path, decode through its single-token
+    update), from nonzero conv and recurrent states: output, conv state and
+    state.  The remaining ~1e-6 is float32 arithmetic and the norm's epsilon
+    (transformers adds 1e-6 to sum(x^2); the reference's rms_norm form adds
+    Dk * 1e-6)."""
+    d, p, dims = _mixer_fixture(name)
+    out, cs, st = _run_mixer(d, p, dims)
+    assert rel_err(out, d["out"]) < 2e-5
+    assert rel_err(cs, d["conv_state_out"]) < 1e-6
+    assert rel_err(st, d["state_out"]) < 2e-5
+
+
+def test_mixer_bf16_module_within_rounding_distance():
+    """The same module run in bfloat16 rounds at more points (after the conv,
+    after SiLU, the L2 norm and beta in bf16 arithmetic) than the oracle's
+    bf16 mode, which rounds where the fused kernels do (projections, q/k/v,
+    y, normed y, output); the reference's own points (mlx-lm) are unknown
+    here.  Two bf16 restatements agree to the size of those roundings."""
+    d, p, dims = _mixer_fixture("mixer_prefill_bf16")
+    out, cs, st = _run_mixer(d, p, dims, round_bf16=True)
+    assert rel_err(out, d["out"]) < 2e-2 and rel_err(st, d["state_out"]) < 2e-2
+    np.testing.assert_array_equal(cs, d["conv_state_out"])
+
+
+def _mixer_mutant(kind, monkeypatch):
+    if kind == "flipped_conv_taps":
+        real = gdn.conv_prologue
+        monkeypatch.setattr(gdn, "conv_prologue", lambda qkv, w, *a, **k: real(qkv, np.asarray(w)[:, ::-1], *a, **k))
+    elif kind == "norm_gated_by_y":
+        real = gdn.gated_rms_norm
+        monkeypatch.setattr(gdn, "gated_rms_norm", lambda x, gate, *a, **k: real(x, x, *a, **k))
+    elif kind == "norm_over_all_heads":
+        real = gdn.gated_rms_norm
+
+        def over_all(x, gate, weight=None, *a, **k):
+            sh = np.shape(x)
+            w = None if weight is None else np.tile(weight, sh[-2])
+            return real(np.reshape(x, sh[:-2] + (-1,)), np.reshape(gate, sh[:-2] + (-1,)), w, *a, **k).reshape(sh)
+        monkeypatch.setattr(gdn, "gated_rms_norm", over_all)
+    elif kind == "q_scaled_like_k":
+        real = gdn.conv_prologue
+
+        def scaled(*a, **k):
+            q, kk, v, cs, ci = real(*a, **k)
+            return q * np.sqrt(q.shape[-1]), kk, v, cs, ci
+        monkeypatch.setattr(gdn, "conv_prologue", scaled)
+
+
+@pytest.mark.parametrize("kind", ["swap_a_b", "flipped_conv_taps", "norm_gated_by_y", "norm_over_all_heads",
+                                  "q_scaled_like_k"])
+def test_mixer_planted_mistakes(kind, monkeypatch):
+    """Plausible wiring mistakes planted in the oracle fail the module pin."""
+    d, p, dims = _mixer_fixture("mixer_prefill_f32")
+    if kind == "swap_a_b":
+        p = dict(p, in_proj_a=p["in_proj_b"], in_proj_b=p["in_proj_a"])
+    _mixer_mutant(kind, monkeypatch)
+    out, _, st = _run_mixer(d, p, dims)
+    assert max(rel_err(out, d["out"]), rel_err(st, d["state_out"])) > 1e-2
