@@ -593,6 +593,7 @@ def main():
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 256 MiB device-to-device copy (counter calibration) and exit")
     ap.add_argument("--prefill-only", action="store_true", help="only the T=4096 prefill workload")
+    ap.add_argument("--mixed-only", action="store_true", help="only the mixed continuous-batching step")
     ap.add_argument("--epilogue-only", action="store_true", help="only the gated RMSNorm epilogue workloads")
     ap.add_argument("--verify-only", action="store_true", help="only the B=32, T=4 verify + commit workload")
     ap.add_argument("--mixer-only", action="store_true", help="only the whole-mixer-layer workloads")
@@ -663,6 +664,9 @@ def main():
     if args.prefill_only:
         p = bench_prefill(torch, mx, dev, timer, iters=args.steps)
         print(json.dumps({"prefill_t4096": p}), flush=True)
+        return
+    if args.mixed_only:
+        print(json.dumps({"mixed": bench_mixed(torch, mx, dev, timer, iters=args.steps)}), flush=True)
         return
 
     dec = bench_decode_b64(torch, mx, dev, args.steps, args.warmup, timer)

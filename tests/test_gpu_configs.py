@@ -171,3 +171,23 @@ def test_verify_b32_full_heads():
     g, beta = gdn.compute_g(r["A_log"], r["a"], r["dt_bias"]), gdn.compute_beta(r["b"])
     y_ref, _ = gdn.recurrent(r["q"], r["k"], r["v"], g, beta, r["state"])
     assert row_errs_y(y.float().cpu().numpy(), y_ref).max() <= Y_TOL
+
+
+def test_commit_verify_one_pass_b32_full_heads():
+    """The bench's one-pass round at B=32: the previous round's 4 drafts with
+    ragged acceptance n_b ~ U{1..4} committed and the next 4 drafts verified
+    in one launch (the streaming MFMA kernel walks 2048 units, several per
+    workgroup), all heads against the oracle."""
+    d = draw(1012, 32, 8, Hk, Hv, D, D)
+    t, r = to_torch(d, DEV)
+    n_b = np.random.default_rng(1013).integers(1, 5, 32)
+    prev = tuple(t[n][:, :4].contiguous() for n in ("q", "k", "v", "a", "b"))
+    new = tuple(t[n][:, 4:].contiguous() for n in ("q", "k", "v", "a", "b"))
+    y, S = mx.gated_delta_commit_verify(prev, torch.tensor(n_b, dtype=torch.int32), *new, t["A_log"], t["dt_bias"],
+                                        t["state"])
+    g, beta = gdn.compute_g(r["A_log"], r["a"], r["dt_bias"]), gdn.compute_beta(r["b"])
+    S_ref = gdn.commit(r["q"], r["k"], r["v"], g, beta, r["state"], n_b)
+    assert head_errs_state(S.cpu().numpy(), S_ref).max() <= STATE_TOL
+    keep = np.concatenate([np.arange(4)[None, :] < n_b[:, None], np.ones((32, 4), dtype=bool)], axis=1)
+    y_ref, _ = gdn.recurrent(r["q"], r["k"], r["v"], g, beta, r["state"], keep)
+    assert row_errs_y(y.float().cpu().numpy(), y_ref[:, 4:]).max() <= Y_TOL

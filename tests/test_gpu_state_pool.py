@@ -210,3 +210,33 @@ def test_mixer_on_pooled_states_equals_dense():
     assert torch.equal(m(x2, None, dense), m(x2, None, pooled))
     same(dense, pooled)
     assert pool.n_free == 12 - 3
+
+
+def test_verify_paths_skip_out_of_range_slots():
+    """A plain verify (the MFMA verify kernel) and a verify that commits the
+    previous round (the stepping kernel) skip rows whose slot lies outside
+    the pool: their y and slots are untouched, the other rows equal the
+    dense launch."""
+    pool = pool_with(11, 6)
+    slots = [1, -1, 6, 4]
+    idx = torch.tensor(slots, dtype=torch.int32, device=DEV)
+    t = inputs(12, len(slots), 4)
+    before = pool.states.clone()
+    dense = torch.zeros(len(slots), Hv, D, D, device=DEV)
+    dense[0], dense[3] = before[1], before[4]
+    y_d, _ = mx.gated_delta_verify(*gdn_args(t), dense)
+    y_p, _ = mx.gated_delta_verify(*gdn_args(t), pool.states, state_index=idx)
+    torch.cuda.synchronize()
+    for b in (0, 3):
+        assert torch.equal(y_p[b], y_d[b])
+    assert torch.equal(pool.states, before)
+    prev = inputs(13, len(slots), 4)
+    pv = tuple(prev[n] for n in ("q", "k", "v", "a", "b"))
+    n_prev = [2, 1, 3, 4]
+    y_d2, S_d2 = mx.gated_delta_commit_verify(pv, n_prev, *gdn_args(t), dense)
+    y_p2, _ = mx.gated_delta_commit_verify(pv, n_prev, *gdn_args(t), pool.states, state_index=idx)
+    torch.cuda.synchronize()
+    for b, s in ((0, 1), (3, 4)):
+        assert torch.equal(y_p2[b], y_d2[b])
+        assert torch.equal(pool.states[s], S_d2[b])
+    others_unchanged(pool, before, [1, 4])
