@@ -280,6 +280,67 @@ int gdn_gated_rmsnorm(const void* x, const void* gate, int io_dtype,
                       const void* weight, int w_dtype, void* out,
                       int64_t rows, int64_t D, float eps, void* stream);
 
+/* ---------------------------------------------------------------------
+ * Full-attention layers: the hybrid trunk's attention layers and the MTP
+ * draft head (mtp.py:160-194 stacks the trunk's own full-attention
+ * DecoderLayer after `fc`).  Those layers run mlx-lm's qwen3_5 Attention:
+ * q_proj gives q and an output gate per head, q_norm / k_norm are RMSNorms
+ * over the head dim, a rotary embedding covers the first
+ * partial_rotary_factor * head_dim dims, scaled dot-product attention over a
+ * KV cache ([B, Hkv, L, D], mlx-lm's KVCache layout), and the output is
+ * multiplied by sigmoid(gate) before o_proj.  bf16 activations throughout.
+ * --------------------------------------------------------------------- */
+
+/*
+ * q/k norm, rotary embedding and cache append for T new tokens per row:
+ *   qg       [B,T,Hq,2D]   q_proj output, per head q then gate; qg_ld
+ *            elements from one token to the next (0 = 2*Hq*D)
+ *   k_new    [B,T,Hkv,D];  v_new [B,T,Hkv,D]; token stride kv_ld (0 = Hkv*D)
+ *            (so q|gate, k and v may be column slices of one fused GEMM output)
+ *   q_norm_w, k_norm_w [D] (w_dtype); y = x / sqrt(mean(x^2) + eps) * w,
+ *            rounded to bf16 before the rotation
+ *   pos0     [B] int32 device: each row's cache length before this call
+ *            (= position of its first new token); clamped to [0, cap - T]
+ *   q_out    [B,T,Hq,D];  k_cache, v_cache [B,Hkv,cap,D]
+ *   rot      rotated dims (rotate-half pairs d, d + rot/2), angle
+ *            pos * rope_base^(-2i/rot) for i = d mod rot/2
+ * Requires D in {128, 256}.
+ */
+int gdn_attn_qk(const void* qg, int64_t qg_ld, const void* k_new, const void* v_new, int64_t kv_ld,
+                const void* q_norm_w, const void* k_norm_w, int w_dtype, float eps,
+                const int32_t* pos0, void* q_out, void* k_cache, void* v_cache, int64_t B,
+                int64_t T, int64_t Hq, int64_t Hkv, int64_t D, int64_t cap, int64_t rot,
+                float rope_base, void* stream);
+
+/* Workspace bytes gdn_attn_fwd needs for n_split > 1 (0 for n_split == 1). */
+size_t gdn_attn_workspace_bytes(int64_t B, int64_t T, int64_t Hq, int64_t Hkv, int64_t D,
+                                int64_t n_split);
+
+/*
+ * Causal GQA attention of the T new tokens of each row over its cache
+ * (keys 0 .. pos0[b] + t for token t; q-head h reads kv-head h / (Hq/Hkv)):
+ *   out[b,t,h] = softmax(scale * q . K^T) V, times sigmoid(gate) when qg is
+ *   not NULL (gate = second half of head h in qg [B,T,Hq,2D], token stride
+ *   qg_ld as in gdn_attn_qk).
+ *   kv_len_max  host bound of pos0[b] + T over the rows, in [T, cap]
+ *   n_split     key ranges per row processed by separate workgroups (decode
+ *               with long caches); > 1 needs gdn_attn_workspace_bytes.
+ * q, caches 16-byte aligned; out and qg 8-byte aligned.  D in {128, 256}.
+ */
+int gdn_attn_fwd(const void* q, const void* qg, int64_t qg_ld, const void* k_cache, const void* v_cache,
+                 const int32_t* pos0, void* out, float scale, int64_t B, int64_t T, int64_t Hq,
+                 int64_t Hkv, int64_t D, int64_t cap, int64_t kv_len_max, int64_t n_split,
+                 void* workspace, size_t workspace_bytes, void* stream);
+
+/* RMSNorm of bf16 rows (mlx nn.RMSNorm): y = x / sqrt(mean(x^2) + eps) * w.
+ * D a multiple of 8; x, y 16-byte aligned; y may alias x. */
+int gdn_rms_norm(const void* x, const void* w, int w_dtype, void* y, int64_t rows, int64_t D,
+                 float eps, void* stream);
+
+/* The MLP activation: out[r, i] = silu(gate_up[r, i]) * gate_up[r, I + i]
+ * (bf16; gate_up is one [rows, 2I] product of the gate and up projections). */
+int gdn_silu_mul(const void* gate_up, void* out, int64_t rows, int64_t I, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

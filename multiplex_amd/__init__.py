@@ -27,8 +27,14 @@ from . import prefix_state
 from .epilogue import gated_rms_norm, prepare_gated_rms_norm
 from .mixer import GatedDeltaNet, commit_verified
 from .mixed_step import MixedStep
+from .attention import Attention, AttentionArgs, DecoderLayer, KVCache, MTPHead
 
 __all__ = [
+    "Attention",
+    "AttentionArgs",
+    "DecoderLayer",
+    "KVCache",
+    "MTPHead",
     "ArraysCache",
     "GatedDeltaNet",
     "MixedStep",

@@ -42,6 +42,11 @@ EXPORTS = (
     "gdn_conv_prologue",
     "gdn_conv_state_commit",
     "gdn_gated_rmsnorm",
+    "gdn_attn_qk",
+    "gdn_attn_workspace_bytes",
+    "gdn_attn_fwd",
+    "gdn_rms_norm",
+    "gdn_silu_mul",
 )
 
 
@@ -142,6 +147,18 @@ _SIGNATURES = {
         c_int,
         [_P, _P, c_int, _I64, _I64, _P, c_int, _P, _I64, _I64, c_float, _P],
     ),
+    "gdn_attn_qk": (
+        c_int,
+        [_P, _I64, _P, _P, _I64, _P, _P, c_int, c_float, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64,
+         c_float, _P],
+    ),
+    "gdn_attn_workspace_bytes": (c_size_t, [_I64, _I64, _I64, _I64, _I64, _I64]),
+    "gdn_attn_fwd": (
+        c_int,
+        [_P, _P, _I64, _P, _P, _P, _P, c_float, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P, c_size_t, _P],
+    ),
+    "gdn_rms_norm": (c_int, [_P, _P, c_int, _P, _I64, _I64, c_float, _P]),
+    "gdn_silu_mul": (c_int, [_P, _P, _I64, _I64, _P]),
 }
 
 

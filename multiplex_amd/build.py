@@ -15,7 +15,14 @@ from pathlib import Path
 PKG_DIR = Path(__file__).resolve().parent
 CSRC = PKG_DIR / "csrc"
 LIB_PATH = PKG_DIR / "libgdn.so"
-SOURCES = ["gdn_api.hip", "gdn_recurrent.hip", "gdn_prologue.hip", "gdn_chunk.hip", "gdn_epilogue.hip"]
+SOURCES = [
+    "gdn_api.hip",
+    "gdn_recurrent.hip",
+    "gdn_prologue.hip",
+    "gdn_chunk.hip",
+    "gdn_epilogue.hip",
+    "gdn_attention.hip",
+]
 ARCH = "gfx950"
 
 # Packed-FP32 VALU ops are disabled for all device code; hipcc -O3 would

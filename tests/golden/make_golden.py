@@ -16,7 +16,11 @@ therefore computed by implementations independent of ``oracle/gdn.py``:
   module, run in bfloat16 (bf16 and fp32 weight) and in float32;
 * the whole mixer: transformers' ``Qwen3_5GatedDeltaNet`` module, run from
   given conv and recurrent states in float32 (prefill and single-token
-  decode) and in bfloat16.
+  decode) and in bfloat16;
+* the full-attention layer of the hybrid trunk: transformers'
+  ``Qwen3_5DecoderLayer`` and ``Qwen3_5Attention`` (float32, a prefill then
+  more tokens over its KV cache), and the MTP draft head composed from it as
+  ``multiplex/kernel/mtp.py:181-194`` composes it.
 
 Inputs are drawn from ``numpy.random.default_rng`` with fixed seeds.
 Run: ``python tests/golden/make_golden.py [case ...]`` (needs transformers;
@@ -234,6 +238,136 @@ def mixer_case(name, seed, B, S, hidden, Hk, Hv, D, dtype, Kt=4, eps=1e-6):
     )
 
 
+def _attn_config(hidden, Hq, Hkv, D, rot_factor, base, inter, eps):
+    from transformers.models.qwen3_5.configuration_qwen3_5 import Qwen3_5TextConfig
+
+    cfg = Qwen3_5TextConfig(hidden_size=hidden, num_attention_heads=Hq, num_key_value_heads=Hkv, head_dim=D,
+                            intermediate_size=inter, rms_norm_eps=eps, num_hidden_layers=1,
+                            layer_types=["full_attention"], attention_bias=False,
+                            rope_parameters={"rope_type": "default", "rope_theta": base,
+                                             "partial_rotary_factor": rot_factor})
+    cfg._attn_implementation = "eager"
+    return cfg
+
+
+def _causal_mask(B, T, offset, dtype):
+    """Additive mask [B,1,T,offset+T]: token t sees keys 0 .. offset + t."""
+    L = offset + T
+    keep = torch.arange(L)[None, :] <= (offset + torch.arange(T))[:, None]
+    m = torch.zeros(T, L, dtype=dtype).masked_fill(~keep, torch.finfo(dtype).min)
+    return m[None, None].expand(B, 1, T, L)
+
+
+def _decoder_layer(cfg, rng, hidden, Hq, Hkv, D, inter):
+    """transformers' Qwen3_5DecoderLayer at a full-attention index with random
+    weights; returns the module and its weights in mlx's convention (norm
+    weights w with y = x / rms * w; transformers keeps w - 1)."""
+    from transformers.models.qwen3_5.modeling_qwen3_5 import Qwen3_5DecoderLayer
+
+    layer = Qwen3_5DecoderLayer(cfg, 0).to(torch.float32)
+    sd = {
+        "self_attn.q_proj.weight": rng.normal(0.0, hidden ** -0.5, (2 * Hq * D, hidden)),
+        "self_attn.k_proj.weight": rng.normal(0.0, hidden ** -0.5, (Hkv * D, hidden)),
+        "self_attn.v_proj.weight": rng.normal(0.0, hidden ** -0.5, (Hkv * D, hidden)),
+        "self_attn.o_proj.weight": rng.normal(0.0, (Hq * D) ** -0.5, (hidden, Hq * D)),
+        "self_attn.q_norm.weight": rng.normal(0.0, 0.2, D),
+        "self_attn.k_norm.weight": rng.normal(0.0, 0.2, D),
+        "mlp.gate_proj.weight": rng.normal(0.0, hidden ** -0.5, (inter, hidden)),
+        "mlp.up_proj.weight": rng.normal(0.0, hidden ** -0.5, (inter, hidden)),
+        "mlp.down_proj.weight": rng.normal(0.0, inter ** -0.5, (hidden, inter)),
+        "input_layernorm.weight": rng.normal(0.0, 0.2, hidden),
+        "post_attention_layernorm.weight": rng.normal(0.0, 0.2, hidden),
+    }
+    with torch.no_grad():
+        for n, w in sd.items():
+            layer.get_parameter(n).copy_(torch.tensor(w, dtype=torch.float32))
+    mlx = {}
+    for n, prm in layer.named_parameters():
+        w = prm.detach().double().numpy()
+        mlx[n] = w + 1.0 if n.endswith("norm.weight") else w
+    return layer, mlx
+
+
+def attention_case(name, seed, B, T0, T1, hidden, Hq, Hkv, D, rot_factor, base, inter, eps=1e-6):
+    """transformers' Qwen3_5DecoderLayer (full attention: gated q_proj,
+    q/k RMSNorm, partial rotary embedding, GQA, SwiGLU MLP) and its
+    Qwen3_5Attention alone, in float32: a prefill of T0 tokens from an empty
+    cache, then T1 more tokens over that cache."""
+    from transformers import DynamicCache
+    from transformers.models.qwen3_5.modeling_qwen3_5 import Qwen3_5TextRotaryEmbedding
+
+    rng = np.random.default_rng(seed)
+    cfg = _attn_config(hidden, Hq, Hkv, D, rot_factor, base, inter, eps)
+    layer, mlx = _decoder_layer(cfg, rng, hidden, Hq, Hkv, D, inter)
+    rotary = Qwen3_5TextRotaryEmbedding(cfg)
+    x0 = rng.standard_normal((B, T0, hidden))
+    x1 = rng.standard_normal((B, T1, hidden))
+    out = {}
+    with torch.no_grad():
+        for tag, run in (("layer", lambda x, **kw: layer(x, **kw)),
+                         ("attn", lambda x, **kw: layer.self_attn(x, **kw)[0])):
+            cache = DynamicCache(config=cfg)
+            off = 0
+            for i, x in enumerate((x0, x1)):
+                xt = torch.tensor(x, dtype=torch.float32)
+                T = x.shape[1]
+                pos = torch.arange(off, off + T)[None].expand(B, T)
+                cos, sin = rotary(xt, pos)
+                y = run(xt, position_embeddings=(cos, sin), attention_mask=_causal_mask(B, T, off, torch.float32),
+                        position_ids=pos, past_key_values=cache)
+                out[f"{tag}_out{i}"] = y.double().numpy()
+                off += T
+    np.savez_compressed(
+        HERE / f"{name}.npz", x0=x0, x1=x1, dims=np.array([B, T0, T1, hidden, Hq, Hkv, D, inter], dtype=np.float64),
+        rot=np.array(int(D * rot_factor)), base=np.array(base), eps=np.array(eps), **out,
+        **{"p_" + k.replace(".", "__"): v for k, v in mlx.items()},
+    )
+
+
+def mtp_case(name, seed, B, L0, hidden, Hq, Hkv, D, rot_factor, base, inter, eps=1e-6):
+    """The MTP draft head as ``multiplex/kernel/mtp.py:181-194`` composes it:
+    plain RMSNorms (mlx ``nn.RMSNorm``, here torch.nn.functional.rms_norm) of
+    the embedding and of the trunk hidden, ``fc`` over their concatenation,
+    one transformers Qwen3_5DecoderLayer at a full-attention index, and a final
+    RMSNorm; float32.  A first call over L0 positions from an empty draft
+    cache, then one draft step over that cache."""
+    from transformers import DynamicCache
+    from transformers.models.qwen3_5.modeling_qwen3_5 import Qwen3_5TextRotaryEmbedding
+
+    rng = np.random.default_rng(seed)
+    cfg = _attn_config(hidden, Hq, Hkv, D, rot_factor, base, inter, eps)
+    layer, mlx = _decoder_layer(cfg, rng, hidden, Hq, Hkv, D, inter)
+    rotary = Qwen3_5TextRotaryEmbedding(cfg)
+    head = {
+        "pre_fc_norm_embedding": rng.normal(1.0, 0.2, hidden),
+        "pre_fc_norm_hidden": rng.normal(1.0, 0.2, hidden),
+        "fc": rng.normal(0.0, (2 * hidden) ** -0.5, (hidden, 2 * hidden)),
+        "norm": rng.normal(1.0, 0.2, hidden),
+    }
+    ht = {k: torch.tensor(v, dtype=torch.float32) for k, v in head.items()}
+    calls = [(rng.standard_normal((B, L, hidden)), rng.standard_normal((B, L, hidden))) for L in (L0, 1)]
+    out = {}
+    with torch.no_grad():
+        cache = DynamicCache(config=cfg)
+        off = 0
+        for i, (emb, hid) in enumerate(calls):
+            e = F.rms_norm(torch.tensor(emb, dtype=torch.float32), (hidden,), ht["pre_fc_norm_embedding"], eps)
+            h = F.rms_norm(torch.tensor(hid, dtype=torch.float32), (hidden,), ht["pre_fc_norm_hidden"], eps)
+            x = torch.cat([e, h], dim=-1) @ ht["fc"].T
+            T = x.shape[1]
+            pos = torch.arange(off, off + T)[None].expand(B, T)
+            x = layer(x, position_embeddings=rotary(x, pos), attention_mask=_causal_mask(B, T, off, torch.float32),
+                      position_ids=pos, past_key_values=cache)
+            out[f"out{i}"] = F.rms_norm(x, (hidden,), ht["norm"], eps).double().numpy()
+            out[f"embed{i}"], out[f"hidden{i}"] = emb, hid
+            off += T
+    np.savez_compressed(
+        HERE / f"{name}.npz", dims=np.array([B, L0, hidden, Hq, Hkv, D, inter], dtype=np.float64),
+        rot=np.array(int(D * rot_factor)), base=np.array(base), eps=np.array(eps), **out,
+        **{"h_" + k: v for k, v in head.items()}, **{"p_" + k.replace(".", "__"): v for k, v in mlx.items()},
+    )
+
+
 CASES = {
     "recurrent_small": lambda: recurrent_case("recurrent_small", 11, B=2, T=6, Hk=2, Hv=4, Dk=16, Dv=8),
     "recurrent_hd128": lambda: recurrent_case("recurrent_hd128", 12, B=1, T=3, Hk=2, Hv=4, Dk=128, Dv=128),
@@ -246,6 +380,10 @@ CASES = {
                                            dtype="f32"),
     "mixer_prefill_bf16": lambda: mixer_case("mixer_prefill_bf16", 18, B=2, S=6, hidden=48, Hk=2, Hv=4, D=16,
                                              dtype="bf16"),
+    "attention_layer_f32": lambda: attention_case("attention_layer_f32", 19, B=2, T0=5, T1=2, hidden=48, Hq=4,
+                                                  Hkv=2, D=16, rot_factor=0.5, base=1000.0, inter=40),
+    "mtp_head_f32": lambda: mtp_case("mtp_head_f32", 20, B=2, L0=3, hidden=48, Hq=4, Hkv=2, D=16, rot_factor=0.25,
+                                     base=10000.0, inter=40),
 }
 
 
