@@ -8,7 +8,8 @@ carried across back-to-back steps, inputs redrawn per step).  ``value`` is
 the algorithmic state+I/O bytes per step over the measured step time (GB/s);
 the JSON line also carries the other workloads of the path measured in the
 same run (decode B=1, MTP verify+commit, chunked prefill T=4096 with the
-fused conv prologue, and a mixed continuous-batching launch set), the
+fused conv prologue, a mixed continuous-batching launch set, and the
+full-attention layers of the hybrid trunk and the MTP draft head), the
 roofline of the dominant kernel and a CPU baseline.
 
 Usage: python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--no-cpu]
@@ -482,6 +483,90 @@ def bench_mixer_layer(torch, mx, dev, timer, iters=20, hidden=2048):
 
 # ------------------------------------------------------------ CPU baseline
 
+QWEN35_ATTN = dict(hidden_size=4096, num_attention_heads=16, num_key_value_heads=4, head_dim=256,
+                   intermediate_size=12288, rms_norm_eps=1e-6, partial_rotary_factor=0.25, rope_theta=1.0e7)
+
+
+def bench_attention(torch, mx, dev, timer, iters=20, L=4096):
+    """The full-attention path at Qwen3.5's attention shapes (Hq=16, Hkv=4,
+    D=256): GQA attention over a 4096-position KV cache for decode (B=64,
+    T=1) and draft verify (B=32, T=4) -- HBM-bound on the cache read -- and a
+    causal prefill of 4096 tokens (MFMA-bound); then one MTP draft step of a
+    one-layer head at hidden 4096 over the same cache length (weights plus
+    cache read per step).  Synthetic bf16 data, random weights."""
+    from multiplex_amd import attention as att
+
+    a = mx.AttentionArgs(**QWEN35_ATTN)
+    Hq, Hkv, D = a.num_attention_heads, a.num_key_value_heads, a.head_dim
+    gen = torch.Generator().manual_seed(1006)
+    res = {}
+
+    def kv(B, cap):
+        k = torch.randn(B, Hkv, cap, D, generator=gen).to(torch.bfloat16).to(dev)
+        return k, torch.randn(B, Hkv, cap, D, generator=gen).to(torch.bfloat16).to(dev)
+
+    for name, B, T in (("decode_b64", 64, 1), ("verify_b32_t4", 32, 4)):
+        kc, vc = kv(B, L)
+        q = torch.randn(B, T, Hq, D, generator=gen).to(torch.bfloat16).to(dev)
+        gate = torch.randn(B, T, Hq * 2 * D, generator=gen).to(torch.bfloat16).to(dev)
+        pos0 = torch.full((B,), L - T, dtype=torch.int32, device=dev)
+        layer = mx.Attention(a, device=dev)
+        ns = layer._splits(B, T, L)
+        ws = torch.empty(max(1, int(mx._lib.load().gdn_attn_workspace_bytes(B, T, Hq, Hkv, D, ns))),
+                         dtype=torch.uint8, device=dev)
+        out = torch.empty(B, T, Hq, D, dtype=torch.bfloat16, device=dev)
+        fn = lambda i: att.attn_fwd(q, kc, vc, pos0, L, gate=gate, n_split=ns, workspace=ws, out=out)
+        for i in range(3):
+            fn(i)
+        ms = timer.total_ms(fn, iters) / iters
+        byts = 2 * B * Hkv * L * D * 2 + 2 * q.numel() * 2 + gate.numel() * 2
+        res[f"attn_{name}"] = {"ms": round(ms, 5), "n_split": ns, "bytes": byts,
+                               "GB/s": round(byts / (ms * 1e-3) / 1e9, 1),
+                               "hbm_frac": round(byts / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+        del kc, vc
+
+    T = 4096
+    kc, vc = kv(1, T)
+    q = torch.randn(1, T, Hq, D, generator=gen).to(torch.bfloat16).to(dev)
+    pos0 = torch.zeros(1, dtype=torch.int32, device=dev)
+    out = torch.empty_like(q)
+    fn = lambda i: att.attn_fwd(q, kc, vc, pos0, T, out=out)
+    for i in range(3):
+        fn(i)
+    ms = timer.total_ms(fn, iters) / iters
+    flops = 4.0 * Hq * D * T * (T + 1) / 2
+    res["attn_prefill_t4096"] = {"ms": round(ms, 5), "gflop": round(flops / 1e9, 2),
+                                 "TFLOP/s": round(flops / (ms * 1e-3) / 1e12, 1),
+                                 "mfma_frac": round(flops / (ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4)}
+    del kc, vc
+
+    B = 64
+    head = mx.MTPHead(a, n_layers=1, device=dev)
+    cache = head.make_cache(B, L + 8)
+    c = cache[0]
+    c.keys.normal_()
+    c.values.normal_()
+    c.advance(L - 1)
+    H = a.hidden_size
+    emb = torch.randn(B, 1, H, generator=gen).to(torch.bfloat16).to(dev)
+    hid = torch.randn(B, 1, H, generator=gen).to(torch.bfloat16).to(dev)
+
+    def step(i):
+        head(emb, hid, cache)
+        c.trim(1)
+
+    for i in range(3):
+        step(i)
+    ms = timer.total_ms(step, iters) / iters
+    wbytes = sum(p.numel() * p.element_size() for p in head.parameters())
+    byts = wbytes + 2 * B * Hkv * L * D * 2
+    res["mtp_draft_step_b64"] = {"ms": round(ms, 5), "weight_bytes": wbytes, "kv_bytes": 2 * B * Hkv * L * D * 2,
+                                 "GB/s": round(byts / (ms * 1e-3) / 1e9, 1),
+                                 "hbm_frac": round(byts / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+    res["shapes"] = dict(QWEN35_ATTN, cache_len=L)
+    return res
+
+
 def cpu_model_name():
     """The host CPU's model name (as ``lscpu`` reports it), from /proc/cpuinfo."""
     try:
@@ -597,6 +682,8 @@ def main():
     ap.add_argument("--epilogue-only", action="store_true", help="only the gated RMSNorm epilogue workloads")
     ap.add_argument("--verify-only", action="store_true", help="only the B=32, T=4 verify + commit workload")
     ap.add_argument("--mixer-only", action="store_true", help="only the whole-mixer-layer workloads")
+    ap.add_argument("--attention-only", action="store_true",
+                    help="only the full-attention (trunk attention layer, MTP draft head) workloads")
     ap.add_argument("--pool-only", action="store_true",
                     help="only the pooled-state and prefix-cache state-record workloads")
     ap.add_argument("--hbm-ceiling", action="store_true",
@@ -650,6 +737,9 @@ def main():
     if args.mixer_only:
         print(json.dumps({"mixer_layer": bench_mixer_layer(torch, mx, dev, timer, iters=args.steps)}), flush=True)
         return
+    if args.attention_only:
+        print(json.dumps({"attention": bench_attention(torch, mx, dev, timer, iters=args.steps)}), flush=True)
+        return
     if args.verify_only:
         print(json.dumps({"verify_b32_t4": bench_verify(torch, mx, dev, timer, iters=args.steps)}), flush=True)
         return
@@ -686,6 +776,7 @@ def main():
         configs["state_pool"] = bench_pool(torch, mx, dev, timer)
         configs["prefix_state"] = bench_prefix_state(torch, mx, dev)
         configs["mixer_layer"] = bench_mixer_layer(torch, mx, dev, timer)
+        configs["attention"] = bench_attention(torch, mx, dev, timer)
     base = None if args.no_cpu else cpu_baseline(torch)
 
     line = {

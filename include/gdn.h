@@ -332,10 +332,14 @@ int gdn_attn_fwd(const void* q, const void* qg, int64_t qg_ld, const void* k_cac
                  int64_t Hkv, int64_t D, int64_t cap, int64_t kv_len_max, int64_t n_split,
                  void* workspace, size_t workspace_bytes, void* stream);
 
-/* RMSNorm of bf16 rows (mlx nn.RMSNorm): y = x / sqrt(mean(x^2) + eps) * w.
- * D a multiple of 8; x, y 16-byte aligned; y may alias x. */
-int gdn_rms_norm(const void* x, const void* w, int w_dtype, void* y, int64_t rows, int64_t D,
-                 float eps, void* stream);
+/* RMSNorm of bf16 rows (mlx nn.RMSNorm): y = h / sqrt(mean(h^2) + eps) * w
+ * with h = x, or h = bf16(x + res) when res is not NULL (a residual add
+ * fused in front; h is written to h_out when not NULL, which may alias x).
+ * y's rows are y_ld elements apart (0 = D), e.g. one half of a
+ * concatenation.  D a multiple of 8; pointers 16-byte aligned; y may alias x
+ * when y_ld == D and h_out is NULL. */
+int gdn_rms_norm(const void* x, const void* res, void* h_out, const void* w, int w_dtype, void* y,
+                 int64_t y_ld, int64_t rows, int64_t D, float eps, void* stream);
 
 /* The MLP activation: out[r, i] = silu(gate_up[r, i]) * gate_up[r, I + i]
  * (bf16; gate_up is one [rows, 2I] product of the gate and up projections). */

@@ -157,7 +157,7 @@ _SIGNATURES = {
         c_int,
         [_P, _P, _I64, _P, _P, _P, _P, c_float, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P, c_size_t, _P],
     ),
-    "gdn_rms_norm": (c_int, [_P, _P, c_int, _P, _I64, _I64, c_float, _P]),
+    "gdn_rms_norm": (c_int, [_P, _P, _P, _P, c_int, _P, _I64, _I64, _I64, c_float, _P]),
     "gdn_silu_mul": (c_int, [_P, _P, _I64, _I64, _P]),
 }
 

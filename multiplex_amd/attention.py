@@ -90,6 +90,22 @@ def _token_stride(t: torch.Tensor, width: int, what: str) -> int:
     return int(ld)
 
 
+def _row_stride(t: torch.Tensor, D: int) -> int:
+    """Elements between consecutive rows of a ``[..., D]`` tensor whose rows
+    are contiguous and evenly spaced (a column slice of a wider buffer)."""
+    if t.stride(-1) != 1:
+        raise ValueError("rows must be contiguous")
+    if t.dim() == 1:
+        return D
+    ld = t.stride(-2)
+    for i in range(t.dim() - 2):
+        if t.shape[i] > 1 and t.stride(i) != t.shape[i + 1] * t.stride(i + 1):
+            raise ValueError("rows must be evenly spaced")
+    if ld < D:
+        raise ValueError("rows overlap")
+    return int(ld)
+
+
 def attn_qk(qg: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor, q_norm_w: torch.Tensor,
             k_norm_w: torch.Tensor, eps: float, pos0: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
             rot: int, rope_base: float, *, q_out: Optional[torch.Tensor] = None) -> torch.Tensor:
@@ -152,20 +168,35 @@ def attn_fwd(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, pos0
     return out
 
 
-def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float, *, out: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """``x / sqrt(mean(x^2) + eps) * weight`` over the last dim (bf16 x)."""
-    dev = _require_device([x, weight], ["x", "weight"])
+def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float, *, residual: Optional[torch.Tensor] = None,
+             out: Optional[torch.Tensor] = None):
+    """``h / sqrt(mean(h^2) + eps) * weight`` over the last dim (bf16), with
+    ``h = x`` or, given ``residual``, ``h = x + residual`` (one launch; then
+    returns ``(h, y)``).  ``out`` may be a column slice of a wider buffer
+    (rows one stride apart), e.g. one half of a concatenation."""
+    dev = _require_device([x, weight, residual, out], ["x", "weight", "residual", "out"])
     _bf16(x, "x")
     D = x.shape[-1]
     if tuple(weight.shape) != (D,):
         raise ValueError(f"weight must be [{D}]")
     x = x.contiguous()
+    rows = x.numel() // D
     if out is None:
         out = torch.empty_like(x)
+        y_ld = D
+    else:
+        if out.shape != x.shape:
+            raise ValueError("out must have x's shape")
+        y_ld = _row_stride(out, D)
+    h = None
+    if residual is not None:
+        _bf16(residual, "residual")
+        residual = residual.contiguous()
+        h = torch.empty_like(x)
     w = weight.contiguous()
-    _lib.call("gdn_rms_norm", _ptr(x), _ptr(w), _dtype_code(w, "weight"), _ptr(out), x.numel() // D, D, float(eps),
-              _stream(dev))
-    return out
+    _lib.call("gdn_rms_norm", _ptr(x), _ptr(residual), _ptr(h), _ptr(w), _dtype_code(w, "weight"), _ptr(out), y_ld,
+              rows, D, float(eps), _stream(dev))
+    return out if residual is None else (h, out)
 
 
 def silu_mul(gate_up: torch.Tensor) -> torch.Tensor:
@@ -286,8 +317,10 @@ class RMSNorm(torch.nn.Module):
         self.weight = torch.nn.Parameter(torch.ones(dim, device=device), requires_grad=False)
         self.eps = eps
 
-    def forward(self, x: torch.Tensor) -> torch.Tensor:
-        return rms_norm(x, self.weight, self.eps)
+    def forward(self, x: torch.Tensor, residual: Optional[torch.Tensor] = None,
+                out: Optional[torch.Tensor] = None):
+        """norm(x), or ``(x + residual, norm(x + residual))`` in one launch."""
+        return rms_norm(x, self.weight, self.eps, residual=residual, out=out)
 
 
 class Attention(torch.nn.Module):
@@ -311,6 +344,7 @@ class Attention(torch.nn.Module):
         self.k_norm = RMSNorm(D, args.rms_norm_eps, device)
         self.scale = D ** -0.5
         self.n_split = n_split
+        self._cus = None
 
     @torch.no_grad()
     def load(self, q_proj, k_proj, v_proj, o_proj, q_norm, k_norm) -> None:
@@ -320,13 +354,16 @@ class Attention(torch.nn.Module):
         self.k_norm.weight.copy_(k_norm)
 
     def _splits(self, B: int, T: int, L: int) -> int:
+        """Key ranges per row for decode and draft verify: about one
+        workgroup per CU (measured best: one 68 KB-LDS workgroup per CU
+        streams the cache faster than two), ranges of at least 512 keys."""
         if self.n_split is not None:
             return self.n_split
         if T * (self.Hq // self.Hkv) > 16:
             return 1
-        # decode / draft verify: enough workgroups to cover the CUs, keys in ranges of >= 256
-        blocks = B * self.Hkv
-        return int(max(1, min(-(-1024 // blocks), L // 256)))
+        if self._cus is None:
+            self._cus = torch.cuda.get_device_properties(self.qkv_proj.device).multi_processor_count
+        return int(max(1, min(round(self._cus / (B * self.Hkv)), L // 512)))
 
     def forward(self, x: torch.Tensor, cache: KVCache) -> torch.Tensor:
         B, T, _ = x.shape
@@ -373,8 +410,9 @@ class DecoderLayer(torch.nn.Module):
         self.post_attention_layernorm = RMSNorm(args.hidden_size, args.rms_norm_eps, device)
 
     def forward(self, x: torch.Tensor, cache: KVCache) -> torch.Tensor:
-        h = x + self.self_attn(self.input_layernorm(x), cache)
-        return h + self.mlp(self.post_attention_layernorm(h))
+        # the residual add in front of the second norm is fused into it
+        h, y = self.post_attention_layernorm(x, residual=self.self_attn(self.input_layernorm(x), cache))
+        return h + self.mlp(y)
 
 
 class MTPHead(torch.nn.Module):
@@ -401,9 +439,12 @@ class MTPHead(torch.nn.Module):
         """Post-norm hidden ``[B, L, H]``; each draft layer's cache advances by L."""
         if len(cache) != len(self.layers):
             raise ValueError(f"expected {len(self.layers)} draft caches, got {len(cache)}")
-        e = self.pre_fc_norm_embedding(embed)
-        h = self.pre_fc_norm_hidden(hidden)
-        x = torch.nn.functional.linear(torch.cat([e, h], dim=-1), self.fc)
+        # both norms write their halves of fc's input in place of a concatenation
+        H = embed.shape[-1]
+        eh = torch.empty(*embed.shape[:-1], 2 * H, dtype=embed.dtype, device=embed.device)
+        self.pre_fc_norm_embedding(embed, out=eh[..., :H])
+        self.pre_fc_norm_hidden(hidden, out=eh[..., H:])
+        x = torch.nn.functional.linear(eh, self.fc)
         for layer, c in zip(self.layers, cache):
             x = layer(x, c)
         return self.norm(x)

@@ -21,7 +21,8 @@
 //                        states then go to a workspace and
 //   attn_combine_kernel  merges them.  The output is multiplied by
 //                        sigmoid(gate) on the way out when a gate is given.
-//   rms_norm_kernel      the layers' RMSNorm over the hidden size.
+//   rms_norm_kernel      the layers' RMSNorm over the hidden size, optionally of
+//                        a residual sum it also writes out.
 //   silu_mul_kernel      the MLP's silu(gate) * up.
 #include "gdn_common.hpp"
 
@@ -458,14 +459,30 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const AttnParams p) {
 
 // ------------------------------------------------------------ rms_norm
 
-// One workgroup per row; 8 bf16 elements per thread and pass.
-__global__ __launch_bounds__(256) void rms_norm_kernel(const uint16_t* x, const void* w, int wdt, uint16_t* y,
-                                                       int D, float eps) {
+// One workgroup per row; 8 bf16 elements per thread and pass.  With a
+// residual, the row is h = bf16(x + res) (written to h_out when given) and
+// y = norm(h); y's rows are y_ld elements apart.
+__global__ __launch_bounds__(256) void rms_norm_kernel(const uint16_t* x, const uint16_t* res, uint16_t* h_out,
+                                                       const void* w, int wdt, uint16_t* y, int64_t y_ld, int D,
+                                                       float eps) {
   const int64_t row = blockIdx.x;
   const uint16_t* xr = x + row * D;
+  const uint16_t* rr = res != nullptr ? res + row * D : nullptr;
+  auto load_h = [&](int c) {
+    u32x4 v = *reinterpret_cast<const u32x4*>(xr + c);
+    if (rr != nullptr) {
+      const u32x4 r = *reinterpret_cast<const u32x4*>(rr + c);
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        v[k] = pk_bf16(__uint_as_float(v[k] << 16) + __uint_as_float(r[k] << 16),
+                       __uint_as_float(v[k] & 0xffff0000u) + __uint_as_float(r[k] & 0xffff0000u));
+    }
+    return v;
+  };
   float ss = 0.0f;
   for (int c = 8 * threadIdx.x; c < D; c += 8 * 256) {
-    const u32x4 v = *reinterpret_cast<const u32x4*>(xr + c);
+    const u32x4 v = load_h(c);
+    if (h_out != nullptr) *reinterpret_cast<u32x4*>(h_out + row * D + c) = v;
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
       const float a = __uint_as_float(v[k] << 16), bb = __uint_as_float(v[k] & 0xffff0000u);
@@ -478,7 +495,8 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const uint16_t* x, const 
   __syncthreads();
   const float r = rsqrtf((part[0] + part[1] + part[2] + part[3]) / D + eps);
   for (int c = 8 * threadIdx.x; c < D; c += 8 * 256) {
-    const u32x4 v = *reinterpret_cast<const u32x4*>(xr + c);
+    // h again: from h_out when this thread wrote it (which may alias x), else recomputed
+    const u32x4 v = h_out != nullptr ? *reinterpret_cast<const u32x4*>(h_out + row * D + c) : load_h(c);
     u32x4 o;
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
@@ -486,7 +504,7 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const uint16_t* x, const 
       const float bb = __uint_as_float(v[k] & 0xffff0000u) * r * load_any(w, wdt, c + 2 * k + 1);
       o[k] = pk_bf16(a, bb);
     }
-    *reinterpret_cast<u32x4*>(y + row * D + c) = o;
+    *reinterpret_cast<u32x4*>(y + row * y_ld + c) = o;
   }
 }
 
@@ -639,17 +657,22 @@ extern "C" int gdn_attn_fwd(const void* q, const void* qg, int64_t qg_ld, const 
   return gdn_host::check_launch("gdn_attn_fwd/combine");
 }
 
-extern "C" int gdn_rms_norm(const void* x, const void* w, int w_dtype, void* y, int64_t rows, int64_t D, float eps,
-                            void* stream) {
+extern "C" int gdn_rms_norm(const void* x, const void* res, void* h_out, const void* w, int w_dtype, void* y,
+                            int64_t y_ld, int64_t rows, int64_t D, float eps, void* stream) {
   using gdn_host::fail;
   if (rows < 0 || D <= 0 || D % 8 != 0 || D > INT32_MAX || rows > INT32_MAX)
     return fail(GDN_ERR_INVALID, "gdn_rms_norm: bad sizes (D must be a multiple of 8)");
+  if (y_ld == 0) y_ld = D;
+  if (y_ld < D || y_ld % 8 != 0) return fail(GDN_ERR_INVALID, "gdn_rms_norm: y row stride must be >= D and a multiple of 8");
   if (!gdn_host::dtype_ok(w_dtype) || !(eps >= 0.0f)) return fail(GDN_ERR_INVALID, "gdn_rms_norm: bad weight dtype or eps");
   if (rows == 0) return GDN_OK;
   if (!x || !w || !y) return fail(GDN_ERR_INVALID, "gdn_rms_norm: null pointer");
-  if (!gdn_host::aligned(x, 16) || !gdn_host::aligned(y, 16)) return fail(GDN_ERR_INVALID, "gdn_rms_norm: misaligned pointer");
+  if (!gdn_host::aligned(x, 16) || !gdn_host::aligned(y, 16) || (res && !gdn_host::aligned(res, 16)) ||
+      (h_out && !gdn_host::aligned(h_out, 16)))
+    return fail(GDN_ERR_INVALID, "gdn_rms_norm: misaligned pointer");
   hipLaunchKernelGGL(rms_norm_kernel, dim3(static_cast<unsigned>(rows)), dim3(256), 0, static_cast<hipStream_t>(stream),
-                     static_cast<const uint16_t*>(x), w, w_dtype, static_cast<uint16_t*>(y), static_cast<int>(D), eps);
+                     static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(res), static_cast<uint16_t*>(h_out),
+                     w, w_dtype, static_cast<uint16_t*>(y), y_ld, static_cast<int>(D), eps);
   return gdn_host::check_launch("gdn_rms_norm");
 }
 

@@ -70,6 +70,24 @@ def test_qk_prep_matches_oracle():
         assert not kc_n[b, :, untouched].any() and not vc_n[b, :, untouched].any()
 
 
+def test_rms_norm_residual_and_strided_output():
+    """``gdn_rms_norm`` with a fused residual add (h = bf16(x + r), written
+    out) and its output in one half of a concatenation buffer, against
+    torch.nn.functional.rms_norm in float64."""
+    gen = torch.Generator().manual_seed(77)
+    rows, H = 37, 4096
+    x, r = _bf16(gen, rows, H, scale=3.0), _bf16(gen, rows, H)
+    w = torch.randn(H, generator=gen) * 0.2 + 1.0
+    buf = torch.zeros(rows, 2 * H, dtype=torch.bfloat16, device=DEV)
+    h, y = att.rms_norm(x.to(DEV), w.to(DEV), 1e-6, residual=r.to(DEV), out=buf[:, H:])
+    torch.cuda.synchronize()
+    h_ref = (x.float() + r.float()).to(torch.bfloat16)
+    assert torch.equal(h.cpu(), h_ref)
+    ref = torch.nn.functional.rms_norm(h_ref.double(), (H,), w.double(), 1e-6).numpy()
+    assert _row_errs(_np(buf[:, H:]), ref).max() < 4e-3
+    assert not buf[:, :H].any()
+
+
 CASES = {
     # name: (B, T, pos0, n_split, gate)
     "decode": (8, 1, [0, 1, 63, 64, 65, 300, 511, 700], 1, True),
