@@ -675,6 +675,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--decode-only", action="store_true", help="only the B=64 decode workload")
+    ap.add_argument("--decode-b1-only", action="store_true", help="only the B=1 decode workload")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 256 MiB device-to-device copy (counter calibration) and exit")
     ap.add_argument("--prefill-only", action="store_true", help="only the T=4096 prefill workload")
@@ -736,6 +737,9 @@ def main():
         return
     if args.mixer_only:
         print(json.dumps({"mixer_layer": bench_mixer_layer(torch, mx, dev, timer, iters=args.steps)}), flush=True)
+        return
+    if args.decode_b1_only:
+        print(json.dumps({"decode_b1": bench_decode_b1(torch, mx, dev, timer, iters=args.steps)}), flush=True)
         return
     if args.attention_only:
         print(json.dumps({"attention": bench_attention(torch, mx, dev, timer, iters=args.steps)}), flush=True)
