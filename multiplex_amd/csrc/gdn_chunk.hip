@@ -595,7 +595,7 @@ struct WaveOps {
   bf16x8 th[2], tl[2];   // T rows 16w + lr, columns 32s + 8lq .. (hi / lo)
   bf16x8 ph[2], pl[2];   // P rows, same layout
   bf16x8 kt[2][2];       // K^T rows 32w + 16j + lr, columns 32s + 8lq ..
-  uint16_t v[4];         // V[16w + 4lq + i][dv0 + lr] (bf16 bits)
+  uint16_t v[2][4];      // V[16w + 4lq + i][dv0 + 16t + lr] (bf16 bits) of tile t
   f32x4 g, b, e;         // gamma / beta / e of tokens 16w + 4lq + i (KT_LDS: .x of token 16w + 4lq + lr % 4)
   float gy;              // gamma of token 16w + lr
   float gC;              // gamma of the chunk's last token
@@ -617,7 +617,12 @@ constexpr int kCUs = 256;  // compute units of an MI355X (8 XCDs x 32)
 // operand loads per chunk for 16 KB of LDS writes and reads: it pays when
 // several workgroups share a CU, and costs a little on the chain when one
 // workgroup has the CU to itself.
-template <bool KT_LDS>
+// TPW: 16-row state tiles per workgroup.  With two, every operand a wave
+// loads (K, Q, T, P, K^T, gates) serves 32 state rows: half the operand
+// bytes per row, for a longer chain per chunk (twice the MFMAs and LDS
+// exchanges per wave).  It pays when the tiles outnumber the CUs and the
+// operand traffic, not one long chain, bounds the scan.
+template <bool KT_LDS, int TPW>
 __global__ __launch_bounds__(256) void chunk_scan_kernel(const ChunkParams p) {
   // Block b runs on XCD b % 8.  The v-heads of one k-head (a GQA group,
   // which share its K, Q and K^T) form a unit; units (over all sequences,
@@ -625,8 +630,9 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(const ChunkParams p) {
   // each head go to the unit's XCD, where they share its operands in L2.
   const int blk = blockIdx.x;
   const int xcd = blk % kXcds, r8 = blk / kXcds;
-  const int tile = r8 % kTiles;
-  const int slot_x = r8 / kTiles;  // head slot on this XCD
+  constexpr int kWgs = kTiles / TPW;  // workgroups per head
+  const int tile = r8 % kWgs;
+  const int slot_x = r8 / kWgs;  // head slot on this XCD
   const int head_rank = ((slot_x / p.group) * kXcds + xcd) * p.group + slot_x % p.group;
   if (head_rank >= p.n_seqs * p.Hv) return;
   const int seq = p.order != nullptr ? p.order[head_rank / p.Hv] : head_rank / p.Hv;
@@ -636,7 +642,7 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(const ChunkParams p) {
     if (slot < 0 || slot >= p.n_slots) return;  // uniform, before any barrier
   }
   const int hv = head_rank % p.Hv;
-  const int dv0 = tile * DVT;
+  const int dv0 = tile * DVT * TPW;
   const int hk = hv / p.group;
   const int hv_k = hk * p.group;  // the v-head whose record holds this k-head's K^T
   const int tid = threadIdx.x, lane = tid & 63;
@@ -645,10 +651,11 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(const ChunkParams p) {
   const SeqRange sr = seq_range(p, seq);
   const int nch = n_chunks(sr.len);
 
-  __shared__ __align__(16) uint16_t Sh[DVT][KP], Sl[DVT][KP];  // S0 [row][dk], hi / lo
-  __shared__ __align__(16) uint16_t Rh[DVT][CP], Rl[DVT][CP];  // R^T [row][token]
-  __shared__ __align__(16) uint16_t Uh[DVT][CP], Ul[DVT][CP];  // U^T
-  __shared__ __align__(16) uint16_t Eh[DVT][CP], El[DVT][CP];  // (diag(e) U)^T
+  constexpr int NR = DVT * TPW;  // state rows of this workgroup; tile t holds rows 16t ..
+  __shared__ __align__(16) uint16_t Sh[NR][KP], Sl[NR][KP];  // S0 [row][dk], hi / lo
+  __shared__ __align__(16) uint16_t Rh[NR][CP], Rl[NR][CP];  // R^T [row][token]
+  __shared__ __align__(16) uint16_t Uh[NR][CP], Ul[NR][CP];  // U^T
+  __shared__ __align__(16) uint16_t Eh[NR][CP], El[NR][CP];  // (diag(e) U)^T
   __shared__ __align__(16) uint16_t Kl[KT_LDS ? CH : 1][KP];   // K [token][dk] (KT_LDS)
 
   // Loop-invariant lane offsets (bytes) into the per-chunk descriptors:
@@ -699,8 +706,10 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(const ChunkParams p) {
     });
   };
   auto load_vg = [&](const ChunkBufs& c) {
-    static_for<4>([&](auto i) {
-      o.v[i.value] = __builtin_amdgcn_raw_buffer_load_b16(c.v, off_v[i.value], 0, 0);
+    static_for<TPW>([&](auto t) {
+      static_for<4>([&](auto i) {
+        o.v[t.value][i.value] = __builtin_amdgcn_raw_buffer_load_b16(c.v, off_v[i.value] + 32 * t.value, 0, 0);
+      });
     });
     if constexpr (KT_LDS) {
       o.g.x = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(c.rec, off_gq, 0, 0));
@@ -756,19 +765,27 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(const ChunkParams p) {
     });
   };
 
-  // This wave's 32 x 16 slice of S^T: state columns [32w, 32w+32) as two
-  // 16x16 accumulator tiles; lane holds S^T[32w + 16j + 4lq + i][lr], i.e.
-  // 4 consecutive columns of state row dv0 + lr.
+  // This wave's 32 x 16 slices of S^T, one per tile t: state columns
+  // [32w, 32w+32) as two 16x16 accumulator tiles; lane holds
+  // S^T[32w + 16j + 4lq + i][lr], i.e. 4 consecutive columns of state row
+  // dv0 + 16t + lr.
   const int64_t srow = (static_cast<int64_t>(slot) * p.Hv + hv) * DV + dv0 + lr;
-  f32x4 sacc[2];
+  f32x4 sacc[TPW][2];
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int64_t idx = srow * DK + 32 * wave + 16 * j + 4 * lq;
-    sacc[j] = p.state_in != nullptr ? *reinterpret_cast<const f32x4*>(p.state_in + idx) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-  }
+  for (int t = 0; t < TPW; ++t)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int64_t idx = (srow + 16 * t) * DK + 32 * wave + 16 * j + 4 * lq;
+      sacc[t][j] =
+          p.state_in != nullptr ? *reinterpret_cast<const f32x4*>(p.state_in + idx) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
   auto write_state = [&]() {
 #pragma unroll
-    for (int j = 0; j < 2; ++j) split4_store(sacc[j], &Sh[lr][32 * wave + 16 * j + 4 * lq], &Sl[lr][32 * wave + 16 * j + 4 * lq]);
+    for (int t = 0; t < TPW; ++t)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        split4_store(sacc[t][j], &Sh[16 * t + lr][32 * wave + 16 * j + 4 * lq],
+                     &Sl[16 * t + lr][32 * wave + 16 * j + 4 * lq]);
   };
 
   const ChunkBufs c0 = bufs_here();  // chunk 0 (only used when the sequence has chunks)
@@ -792,15 +809,19 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(const ChunkParams p) {
     __syncthreads();  // state hi/lo of this chunk is in LDS
 
     // ---- X_K = K S0^T (tokens x rows) and X_Q^T = S0 Q^T (rows x tokens)
-    f32x4 xk0 = z, xk1 = z, xq0 = z, xq1 = z;
+    f32x4 xk0[TPW], xk1[TPW], xq0[TPW], xq1[TPW];
+#pragma unroll
+    for (int t = 0; t < TPW; ++t) xk0[t] = xk1[t] = xq0[t] = xq1[t] = z;
     static_for<4>([&](auto s) {
       const int kc = 32 * s.value + lg8;
-      const bf16x8 sh = lds8(&Sh[lr][kc]);
-      const bf16x8 sl = lds8(&Sl[lr][kc]);
-      xk0 = mfma16(o.k[s.value], sh, xk0);
-      xk1 = mfma16(o.k[s.value], sl, xk1);
-      xq0 = mfma16(sh, o.q[s.value], xq0);
-      xq1 = mfma16(sl, o.q[s.value], xq1);
+      static_for<TPW>([&](auto t) {
+        const bf16x8 sh = lds8(&Sh[16 * t.value + lr][kc]);
+        const bf16x8 sl = lds8(&Sl[16 * t.value + lr][kc]);
+        xk0[t.value] = mfma16(o.k[s.value], sh, xk0[t.value]);
+        xk1[t.value] = mfma16(o.k[s.value], sl, xk1[t.value]);
+        xq0[t.value] = mfma16(sh, o.q[s.value], xq0[t.value]);
+        xq1[t.value] = mfma16(sl, o.q[s.value], xq1[t.value]);
+      });
     });
     if constexpr (KT_LDS) {
       // this wave's K rows to LDS (read transposed after the next barrier),
@@ -812,13 +833,14 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(const ChunkParams p) {
     load_kq(cn);
 
     // ---- R = beta (V - gamma X_K) -> R^T
-    {
+    static_for<TPW>([&](auto t) {
       f32x4 r;
       static_for<4>([&](auto i) {
-        r[i.value] = tok4(o.b, i) * (bf16_to_f32(o.v[i.value]) - tok4(o.g, i) * (xk0[i.value] + xk1[i.value]));
+        r[i.value] = tok4(o.b, i) * (bf16_to_f32(o.v[t.value][i.value]) -
+                                     tok4(o.g, i) * (xk0[t.value][i.value] + xk1[t.value][i.value]));
       });
-      split4_store(r, &Rh[lr][16 * wave + 4 * lq], &Rl[lr][16 * wave + 4 * lq]);
-    }
+      split4_store(r, &Rh[16 * t.value + lr][16 * wave + 4 * lq], &Rl[16 * t.value + lr][16 * wave + 4 * lq]);
+    });
     const float gy = o.gy;  // kept for Y
     load_vg(cn);
     __syncthreads();  // R^T complete
@@ -837,63 +859,79 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(const ChunkParams p) {
     });
 
     // ---- U = T R for this wave's 16 tokens
-    f32x4 u0 = z, u1 = z;
+    f32x4 u0[TPW], u1[TPW];
+#pragma unroll
+    for (int t = 0; t < TPW; ++t) u0[t] = u1[t] = z;
     static_for<2>([&](auto s) {
       if (s.value == 1 && !full_rows) return;
       const int kc = 32 * s.value + lg8;
-      const bf16x8 rh = lds8(&Rh[lr][kc]);
-      u0 = mfma16(o.th[s.value], rh, u0);
-      u1 = mfma16(o.th[s.value], lds8(&Rl[lr][kc]), u1);
-      u1 = mfma16(o.tl[s.value], rh, u1);
+      static_for<TPW>([&](auto t) {
+        const bf16x8 rh = lds8(&Rh[16 * t.value + lr][kc]);
+        u0[t.value] = mfma16(o.th[s.value], rh, u0[t.value]);
+        u1[t.value] = mfma16(o.th[s.value], lds8(&Rl[16 * t.value + lr][kc]), u1[t.value]);
+        u1[t.value] = mfma16(o.tl[s.value], rh, u1[t.value]);
+      });
     });
     load_t(cn);
     {
-      const f32x4 uv = u0 + u1;
-      split4_store(uv, &Uh[lr][16 * wave + 4 * lq], &Ul[lr][16 * wave + 4 * lq]);
       const f32x4 ev = {tok4(o.e, std::integral_constant<int, 0>{}), tok4(o.e, std::integral_constant<int, 1>{}),
                         tok4(o.e, std::integral_constant<int, 2>{}), tok4(o.e, std::integral_constant<int, 3>{})};
-      split4_store(ev * uv, &Eh[lr][16 * wave + 4 * lq], &El[lr][16 * wave + 4 * lq]);
+      static_for<TPW>([&](auto t) {
+        const f32x4 uv = u0[t.value] + u1[t.value];
+        split4_store(uv, &Uh[16 * t.value + lr][16 * wave + 4 * lq], &Ul[16 * t.value + lr][16 * wave + 4 * lq]);
+        split4_store(ev * uv, &Eh[16 * t.value + lr][16 * wave + 4 * lq], &El[16 * t.value + lr][16 * wave + 4 * lq]);
+      });
     }
     load_e(cn);
     __syncthreads();  // U^T, (eU)^T complete
 
     // ---- S^T = gamma_C S0^T + K^T (diag(e) U) on this wave's 32 columns
 #pragma unroll
-    for (int j = 0; j < 2; ++j) sacc[j] *= o.gC;
+    for (int t = 0; t < TPW; ++t)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) sacc[t][j] *= o.gC;
     static_for<2>([&](auto s) {
       const int kc = 32 * s.value + lg8;
-      const bf16x8 eh = lds8(&Eh[lr][kc]);
-      const bf16x8 el = lds8(&El[lr][kc]);
-      static_for<2>([&](auto j) {
-        sacc[j.value] = mfma16(kt[j.value][s.value], eh, sacc[j.value]);
-        sacc[j.value] = mfma16(kt[j.value][s.value], el, sacc[j.value]);
+      static_for<TPW>([&](auto t) {
+        const bf16x8 eh = lds8(&Eh[16 * t.value + lr][kc]);
+        const bf16x8 el = lds8(&El[16 * t.value + lr][kc]);
+        static_for<2>([&](auto j) {
+          sacc[t.value][j.value] = mfma16(kt[j.value][s.value], eh, sacc[t.value][j.value]);
+          sacc[t.value][j.value] = mfma16(kt[j.value][s.value], el, sacc[t.value][j.value]);
+        });
       });
     });
     load_kt(cn);
     write_state();  // every wave read S0 before the R^T barrier
 
     // ---- Y^T = gamma X_Q^T + U^T P^T (rows x this wave's 16 tokens)
-    f32x4 y0 = z, y1 = z;
+    f32x4 y0[TPW], y1[TPW];
+#pragma unroll
+    for (int t = 0; t < TPW; ++t) y0[t] = y1[t] = z;
     static_for<2>([&](auto s) {
       if (s.value == 1 && !full_rows) return;
       const int kc = 32 * s.value + lg8;
-      const bf16x8 uh = lds8(&Uh[lr][kc]);
-      y0 = mfma16(uh, o.ph[s.value], y0);
-      y1 = mfma16(lds8(&Ul[lr][kc]), o.ph[s.value], y1);
-      y1 = mfma16(uh, o.pl[s.value], y1);
+      static_for<TPW>([&](auto t) {
+        const bf16x8 uh = lds8(&Uh[16 * t.value + lr][kc]);
+        y0[t.value] = mfma16(uh, o.ph[s.value], y0[t.value]);
+        y1[t.value] = mfma16(lds8(&Ul[16 * t.value + lr][kc]), o.ph[s.value], y1[t.value]);
+        y1[t.value] = mfma16(uh, o.pl[s.value], y1[t.value]);
+      });
     });
     load_p(cn);
-    {
-      const f32x4 yv = gy * (xq0 + xq1) + (y0 + y1);
+    static_for<TPW>([&](auto t) {
+      const f32x4 yv = gy * (xq0[t.value] + xq1[t.value]) + (y0[t.value] + y1[t.value]);
       const bf16x4 yb = __builtin_convertvector(yv, bf16x4);
-      __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, yb), y_cur, off_y, 0, 0);
-    }
+      __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, yb), y_cur, off_y + 32 * t.value, 0, 0);
+    });
     y_cur = cn.y;
   }
 
 #pragma unroll
-  for (int j = 0; j < 2; ++j)
-    *reinterpret_cast<f32x4*>(p.state_out + srow * DK + 32 * wave + 16 * j + 4 * lq) = sacc[j];
+  for (int t = 0; t < TPW; ++t)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      *reinterpret_cast<f32x4*>(p.state_out + (srow + 16 * t) * DK + 32 * wave + 16 * j + 4 * lq) = sacc[t][j];
 }
 
 // Bytes of the records (every chunk slot of a packed call, which bounds the
@@ -1077,11 +1115,18 @@ int chunk_fwd(const void* q, const void* k, const void* v, int qkv_dtype, int ga
   }
   // whole GQA units per XCD (a unit never spans two sequences: Hv % group == 0)
   const int64_t heads = n_seqs * Hv, unit = Hv / Hk;
-  const int64_t scan_blocks = kTiles * kXcds * unit * ((heads + kXcds * unit - 1) / (kXcds * unit));
+  // Two tiles per workgroup when the tiles outnumber the CUs and every
+  // sequence has the same length.  Packed sequences keep one: their longest
+  // chain bounds the scan, and a two-tile workgroup's chunk takes about 1.8x
+  // as long (measured at T=4096: B=2 153 against 167 us, B=4 260 against
+  // 333 us, but the 1024/2560/7168 packed step 361 against 356 us).
+  const int tpw = kt_lds && !packed ? 2 : 1;
+  const int64_t scan_blocks = (kTiles / tpw) * kXcds * unit * ((heads + kXcds * unit - 1) / (kXcds * unit));
   if (!(phases & kPhaseScan)) return GDN_OK;
   const dim3 sgrid(static_cast<unsigned>(scan_blocks));
-  if (kt_lds) hipLaunchKernelGGL(chunk_scan_kernel<true>, sgrid, dim3(256), 0, st, p);
-  else hipLaunchKernelGGL(chunk_scan_kernel<false>, sgrid, dim3(256), 0, st, p);
+  if (tpw == 2) hipLaunchKernelGGL((chunk_scan_kernel<true, 2>), sgrid, dim3(256), 0, st, p);
+  else if (kt_lds) hipLaunchKernelGGL((chunk_scan_kernel<true, 1>), sgrid, dim3(256), 0, st, p);
+  else hipLaunchKernelGGL((chunk_scan_kernel<false, 1>), sgrid, dim3(256), 0, st, p);
   return gdn_host::check_launch("gdn_chunk_fwd/scan");
 }
 
