@@ -51,8 +51,9 @@ def test_short_sequences_match_oracle(T):
 def test_gqa_groups_match_oracle(B, Hk, Hv):
     """GQA groups of 1, 3 and 4 v-heads per k-head (the other tests use 2).
     The scan deals whole groups to an XCD and the prep writes a k-head's K, Q
-    and K^T records once per group; B=3 with Hv=12 is 288 scan workgroups,
-    so K^T then comes from transposed LDS reads."""
+    and K^T records once per group; B=3 with Hv=12 is 288 scan tiles, so K^T
+    then comes from transposed LDS reads and each scan workgroup holds two
+    16-row tiles."""
     d = draw(320 + 16 * B + Hk + Hv, B, 150, Hk, Hv, 128, 128)
     t, r = to_torch(d, DEV)
     y, S = chunked(t, t["state"])
@@ -175,10 +176,12 @@ def test_prepared_launch_equals_call():
 
 
 def test_kt_sources_agree_bitwise():
-    """With more scan workgroups than CUs the scan forms K^T by transposed LDS
-    reads of K; with at most one per CU it reads the record's K^T.  Two
-    Hv=32 sequences in one call (512 workgroups) against each alone (256):
-    the transposes are exact, so the results are bit-identical."""
+    """With more scan tiles than CUs the scan forms K^T by transposed LDS
+    reads of K and (for rows of one length) puts two 16-row tiles in each
+    workgroup; with at most one tile per CU it reads the record's K^T, one
+    tile per workgroup.  Two Hv=32 sequences in one call (512 tiles) against
+    each alone (256): the transposes are exact and each tile's products run
+    in the same order, so the results are bit-identical."""
     d = draw(309, 2, 200, 16, 32, 128, 128)
     t, _ = to_torch(d, DEV)
     y2, S2 = chunked(t, t["state"])
@@ -187,6 +190,19 @@ def test_kt_sources_agree_bitwise():
         y1, S1 = chunked(one, one["state"])
         assert torch.equal(y1[0], y2[b]), f"row {b}: y"
         assert torch.equal(S1[0], S2[b]), f"row {b}: state"
+
+
+def test_two_tile_workgroups_b4_match_oracle():
+    """B=4 rows of 130 tokens at Hv=32 (1024 tiles, two per workgroup, two
+    workgroups per CU), a partial last chunk and nonzero initial states:
+    6 heads against the oracle."""
+    d = draw(311, 4, 130, 16, 32, 128, 128)
+    t, r = to_torch(d, DEV)
+    y, S = chunked(t, t["state"])
+    heads = [0, 1, 13, 14, 30, 31]
+    y_ref, S_ref = oracle_heads(r, heads, 32, 16, r["state"])
+    assert row_errs_y(y[:, :, heads].float().cpu().numpy(), y_ref).max() <= Y_TOL
+    assert head_errs_state(S[:, heads].cpu().numpy(), S_ref).max() <= STATE_TOL
 
 
 @pytest.mark.parametrize("gate_dtype,param_dtype", [("f32", "f32"), ("f16", "bf16"), ("bf16", "f16")])
