@@ -203,3 +203,45 @@ def test_noalloc_chunk_rejects_calls_beyond_its_scratch(lib):
     assert "static scratch" in msg and "67108864" in msg
     assert lib.gdn_chunk_workspace_bytes(1, 2048, 32, 128, 128, 64) > 64 << 20
     assert lib.gdn_chunk_workspace_bytes(1, 1536, 32, 128, 128, 64) <= 64 << 20
+
+
+def test_attention_entry_points_reject_bad_arguments(lib):
+    """gdn_attn_qk / gdn_attn_fwd / gdn_rms_norm / gdn_silu_mul validate
+    before any HIP call."""
+    def qk(**kw):
+        a = dict(qg=FAKE, qg_ld=0, k=FAKE, v=FAKE, kv_ld=0, qw=FAKE, kw=FAKE, wdt=_lib.DTYPE_F32, eps=1e-6,
+                 pos=FAKE, q=FAKE, kc=FAKE, vc=FAKE, B=2, T=3, Hq=16, Hkv=4, D=256, cap=64, rot=64, base=1e7)
+        a.update(kw)
+        return lib.gdn_attn_qk(*a.values(), None)
+
+    assert qk(D=96) == _lib.ERR_UNSUPPORTED
+    assert qk(rot=6) == _lib.ERR_UNSUPPORTED          # not whole lane groups
+    assert qk(Hkv=3) == _lib.ERR_INVALID              # Hq not a multiple of Hkv
+    assert qk(cap=2) == _lib.ERR_INVALID              # T new tokens cannot fit
+    assert qk(qg_ld=100) == _lib.ERR_INVALID          # token stride below the row
+    assert qk(pos=None) == _lib.ERR_INVALID
+    assert qk(base=0.0) == _lib.ERR_INVALID
+    assert qk(B=0) == _lib.OK                         # nothing to do
+
+    def fwd(**kw):
+        a = dict(q=FAKE, qg=FAKE, qg_ld=0, kc=FAKE, vc=FAKE, pos=FAKE, out=FAKE, scale=0.0625, B=2, T=1, Hq=16,
+                 Hkv=4, D=256, cap=64, kvmax=64, n_split=1, ws=None, ws_bytes=0)
+        a.update(kw)
+        return lib.gdn_attn_fwd(*a.values(), None)
+
+    assert fwd(D=64) == _lib.ERR_UNSUPPORTED
+    assert fwd(kvmax=0) == _lib.ERR_INVALID           # below T
+    assert fwd(kvmax=65) == _lib.ERR_INVALID          # beyond the cache
+    assert fwd(scale=0.0) == _lib.ERR_INVALID
+    assert fwd(n_split=4) == _lib.ERR_INVALID         # split partials need a workspace
+    assert fwd(q=FAKE + 2) == _lib.ERR_INVALID        # misaligned
+    assert fwd(qg_ld=6) == _lib.ERR_INVALID
+    need = lib.gdn_attn_workspace_bytes(2, 1, 16, 4, 256, 4)
+    assert need == 2 * 4 * 16 * 4 * (256 + 2) * 4     # rows padded to one 16-row tile
+    assert lib.gdn_attn_workspace_bytes(2, 1, 16, 4, 256, 1) == 0
+
+    assert lib.gdn_rms_norm(FAKE, None, None, FAKE, _lib.DTYPE_F32, FAKE, 0, 4, 100, 1e-6, None) == _lib.ERR_INVALID
+    assert lib.gdn_rms_norm(FAKE, None, None, FAKE, _lib.DTYPE_F32, FAKE, 8, 4, 16, 1e-6, None) == _lib.ERR_INVALID
+    assert lib.gdn_rms_norm(FAKE, None, None, None, _lib.DTYPE_F32, FAKE, 0, 4, 16, 1e-6, None) == _lib.ERR_INVALID
+    assert lib.gdn_silu_mul(FAKE, FAKE, 4, 12, None) == _lib.ERR_INVALID
+    assert lib.gdn_silu_mul(FAKE, FAKE, 0, 16, None) == _lib.OK
