@@ -19,8 +19,13 @@
 //                        partial softmax states merge in LDS at the end.
 //                        Keys may also be split over workgroups; the partial
 //                        states then go to a workspace and
-//   attn_combine_kernel  merges them.  The output is multiplied by
-//                        sigmoid(gate) on the way out when a gate is given.
+//   attn_combine_kernel  merges them.
+//   attn_prefill_kernel  long prefills (one key range, >= 512 rows per kv-head):
+//                        128-row workgroups, 32 rows per wave, 64-key K / V
+//                        blocks double-buffered in LDS (K by direct loads, V
+//                        transposed on its way in), one barrier per block.
+//                        The output is multiplied by sigmoid(gate) on the way
+//                        out when a gate is given.
 //   rms_norm_kernel      the layers' RMSNorm over the hidden size, optionally of
 //                        a residual sum it also writes out.
 //   silu_mul_kernel      the MLP's silu(gate) * up.
@@ -408,6 +413,307 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(const AttnParams p) {
   }
 }
 
+// Long causal prefills (one key range, at least kPrefillRows rows per kv-head):
+// a workgroup owns 128 rows, four waves of 32, so every K or V fragment a
+// wave reads from LDS feeds two 16-row MFMA tiles.  64-key blocks are double-
+// buffered in LDS and a block costs one barrier:
+//   K  goes in by direct global -> LDS loads (each lane's 16 bytes land at
+//      16 * lane past the wave's base), rows of D bf16 whose 16-byte granules
+//      are XOR-swizzled by (key & 7), so the fragment reads of 8 consecutive
+//      keys hit distinct banks;
+//   V  is transposed in registers on its way in: Vt[d][position], with the
+//      keys of each 32-key group in the k-slot order of the P^T operand
+//      (position 8q + 4h + i holds key 16h + 4q + i), so that a V^T fragment
+//      is one 16-byte read, like K's.  (Transposed LDS reads of a [key][d]
+//      block deliver about 45 bytes per clock per CU, against 128 for 16-byte
+//      reads.)
+// The softmax max is raised only when a row's block max exceeds it by more
+// than 8 (log2 units; P stays below 2^8), which skips the rescale of the
+// output on most blocks, and only blocks that cross the diagonal or the end
+// of the keys are masked.  Workgroups with the longest key ranges go first.
+// 16 bytes per lane from global memory straight into LDS at lds_base + 16 * lane (lds_base wave-
+// uniform).  Issued from inline assembly: the compiler's wait insertion, seeing an LDS DMA in a
+// loop, would otherwise drain every LDS read with lgkmcnt(0).  It increments vmcnt like any load;
+// the caller waits for it (vmcnt(0)) before the barrier that publishes the block.
+__device__ __forceinline__ void lds_dma16(const void* gptr, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+               :
+               : "v"(gptr), "s"(lds_base)
+               : "memory", "m0");
+}
+
+constexpr int kPrefillRows = 512;  // rows (tokens x heads of a group) per kv-head from which it is used
+constexpr int PR = 128;            // rows per workgroup
+constexpr int VTP = KB + 8;        // Vt row stride (bf16): 16-byte reads of 8 consecutive d rows hit distinct banks
+
+template <int D>
+__global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnParams p) {
+  constexpr int NS = D / 32;                  // k-steps of q . k
+  constexpr int NJ = D / 16;                  // 16-wide d tiles of the output
+  constexpr int KG = D / 8;                   // 16-byte granules per K row
+  constexpr int KDMA = KB * KG / 256;         // direct loads per thread and K block
+  constexpr int VPAIRS = (KB / 4) * KG / 256;  // (key quad, d octet) pairs per thread and V block
+  constexpr int KSTAGE = KB * D * 2;          // bytes
+  constexpr int VSTAGE = D * VTP * 2;
+  static_assert(KDMA * 256 == KB * KG && VPAIRS * 256 == (KB / 4) * KG, "block must split evenly over 256 threads");
+
+  __shared__ __align__(16) unsigned char smem[2 * (KSTAGE + VSTAGE)];
+
+  const int b = blockIdx.z;
+  const int n_rb = gridDim.x / p.Hkv;
+  const int hkv = blockIdx.x % p.Hkv;
+  const int rb = n_rb - 1 - static_cast<int>(blockIdx.x) / p.Hkv;  // longest key ranges first
+  const int g = p.Hq / p.Hkv;
+  const int n_rows = p.T * g;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lr = lane & 15, lq = lane >> 4;
+  const int p0 = first_pos(p.pos0, b, p.T, p.cap);
+
+  const int row0 = rb * PR;
+  const int t_last = min((row0 + PR - 1) / g, p.T - 1);
+  const int k_hi = min(p0 + t_last + 1, p.split_len);  // keys of this workgroup: [0, k_hi)
+  const int k_free = min(p0 + row0 / g + 1, k_hi);      // keys below this are visible to every row
+
+  // the wave's two 16-row tiles; rows past the end compute on q = 0 and are not stored
+  int t[2], hq[2], kmax[2];
+  bool row_ok[2];
+  bf16x8 qf[2][NS];
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt) {
+    const int r = row0 + 32 * wave + 16 * rt + lr;
+    row_ok[rt] = r < n_rows;
+    t[rt] = row_ok[rt] ? r / g : p.T - 1;
+    hq[rt] = hkv * g + (row_ok[rt] ? r % g : 0);
+    kmax[rt] = p0 + t[rt];
+    const uint16_t* qrow = p.q + ((static_cast<int64_t>(b) * p.T + t[rt]) * p.Hq + hq[rt]) * D;
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      const u32x4 v = *reinterpret_cast<const u32x4*>(qrow + 32 * s + 8 * lq);
+      qf[rt][s] = __builtin_bit_cast(bf16x8, row_ok[rt] ? v : u32x4{0u, 0u, 0u, 0u});
+    }
+  }
+
+  const uint16_t* kc_head = p.kc + (static_cast<int64_t>(b) * p.Hkv + hkv) * p.cap * D;
+  const uint16_t* vc_head = p.vc + (static_cast<int64_t>(b) * p.Hkv + hkv) * p.cap * D;
+  // K block kb -> stage st: thread tid's load i fills physical granule i * 256 + tid, which is row
+  // i * KR + tid / KG, granule (tid % KG) ^ (row & 7) of the block (the swizzle does not depend on i)
+  constexpr int KR = 256 / KG;
+  const int k_row0 = tid / KG;
+  const int k_off = k_row0 * D + (((tid % KG) ^ (k_row0 & 7)) * 8);
+  // LDS address of the wave's 1 KB slice of load 0 in stage 0
+  const uint32_t k_lds = __builtin_amdgcn_readfirstlane(
+      static_cast<uint32_t>(reinterpret_cast<uintptr_t>(smem)) + wave * 1024);
+  auto k_dma = [&](int kb, int st, bool clamp) {
+    if (clamp) {  // keys past the range re-read the last one (in bounds; they are masked)
+#pragma unroll
+      for (int i = 0; i < KDMA; ++i) {
+        const int off = min(kb + i * KR + k_row0, k_hi - 1) * D + (k_off - k_row0 * D);
+        lds_dma16(kc_head + off, k_lds + st * KSTAGE + i * 4096);
+      }
+    } else {
+      const uint16_t* src = kc_head + kb * D + k_off;
+#pragma unroll
+      for (int i = 0; i < KDMA; ++i) {
+        lds_dma16(src + i * KR * D, k_lds + st * KSTAGE + i * 4096);
+      }
+    }
+  };
+  // V block kb -> registers: pair i is key quad tid % 16 (4 rows) x d octet i * 16 + tid / 16
+  const int v_kq = tid % (KB / 4), v_dq = tid / (KB / 4);
+  const int v_off = 4 * v_kq * D + v_dq * 8;
+  u32x4 vr[4];
+  auto v_load = [&](int kb, int i, bool clamp) {
+    if (clamp) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        vr[e] = *reinterpret_cast<const u32x4*>(vc_head + min(kb + 4 * v_kq + e, k_hi - 1) * D + (v_dq + i * 16) * 8);
+    } else {
+      const uint16_t* src = vc_head + kb * D + v_off + i * 128;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) vr[e] = *reinterpret_cast<const u32x4*>(src + e * D);
+    }
+  };
+  // registers -> Vt stage st: for each of the octet's 8 d, the quad's 4 keys as one 8-byte write
+  const int v_pos = 32 * (v_kq >> 3) + 8 * (v_kq & 3) + 4 * ((v_kq >> 2) & 1);
+  auto v_store = [&](int st, int i) {
+    uint16_t* Vt = reinterpret_cast<uint16_t*>(smem + 2 * KSTAGE + st * VSTAGE) + (8 * (v_dq + i * 16)) * VTP + v_pos;
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      const uint32_t k0 = vr[0][m], k1 = vr[1][m], k2 = vr[2][m], k3 = vr[3][m];
+      const u32x2 even = {(k0 & 0xffffu) | (k1 << 16), (k2 & 0xffffu) | (k3 << 16)};
+      const u32x2 odd = {(k0 >> 16) | (k1 & 0xffff0000u), (k2 >> 16) | (k3 & 0xffff0000u)};
+      *reinterpret_cast<u32x2*>(Vt + (2 * m) * VTP) = even;
+      *reinterpret_cast<u32x2*>(Vt + (2 * m + 1) * VTP) = odd;
+    }
+  };
+
+  float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.0f, 0.0f};
+  f32x4 o[2][NJ];
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) o[rt][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  // K fragment (tile kt, k-step s) of lane (r, q): row 16 kt + r, granule (4s + q) ^ (r & 7)
+  // = 8 (s >> 1) + 4 ((s & 1) ^ x2) + (q ^ x01) with x = r & 7: one base for even s, one for odd,
+  // each plus 64 (s & ~1) bytes
+  const int x2 = (lr >> 2) & 1, y01 = lq ^ (lr & 3);
+  const int kfe = lr * (D * 2) + (4 * x2 + y01) * 16, kfo = lr * (D * 2) + (4 * (x2 ^ 1) + y01) * 16;
+  const int vfo = lr * (VTP * 2) + 16 * lq;  // V^T fragment of lane (r, q): d row 16 j + r, positions 32 ks + 8q ..
+
+  const int nblk = (k_hi + KB - 1) / KB;  // >= 1: k_hi > p0 + row0 / g >= 0
+  k_dma(0, 0, KB > k_hi);
+#pragma unroll
+  for (int i = 0; i < VPAIRS; ++i) {
+    v_load(0, i, KB > k_hi);
+    v_store(0, i);
+  }
+  for (int blk = 0; blk < nblk; ++blk) {
+    const int kb = KB * blk, st = blk & 1;
+    __builtin_amdgcn_s_waitcnt(0);  // this thread's direct loads of block blk have landed
+    __syncthreads();                // everyone's have, Vt[st] is written, stage st ^ 1 is free
+    const bool more = blk + 1 < nblk;
+    const bool clamp = kb + 2 * KB > k_hi;  // the next block runs past the keys
+    if (more) {
+      k_dma(kb + KB, st ^ 1, clamp);
+      v_load(kb + KB, 0, clamp);
+    }
+
+    // S^T = K Q^T: lane (r, q) holds keys 16 kt + 4q + i of row r, for both row tiles
+    const unsigned char* Ks = smem + st * KSTAGE;
+    auto k_frag = [&](int s, int kt) {
+      return *reinterpret_cast<const bf16x8*>(Ks + ((s & 1) ? kfo : kfe) + kt * 16 * (D * 2) + (s & ~1) * 64);
+    };
+    f32x4 sc[2][4];
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt) sc[0][kt] = sc[1][kt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    bf16x8 kf[2][4];  // the fragments of k-step s, and those of s + 1 in flight
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt) kf[0][kt] = k_frag(0, kt);
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      if (s + 1 < NS) {
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt) kf[(s + 1) & 1][kt] = k_frag(s + 1, kt);
+      }
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt) {
+        sc[0][kt] = mfma16(kf[s & 1][kt], qf[0][s], sc[0][kt]);
+        sc[1][kt] = mfma16(kf[s & 1][kt], qf[1][s], sc[1][kt]);
+      }
+    }
+    // issue order: k-step s + 1's four fragment reads ahead of k-step s's eight products
+    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      if (s + 1 < NS) __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+    }
+    if (VPAIRS > 1 && more) {
+      v_store(st ^ 1, 0);
+      v_load(kb + KB, 1, clamp);
+    }
+
+    if (kb + KB > k_free) {
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int key = kb + 16 * kt + 4 * lq + i;
+            if (!(key <= kmax[rt] && key < k_hi)) sc[rt][kt][i] = -INFINITY;
+          }
+    }
+    float mb[2];
+    bool grow = false;
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+      float x = -INFINITY;
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) x = fmaxf(x, sc[rt][kt][i]);
+      x = fmaxf(x, __shfl_xor(x, 16, 64));
+      x = fmaxf(x, __shfl_xor(x, 32, 64));
+      mb[rt] = x * p.scale_log2;
+      grow |= mb[rt] > m[rt] + 8.0f;
+    }
+    if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt) {
+        const float m_new = fmaxf(m[rt], mb[rt]);
+        const float alpha = __builtin_amdgcn_exp2f(m[rt] - m_new);
+        m[rt] = m_new;
+        l[rt] *= alpha;
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) o[rt][j] *= alpha;
+      }
+    }
+    // P = exp2(s * scale - m) as the B operand of O^T += V^T P^T: k-slots 8q .. 8q+3 are keys
+    // 32 ks + 4q + (0..3) (accumulator tile 2 ks), 8q+4 .. 8q+7 are keys 32 ks + 16 + 4q + (0..3)
+    bf16x8 pb[2][2];
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+      float ps = 0.0f;
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          sc[rt][kt][i] = __builtin_amdgcn_exp2f(fmaf(sc[rt][kt][i], p.scale_log2, -m[rt]));
+          ps += sc[rt][kt][i];
+        }
+      l[rt] += ps;
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+        pb[rt][ks] = __builtin_bit_cast(
+            bf16x8, u32x4{pk_bf16(sc[rt][2 * ks][0], sc[rt][2 * ks][1]), pk_bf16(sc[rt][2 * ks][2], sc[rt][2 * ks][3]),
+                          pk_bf16(sc[rt][2 * ks + 1][0], sc[rt][2 * ks + 1][1]),
+                          pk_bf16(sc[rt][2 * ks + 1][2], sc[rt][2 * ks + 1][3])});
+    }
+
+    // O^T += V^T P^T
+    const unsigned char* Vt = smem + 2 * KSTAGE + st * VSTAGE + vfo;
+    constexpr int NF = 2 * NJ;  // V^T fragments per block: (ks, j) = (f / NJ, f % NJ)
+    constexpr int VPF = 4;      // fragments in flight
+    auto v_frag = [&](int f) {
+      return *reinterpret_cast<const bf16x8*>(Vt + (f % NJ) * 16 * (VTP * 2) + (f / NJ) * 64);
+    };
+    bf16x8 vf[VPF];
+#pragma unroll
+    for (int f = 0; f < VPF; ++f) vf[f] = v_frag(f);
+#pragma unroll
+    for (int f = 0; f < NF; ++f) {
+      const bf16x8 a = vf[f % VPF];
+      if (f + VPF < NF) vf[f % VPF] = v_frag(f + VPF);
+      const int j = f % NJ, ks = f / NJ;
+      o[0][j] = mfma16(a, pb[0][ks], o[0][j]);
+      o[1][j] = mfma16(a, pb[1][ks], o[1][j]);
+    }
+    // issue order: fragment f + VPF read ahead of fragment f's two products
+    __builtin_amdgcn_sched_group_barrier(0x100, VPF, 1);
+#pragma unroll
+    for (int f = 0; f < NF; ++f) {
+      if (f + VPF < NF) __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 1);
+    }
+
+    if (more) v_store(st ^ 1, VPAIRS - 1);
+  }
+
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt) {
+    float lt = l[rt];
+    lt += __shfl_xor(lt, 16, 64);
+    lt += __shfl_xor(lt, 32, 64);
+    if (!row_ok[rt]) continue;
+    const float inv_l = lt > 0.0f ? 1.0f / lt : 0.0f;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) store_out4<D>(p, b, t[rt], hq[rt], 16 * j + 4 * lq, o[rt][j], inv_l);
+  }
+}
+
 // One wave per (row, kv-head, batch row): the split partials of a row merged.
 template <int D>
 __global__ __launch_bounds__(256) void attn_combine_kernel(const AttnParams p) {
@@ -640,6 +946,14 @@ extern "C" int gdn_attn_fwd(const void* q, const void* qg, int64_t qg_ld, const 
   p.rows_pad = static_cast<int>(rows_pad);
   p.scale_log2 = scale * kLog2e;
   hipStream_t st = static_cast<hipStream_t>(stream);
+  if (n_split == 1 && T * (Hq / Hkv) >= kPrefillRows) {
+    const int64_t n_prb = (T * (Hq / Hkv) + PR - 1) / PR;
+    if (Hkv * n_prb > INT32_MAX) return fail(GDN_ERR_UNSUPPORTED, "gdn_attn_fwd: problem too large");
+    const dim3 pgrid(static_cast<unsigned>(Hkv * n_prb), 1, static_cast<unsigned>(B));
+    if (D == 256) hipLaunchKernelGGL(attn_prefill_kernel<256>, pgrid, dim3(256), 0, st, p);
+    else hipLaunchKernelGGL(attn_prefill_kernel<128>, pgrid, dim3(256), 0, st, p);
+    return gdn_host::check_launch("gdn_attn_fwd/prefill");
+  }
   const dim3 grid(static_cast<unsigned>(n_split), static_cast<unsigned>(Hkv * n_rb), static_cast<unsigned>(B));
   if (D == 256) {
     if (rt == 4) hipLaunchKernelGGL((attn_fwd_kernel<256, 4>), grid, dim3(256), 0, st, p);

@@ -89,24 +89,29 @@ def test_rms_norm_residual_and_strided_output():
 
 
 CASES = {
-    # name: (B, T, pos0, n_split, gate)
+    # name: (B, T, pos0, n_split, gate[, (Hq, Hkv, D)]); heads default to 16, 4, 256
     "decode": (8, 1, [0, 1, 63, 64, 65, 300, 511, 700], 1, True),
     "decode_split": (8, 1, [0, 1, 63, 64, 65, 300, 511, 700], 4, True),
     "verify_t4": (4, 4, [3, 100, 257, 0], 1, True),
     "verify_t4_split": (4, 4, [3, 100, 257, 0], 3, False),
     "prefill": (2, 150, [0, 33], 1, True),
     "prefill_nogate": (1, 70, [5], 1, False),
+    "prefill_long": (2, 611, [0, 77], 1, True),
+    "prefill_d128": (2, 300, [20, 0], 1, True, (16, 4, 128)),
+    "prefill_g8": (1, 97, [130], 1, False, (16, 2, 256)),
 }
 
 
 @pytest.mark.parametrize("name", list(CASES))
 def test_attention_matches_oracle(name):
-    """Causal GQA attention over per-row cache lengths (Hq=16, Hkv=4, D=256):
-    decode and 4-token verify (one 16-row tile, keys split over the waves
-    and optionally over workgroups), and prefill (64-row tiles).  Cache
-    positions past each row's keys hold NaN, which must not leak."""
-    B, T, pos0, n_split, use_gate = CASES[name]
-    Hq, Hkv, D = 16, 4, 256
+    """Causal GQA attention over per-row cache lengths: decode and 4-token
+    verify (one 16-row tile, keys split over the waves and optionally over
+    workgroups), short prefills (64-row tiles, below 512 rows per kv-head)
+    and long ones (128-row workgroups with double-buffered K/V blocks, from
+    512 rows: T=150 and up at 4 heads per group), at head dims 256 and 128.
+    Cache positions past each row's keys hold NaN, which must not leak."""
+    B, T, pos0, n_split, use_gate = CASES[name][:5]
+    Hq, Hkv, D = CASES[name][5] if len(CASES[name]) > 5 else (16, 4, 256)
     gen = torch.Generator().manual_seed(72)
     L = max(pos0) + T
     cap = L + 40
