@@ -504,48 +504,27 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnParams p) {
   // LDS address of the wave's 1 KB slice of load 0 in stage 0
   const uint32_t k_lds = __builtin_amdgcn_readfirstlane(
       static_cast<uint32_t>(reinterpret_cast<uintptr_t>(smem)) + wave * 1024);
-  auto k_dma = [&](int kb, int st, bool clamp) {
-    if (clamp) {  // keys past the range re-read the last one (in bounds; they are masked)
-#pragma unroll
-      for (int i = 0; i < KDMA; ++i) {
-        const int off = min(kb + i * KR + k_row0, k_hi - 1) * D + (k_off - k_row0 * D);
-        lds_dma16(kc_head + off, k_lds + st * KSTAGE + i * 4096);
-      }
-    } else {
-      const uint16_t* src = kc_head + kb * D + k_off;
-#pragma unroll
-      for (int i = 0; i < KDMA; ++i) {
-        lds_dma16(src + i * KR * D, k_lds + st * KSTAGE + i * 4096);
-      }
-    }
+  // keys past the range re-read the last one (in bounds; they are masked)
+  auto k_dma = [&](int kb, int st, int i) {
+    const int key = min(kb + i * KR + k_row0, k_hi - 1);
+    lds_dma16(kc_head + key * D + (k_off - k_row0 * D), k_lds + st * KSTAGE + i * 4096);
   };
   // V block kb -> registers: pair i is key quad tid % 16 (4 rows) x d octet i * 16 + tid / 16
   const int v_kq = tid % (KB / 4), v_dq = tid / (KB / 4);
-  const int v_off = 4 * v_kq * D + v_dq * 8;
-  u32x4 vr[4];
-  auto v_load = [&](int kb, int i, bool clamp) {
-    if (clamp) {
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        vr[e] = *reinterpret_cast<const u32x4*>(vc_head + min(kb + 4 * v_kq + e, k_hi - 1) * D + (v_dq + i * 16) * 8);
-    } else {
-      const uint16_t* src = vc_head + kb * D + v_off + i * 128;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) vr[e] = *reinterpret_cast<const u32x4*>(src + e * D);
-    }
+  u32x4 vr[VPAIRS][4];
+  auto v_load = [&](int kb, int i, int e) {
+    const int key = min(kb + 4 * v_kq + e, k_hi - 1);
+    vr[i][e] = *reinterpret_cast<const u32x4*>(vc_head + key * D + (v_dq + i * 16) * 8);
   };
   // registers -> Vt stage st: for each of the octet's 8 d, the quad's 4 keys as one 8-byte write
   const int v_pos = 32 * (v_kq >> 3) + 8 * (v_kq & 3) + 4 * ((v_kq >> 2) & 1);
-  auto v_store = [&](int st, int i) {
+  auto v_store = [&](int st, int i, int m) {  // d rows 8 (v_dq + 16 i) + 2m, + 2m + 1
     uint16_t* Vt = reinterpret_cast<uint16_t*>(smem + 2 * KSTAGE + st * VSTAGE) + (8 * (v_dq + i * 16)) * VTP + v_pos;
-#pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      const uint32_t k0 = vr[0][m], k1 = vr[1][m], k2 = vr[2][m], k3 = vr[3][m];
-      const u32x2 even = {(k0 & 0xffffu) | (k1 << 16), (k2 & 0xffffu) | (k3 << 16)};
-      const u32x2 odd = {(k0 >> 16) | (k1 & 0xffff0000u), (k2 >> 16) | (k3 & 0xffff0000u)};
-      *reinterpret_cast<u32x2*>(Vt + (2 * m) * VTP) = even;
-      *reinterpret_cast<u32x2*>(Vt + (2 * m + 1) * VTP) = odd;
-    }
+    const uint32_t k0 = vr[i][0][m], k1 = vr[i][1][m], k2 = vr[i][2][m], k3 = vr[i][3][m];
+    const u32x2 even = {(k0 & 0xffffu) | (k1 << 16), (k2 & 0xffffu) | (k3 << 16)};
+    const u32x2 odd = {(k0 >> 16) | (k1 & 0xffff0000u), (k2 >> 16) | (k3 & 0xffff0000u)};
+    *reinterpret_cast<u32x2*>(Vt + (2 * m) * VTP) = even;
+    *reinterpret_cast<u32x2*>(Vt + (2 * m + 1) * VTP) = odd;
   };
 
   float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.0f, 0.0f};
@@ -563,22 +542,23 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnParams p) {
   const int vfo = lr * (VTP * 2) + 16 * lq;  // V^T fragment of lane (r, q): d row 16 j + r, positions 32 ks + 8q ..
 
   const int nblk = (k_hi + KB - 1) / KB;  // >= 1: k_hi > p0 + row0 / g >= 0
-  k_dma(0, 0, KB > k_hi);
+#pragma unroll
+  for (int i = 0; i < KDMA; ++i) k_dma(0, 0, i);
 #pragma unroll
   for (int i = 0; i < VPAIRS; ++i) {
-    v_load(0, i, KB > k_hi);
-    v_store(0, i);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v_load(0, i, e);
+#pragma unroll
+    for (int m = 0; m < 4; ++m) v_store(0, i, m);
   }
   for (int blk = 0; blk < nblk; ++blk) {
     const int kb = KB * blk, st = blk & 1;
     __builtin_amdgcn_s_waitcnt(0);  // this thread's direct loads of block blk have landed
     __syncthreads();                // everyone's have, Vt[st] is written, stage st ^ 1 is free
-    const bool more = blk + 1 < nblk;
-    const bool clamp = kb + 2 * KB > k_hi;  // the next block runs past the keys
-    if (more) {
-      k_dma(kb + KB, st ^ 1, clamp);
-      v_load(kb + KB, 0, clamp);
-    }
+    // the next block's K and V go in while this one computes: one K load and one V load per k-step of
+    // S^T, V stored (transposed) during O^T; the last block re-reads itself into the free stage (never
+    // read) so that no load sits behind a branch
+    const int kb_next = blk + 1 < nblk ? kb + KB : kb;
 
     // S^T = K Q^T: lane (r, q) holds keys 16 kt + 4q + i of row r, for both row tiles
     const unsigned char* Ks = smem + st * KSTAGE;
@@ -597,6 +577,9 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnParams p) {
 #pragma unroll
         for (int kt = 0; kt < 4; ++kt) kf[(s + 1) & 1][kt] = k_frag(s + 1, kt);
       }
+      static_assert(KDMA == NS, "one K load per k-step");
+      k_dma(kb_next, st ^ 1, s);
+      if (s < 4 * VPAIRS) v_load(kb_next, s / 4, s % 4);
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt) {
         sc[0][kt] = mfma16(kf[s & 1][kt], qf[0][s], sc[0][kt]);
@@ -608,11 +591,8 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnParams p) {
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
       if (s + 1 < NS) __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+      if (s < 4 * VPAIRS) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
       __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
-    }
-    if (VPAIRS > 1 && more) {
-      v_store(st ^ 1, 0);
-      v_load(kb + KB, 1, clamp);
     }
 
     if (kb + KB > k_free) {
@@ -690,6 +670,8 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnParams p) {
       const int j = f % NJ, ks = f / NJ;
       o[0][j] = mfma16(a, pb[0][ks], o[0][j]);
       o[1][j] = mfma16(a, pb[1][ks], o[1][j]);
+      // the next block's V into the free stage
+      if (f % 2 == 1 && f / 2 < 4 * VPAIRS) v_store(st ^ 1, f / 8, (f / 2) % 4);
     }
     // issue order: fragment f + VPF read ahead of fragment f's two products
     __builtin_amdgcn_sched_group_barrier(0x100, VPF, 1);
@@ -699,7 +681,6 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnParams p) {
       __builtin_amdgcn_sched_group_barrier(0x008, 2, 1);
     }
 
-    if (more) v_store(st ^ 1, VPAIRS - 1);
   }
 
 #pragma unroll
