@@ -442,6 +442,22 @@ __device__ __forceinline__ void lds_dma16(const void* gptr, uint32_t lds_base) {
                : "memory", "m0");
 }
 
+// Max / sum over the four 16-lane rows of a wave (lanes r, r + 16, r + 32, r + 48), by the
+// gfx950 row-swap moves (VALU, no LDS round trip): permlane16_swap(x, x) yields the even and the
+// odd rows, permlane32_swap(x, x) the low and the high halves, each in both places.
+__device__ __forceinline__ float rows_max(float x) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float rows_sum(float x) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
 constexpr int kPrefillRows = 512;  // rows (tokens x heads of a group) per kv-head from which it is used
 constexpr int PR = 128;            // rows per workgroup
 constexpr int VTP = KB + 8;        // Vt row stride (bf16): 16-byte reads of 8 consecutive d rows hit distinct banks
@@ -615,9 +631,7 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnParams p) {
       for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
         for (int i = 0; i < 4; ++i) x = fmaxf(x, sc[rt][kt][i]);
-      x = fmaxf(x, __shfl_xor(x, 16, 64));
-      x = fmaxf(x, __shfl_xor(x, 32, 64));
-      mb[rt] = x * p.scale_log2;
+      mb[rt] = rows_max(x) * p.scale_log2;
       grow |= mb[rt] > m[rt] + 8.0f;
     }
     if (__builtin_amdgcn_ballot_w64(grow) != 0) {
@@ -685,9 +699,7 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnParams p) {
 
 #pragma unroll
   for (int rt = 0; rt < 2; ++rt) {
-    float lt = l[rt];
-    lt += __shfl_xor(lt, 16, 64);
-    lt += __shfl_xor(lt, 32, 64);
+    const float lt = rows_sum(l[rt]);
     if (!row_ok[rt]) continue;
     const float inv_l = lt > 0.0f ? 1.0f / lt : 0.0f;
 #pragma unroll
