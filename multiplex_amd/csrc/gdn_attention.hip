@@ -424,7 +424,9 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(const AttnParams p) {
 //   V  is transposed in registers on its way in: Vt[d][position], with the
 //      keys of each 32-key group in the k-slot order of the P^T operand
 //      (position 8q + 4h + i holds key 16h + 4q + i), so that a V^T fragment
-//      is one 16-byte read, like K's.  (Transposed LDS reads of a [key][d]
+//      is one 16-byte read, like K's; rows of 64 positions whose 16-byte
+//      granules are XOR-swizzled by (d & 7), which keeps both the fragment
+//      reads and the 8-byte transposed writes free of bank conflicts.  (Transposed LDS reads of a [key][d]
 //      block deliver about 45 bytes per clock per CU, against 128 for 16-byte
 //      reads.)
 // The softmax max is raised only when a row's block max exceeds it by more
@@ -460,7 +462,7 @@ __device__ __forceinline__ float rows_sum(float x) {
 
 constexpr int kPrefillRows = 512;  // rows (tokens x heads of a group) per kv-head from which it is used
 constexpr int PR = 128;            // rows per workgroup
-constexpr int VTP = KB + 8;        // Vt row stride (bf16): 16-byte reads of 8 consecutive d rows hit distinct banks
+constexpr int VTP = KB;            // Vt row stride (bf16); 16-byte granules XOR-swizzled by (d & 7)
 
 template <int D>
 __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnParams p) {
@@ -534,13 +536,14 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnParams p) {
   };
   // registers -> Vt stage st: for each of the octet's 8 d, the quad's 4 keys as one 8-byte write
   const int v_pos = 32 * (v_kq >> 3) + 8 * (v_kq & 3) + 4 * ((v_kq >> 2) & 1);
-  auto v_store = [&](int st, int i, int m) {  // d rows 8 (v_dq + 16 i) + 2m, + 2m + 1
-    uint16_t* Vt = reinterpret_cast<uint16_t*>(smem + 2 * KSTAGE + st * VSTAGE) + (8 * (v_dq + i * 16)) * VTP + v_pos;
+  const int v_gran = v_pos >> 3, v_half = v_pos & 7;  // the position's granule and offset in it
+  auto v_store = [&](int st, int i, int m) {  // d rows 8 (v_dq + 16 i) + 2m, + 2m + 1 (d & 7 = 2m, 2m + 1)
+    uint16_t* Vt = reinterpret_cast<uint16_t*>(smem + 2 * KSTAGE + st * VSTAGE) + (8 * (v_dq + i * 16)) * VTP + v_half;
     const uint32_t k0 = vr[i][0][m], k1 = vr[i][1][m], k2 = vr[i][2][m], k3 = vr[i][3][m];
     const u32x2 even = {(k0 & 0xffffu) | (k1 << 16), (k2 & 0xffffu) | (k3 << 16)};
     const u32x2 odd = {(k0 >> 16) | (k1 & 0xffff0000u), (k2 >> 16) | (k3 & 0xffff0000u)};
-    *reinterpret_cast<u32x2*>(Vt + (2 * m) * VTP) = even;
-    *reinterpret_cast<u32x2*>(Vt + (2 * m + 1) * VTP) = odd;
+    *reinterpret_cast<u32x2*>(Vt + (2 * m) * VTP + ((v_gran ^ (2 * m)) << 3)) = even;
+    *reinterpret_cast<u32x2*>(Vt + (2 * m + 1) * VTP + ((v_gran ^ (2 * m + 1)) << 3)) = odd;
   };
 
   float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.0f, 0.0f};
@@ -555,7 +558,8 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnParams p) {
   // each plus 64 (s & ~1) bytes
   const int x2 = (lr >> 2) & 1, y01 = lq ^ (lr & 3);
   const int kfe = lr * (D * 2) + (4 * x2 + y01) * 16, kfo = lr * (D * 2) + (4 * (x2 ^ 1) + y01) * 16;
-  const int vfo = lr * (VTP * 2) + 16 * lq;  // V^T fragment of lane (r, q): d row 16 j + r, positions 32 ks + 8q ..
+  // V^T fragment (j, ks) of lane (r, q): d row 16 j + r, positions 32 ks + 8q .., granule (4 ks + q) ^ (r & 7)
+  const int vfo0 = lr * (VTP * 2) + (4 * x2 + y01) * 16, vfo1 = lr * (VTP * 2) + (4 * (x2 ^ 1) + y01) * 16;
 
   const int nblk = (k_hi + KB - 1) / KB;  // >= 1: k_hi > p0 + row0 / g >= 0
 #pragma unroll
@@ -668,11 +672,11 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnParams p) {
     }
 
     // O^T += V^T P^T
-    const unsigned char* Vt = smem + 2 * KSTAGE + st * VSTAGE + vfo;
+    const unsigned char* Vt = smem + 2 * KSTAGE + st * VSTAGE;
     constexpr int NF = 2 * NJ;  // V^T fragments per block: (ks, j) = (f / NJ, f % NJ)
     constexpr int VPF = 4;      // fragments in flight
     auto v_frag = [&](int f) {
-      return *reinterpret_cast<const bf16x8*>(Vt + (f % NJ) * 16 * (VTP * 2) + (f / NJ) * 64);
+      return *reinterpret_cast<const bf16x8*>(Vt + (f / NJ ? vfo1 : vfo0) + (f % NJ) * 16 * (VTP * 2));
     };
     bf16x8 vf[VPF];
 #pragma unroll
