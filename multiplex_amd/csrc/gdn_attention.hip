@@ -762,9 +762,36 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const AttnParams p) {
 
 // ------------------------------------------------------------ rms_norm
 
-// One workgroup per row; 8 bf16 elements per thread and pass.  With a
-// residual, the row is h = bf16(x + res) (written to h_out when given) and
-// y = norm(h); y's rows are y_ld elements apart.
+// Eight weights from index i (a multiple of 8) as floats: one 16-byte load for
+// bf16 / fp16, two for fp32 (the branch is uniform).
+__device__ __forceinline__ void load_w8(const void* w, int wdt, int i, float out[8]) {
+  if (wdt == GDN_DTYPE_F32) {
+    const f32x4 a = *reinterpret_cast<const f32x4*>(static_cast<const float*>(w) + i);
+    const f32x4 b = *reinterpret_cast<const f32x4*>(static_cast<const float*>(w) + i + 4);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      out[k] = a[k];
+      out[4 + k] = b[k];
+    }
+  } else {
+    const u32x4 v = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(w) + i);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const uint16_t lo = static_cast<uint16_t>(v[k] & 0xffffu), hi = static_cast<uint16_t>(v[k] >> 16);
+      out[2 * k] = wdt == GDN_DTYPE_BF16 ? bf16_to_f32(lo) : f16_to_f32(lo);
+      out[2 * k + 1] = wdt == GDN_DTYPE_BF16 ? bf16_to_f32(hi) : f16_to_f32(hi);
+    }
+  }
+}
+
+// One workgroup per row; 8 bf16 elements per thread and chunk, chunk c of
+// thread t at 8 t + 2048 c.  With a residual, the row is h = bf16(x + res)
+// (written to h_out when given) and y = norm(h); y's rows are y_ld elements
+// apart.  The first kRegChunks chunks of h stay in registers between the sum
+// of squares and the output (one pass over memory up to D = 8192); chunks
+// beyond are read again, from h_out when this thread wrote them (h_out may
+// alias x), else recomputed.
+constexpr int kRegChunks = 4;
 __global__ __launch_bounds__(256) void rms_norm_kernel(const uint16_t* x, const uint16_t* res, uint16_t* h_out,
                                                        const void* w, int wdt, uint16_t* y, int64_t y_ld, int D,
                                                        float eps) {
@@ -782,32 +809,62 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const uint16_t* x, const 
     }
     return v;
   };
-  float ss = 0.0f;
-  for (int c = 8 * threadIdx.x; c < D; c += 8 * 256) {
-    const u32x4 v = load_h(c);
-    if (h_out != nullptr) *reinterpret_cast<u32x4*>(h_out + row * D + c) = v;
+  auto sq = [](u32x4 v) {
+    float ss = 0.0f;
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
       const float a = __uint_as_float(v[k] << 16), bb = __uint_as_float(v[k] & 0xffff0000u);
       ss += a * a + bb * bb;
     }
+    return ss;
+  };
+  const int c0 = 8 * threadIdx.x;
+  u32x4 hv[kRegChunks];
+  float wv[kRegChunks][8];
+  float ss = 0.0f;
+#pragma unroll
+  for (int j = 0; j < kRegChunks; ++j) {
+    const int c = c0 + 2048 * j;
+    if (c < D) {
+      hv[j] = load_h(c);
+      load_w8(w, wdt, c, wv[j]);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < kRegChunks; ++j) {
+    const int c = c0 + 2048 * j;
+    if (c < D) {
+      if (h_out != nullptr) *reinterpret_cast<u32x4*>(h_out + row * D + c) = hv[j];
+      ss += sq(hv[j]);
+    }
+  }
+  for (int c = c0 + 2048 * kRegChunks; c < D; c += 2048) {
+    const u32x4 v = load_h(c);
+    if (h_out != nullptr) *reinterpret_cast<u32x4*>(h_out + row * D + c) = v;
+    ss += sq(v);
   }
   __shared__ float part[4];
   ss = wave_sum(ss);
   if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = ss;
   __syncthreads();
   const float r = rsqrtf((part[0] + part[1] + part[2] + part[3]) / D + eps);
-  for (int c = 8 * threadIdx.x; c < D; c += 8 * 256) {
-    // h again: from h_out when this thread wrote it (which may alias x), else recomputed
-    const u32x4 v = h_out != nullptr ? *reinterpret_cast<const u32x4*>(h_out + row * D + c) : load_h(c);
+  auto out8 = [&](int c, u32x4 v, const float* wk) {
     u32x4 o;
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const float a = __uint_as_float(v[k] << 16) * r * load_any(w, wdt, c + 2 * k);
-      const float bb = __uint_as_float(v[k] & 0xffff0000u) * r * load_any(w, wdt, c + 2 * k + 1);
-      o[k] = pk_bf16(a, bb);
-    }
+    for (int k = 0; k < 4; ++k)
+      o[k] = pk_bf16(__uint_as_float(v[k] << 16) * r * wk[2 * k], __uint_as_float(v[k] & 0xffff0000u) * r * wk[2 * k + 1]);
     *reinterpret_cast<u32x4*>(y + row * y_ld + c) = o;
+  };
+#pragma unroll
+  for (int j = 0; j < kRegChunks; ++j) {
+    const int c = c0 + 2048 * j;
+    if (c < D) out8(c, hv[j], wv[j]);
+  }
+  for (int c = c0 + 2048 * kRegChunks; c < D; c += 2048) {
+    const u32x4 v = h_out != nullptr ? *reinterpret_cast<const u32x4*>(h_out + row * D + c) : load_h(c);
+    float wk[8];
+    load_w8(w, wdt, c, wk);
+    out8(c, v, wk);
   }
 }
 
@@ -978,8 +1035,8 @@ extern "C" int gdn_rms_norm(const void* x, const void* res, void* h_out, const v
   if (!gdn_host::dtype_ok(w_dtype) || !(eps >= 0.0f)) return fail(GDN_ERR_INVALID, "gdn_rms_norm: bad weight dtype or eps");
   if (rows == 0) return GDN_OK;
   if (!x || !w || !y) return fail(GDN_ERR_INVALID, "gdn_rms_norm: null pointer");
-  if (!gdn_host::aligned(x, 16) || !gdn_host::aligned(y, 16) || (res && !gdn_host::aligned(res, 16)) ||
-      (h_out && !gdn_host::aligned(h_out, 16)))
+  if (!gdn_host::aligned(x, 16) || !gdn_host::aligned(y, 16) || !gdn_host::aligned(w, 16) ||
+      (res && !gdn_host::aligned(res, 16)) || (h_out && !gdn_host::aligned(h_out, 16)))
     return fail(GDN_ERR_INVALID, "gdn_rms_norm: misaligned pointer");
   hipLaunchKernelGGL(rms_norm_kernel, dim3(static_cast<unsigned>(rows)), dim3(256), 0, static_cast<hipStream_t>(stream),
                      static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(res), static_cast<uint16_t*>(h_out),
