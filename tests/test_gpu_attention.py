@@ -99,6 +99,8 @@ CASES = {
     "prefill_long": (2, 611, [0, 77], 1, True),
     "prefill_d128": (2, 300, [20, 0], 1, True, (16, 4, 128)),
     "prefill_g8": (1, 97, [130], 1, False, (16, 2, 256)),
+    "prefill_mha": (1, 520, [3], 1, True, (4, 4, 128)),
+    "prefill_g2": (3, 300, [0, 260, 41], 1, True, (8, 4, 256)),
 }
 
 
