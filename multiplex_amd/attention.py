@@ -410,9 +410,21 @@ class DecoderLayer(torch.nn.Module):
         self.post_attention_layernorm = RMSNorm(args.hidden_size, args.rms_norm_eps, device)
 
     def forward(self, x: torch.Tensor, cache: KVCache) -> torch.Tensor:
+        h, m = self.forward_parts(x, None, cache)
+        return h + m
+
+    def forward_parts(self, x: torch.Tensor, residual: Optional[torch.Tensor], cache: KVCache):
+        """The layer on ``x + residual`` (or ``x``), returning ``(h, m)`` whose
+        sum is its output: the caller adds them inside the next norm
+        (``gdn_rms_norm`` with a residual, the same bf16 rounding point), so no
+        residual add runs as a launch of its own."""
+        if residual is None:
+            xin, y0 = x, self.input_layernorm(x)
+        else:
+            xin, y0 = self.input_layernorm(x, residual=residual)
         # the residual add in front of the second norm is fused into it
-        h, y = self.post_attention_layernorm(x, residual=self.self_attn(self.input_layernorm(x), cache))
-        return h + self.mlp(y)
+        h, y = self.post_attention_layernorm(xin, residual=self.self_attn(y0, cache))
+        return h, self.mlp(y)
 
 
 class MTPHead(torch.nn.Module):
@@ -445,9 +457,11 @@ class MTPHead(torch.nn.Module):
         self.pre_fc_norm_embedding(embed, out=eh[..., :H])
         self.pre_fc_norm_hidden(hidden, out=eh[..., H:])
         x = torch.nn.functional.linear(eh, self.fc)
+        res = None  # the pending residual: each layer's output is x + res
         for layer, c in zip(self.layers, cache):
-            x = layer(x, c)
-        return self.norm(x)
+            x, res = layer.forward_parts(x, res, c)
+        # the last layer's residual add happens inside the final norm
+        return self.norm(res, residual=x)[1]
 
     @staticmethod
     def trim_cache_to(cache: Sequence[KVCache], size: int) -> None:
