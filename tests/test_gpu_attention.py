@@ -101,6 +101,9 @@ CASES = {
     "prefill_g8": (1, 97, [130], 1, False, (16, 2, 256)),
     "prefill_mha": (1, 520, [3], 1, True, (4, 4, 128)),
     "prefill_g2": (3, 300, [0, 260, 41], 1, True, (8, 4, 256)),
+    "prefill_g3": (1, 200, [17], 1, True, (12, 4, 128)),
+    "prefill_512_rows": (2, 128, [0, 5], 1, False),
+    "prefill_508_rows": (1, 127, [9], 1, True),
 }
 
 
