@@ -89,6 +89,24 @@ class Timer:
     def __init__(self, torch):
         self.torch = torch
 
+    def settle(self, fn, ms=100.0, batch=50):
+        """Untimed launches of ``fn`` until ``ms`` of device time has passed:
+        a GPU that was idle (input generation on the host) runs its first few
+        milliseconds at lower clocks, which a handful of warmup launches does
+        not cover.  Returns the launches made."""
+        t = self.torch
+        spent, n = 0.0, 0
+        while spent < ms:
+            s, e = t.cuda.Event(enable_timing=True), t.cuda.Event(enable_timing=True)
+            s.record()
+            for i in range(batch):
+                fn(n + i)
+            e.record()
+            t.cuda.synchronize()
+            spent += s.elapsed_time(e)
+            n += batch
+        return n
+
     def total_ms(self, fn, iters):
         t = self.torch
         t.cuda.synchronize()
@@ -159,6 +177,7 @@ def bench_decode_b64(torch, mx, dev, steps, warmup, timer):
                                   d["dt_bias"], state, state_out=state) for s in range(n)]
     for i in range(warmup):
         plans[i % n].launch()
+    timer.settle(lambda i: plans[i % n].launch())
     total = timer.total_ms(lambda i: plans[i % n].launch(), steps)
     per_launch, median = timer.per_launch_ms(lambda i: plans[i % n].launch(), steps)
     ok = bool(torch.isfinite(state).all())
@@ -329,6 +348,7 @@ def bench_decode_past_mall(torch, mx, dev, timer, B=256, steps=50):
                                 state_out=d["state"])
     for _ in range(5):
         plan.launch()
+    timer.settle(lambda i: plan.launch())
     t = timer.total_ms(lambda i: plan.launch(), steps) / steps
     gbs = decode_bytes(B) / (t * 1e-3) / 1e9
     del d, plan
@@ -406,6 +426,7 @@ def bench_pool(torch, mx, dev, timer, iters=20):
                                 state_index=pool.index(slots), state_out=pool.states)
     for _ in range(10):
         plan.launch()
+    timer.settle(lambda i: plan.launch())
     t_dec = timer.total_ms(lambda i: plan.launch(), 100) / 100
     return dict(change_dense_us=round(1e3 * t_dense, 2), change_pooled_us=round(1e3 * t_pool, 2),
                 dense_bytes_moved=(48 + 48 + 64) * state_bytes(1),

@@ -72,9 +72,21 @@ __device__ __forceinline__ float load_any(const void* p, int dt, int64_t i) {
 template <int DT>
 struct IO;
 
+// raw4 / raw1: the loaded bits before conversion (load4_raw, cvt4), for a
+// caller that issues many loads before it uses any of them.
 template <>
 struct IO<GDN_DTYPE_F32> {
   using elem = float;
+  using raw4 = f32x4;
+  using raw1 = float;
+  __device__ __forceinline__ static raw4 load4_raw(const void* p, int64_t i) {
+    return *reinterpret_cast<const f32x4*>(static_cast<const float*>(p) + i);
+  }
+  __device__ __forceinline__ static f32x4 cvt4(raw4 h) { return h; }
+  __device__ __forceinline__ static raw1 load1_raw(const void* p, int64_t i) {
+    return static_cast<const float*>(p)[i];
+  }
+  __device__ __forceinline__ static float cvt1(raw1 h) { return h; }
   __device__ __forceinline__ static f32x4 load4(const void* p, int64_t i) {
     return *reinterpret_cast<const f32x4*>(static_cast<const float*>(p) + i);
   }
@@ -96,6 +108,18 @@ struct IO<GDN_DTYPE_F32> {
 template <>
 struct IO<GDN_DTYPE_BF16> {
   using elem = uint16_t;
+  using raw4 = u16x4;
+  using raw1 = uint16_t;
+  __device__ __forceinline__ static raw4 load4_raw(const void* p, int64_t i) {
+    return *reinterpret_cast<const u16x4*>(static_cast<const uint16_t*>(p) + i);
+  }
+  __device__ __forceinline__ static f32x4 cvt4(raw4 h) {
+    return f32x4{bf16_to_f32(h.x), bf16_to_f32(h.y), bf16_to_f32(h.z), bf16_to_f32(h.w)};
+  }
+  __device__ __forceinline__ static raw1 load1_raw(const void* p, int64_t i) {
+    return static_cast<const uint16_t*>(p)[i];
+  }
+  __device__ __forceinline__ static float cvt1(raw1 h) { return bf16_to_f32(h); }
   __device__ __forceinline__ static f32x4 load4(const void* p, int64_t i) {
     u16x4 h = *reinterpret_cast<const u16x4*>(static_cast<const uint16_t*>(p) + i);
     return f32x4{bf16_to_f32(h.x), bf16_to_f32(h.y), bf16_to_f32(h.z), bf16_to_f32(h.w)};
@@ -119,6 +143,18 @@ struct IO<GDN_DTYPE_BF16> {
 template <>
 struct IO<GDN_DTYPE_F16> {
   using elem = uint16_t;
+  using raw4 = u16x4;
+  using raw1 = uint16_t;
+  __device__ __forceinline__ static raw4 load4_raw(const void* p, int64_t i) {
+    return *reinterpret_cast<const u16x4*>(static_cast<const uint16_t*>(p) + i);
+  }
+  __device__ __forceinline__ static f32x4 cvt4(raw4 h) {
+    return f32x4{f16_to_f32(h.x), f16_to_f32(h.y), f16_to_f32(h.z), f16_to_f32(h.w)};
+  }
+  __device__ __forceinline__ static raw1 load1_raw(const void* p, int64_t i) {
+    return static_cast<const uint16_t*>(p)[i];
+  }
+  __device__ __forceinline__ static float cvt1(raw1 h) { return f16_to_f32(h); }
   __device__ __forceinline__ static f32x4 load4(const void* p, int64_t i) {
     u16x4 h = *reinterpret_cast<const u16x4*>(static_cast<const uint16_t*>(p) + i);
     return f32x4{f16_to_f32(h.x), f16_to_f32(h.y), f16_to_f32(h.z), f16_to_f32(h.w)};
@@ -141,12 +177,25 @@ struct IO<GDN_DTYPE_F16> {
 
 // ------------------------------------------------------------ gate math
 
-// softplus(x) = log(1 + e^x) = max(x, 0) + log1p(e^-|x|), stable for all x.
+// The gates are transformed once per (token, head) and wave, where the
+// library's correctly rounded expf / log1pf and IEEE division cost ~150
+// instructions: the hardware exp2, log2 and reciprocal (v_exp_f32,
+// v_log_f32, v_rcp_f32, each within ~1 ulp) do it in ~20.  e^x = 2^(x log2 e)
+// has a relative error of ~|x| 2^-24, so g keeps ~1e-6 relative accuracy
+// wherever it is not negligibly small, and beta ~1e-7.
+__device__ __forceinline__ float exp_fast(float x) { return __builtin_amdgcn_exp2f(x * 1.44269504088896341f); }
+
+// softplus(x) = log(1 + e^x) = max(x, 0) + log1p(u), u = e^-|x| in (0, 1],
+// stable for all x.  log1p(u) = log(w) u / (w - 1) with w = 1 + u rounded
+// (Goldberg's correction of the rounding in w; u itself when w == 1).
 __device__ __forceinline__ float softplus_f(float x) {
-  return fmaxf(x, 0.0f) + log1pf(expf(-fabsf(x)));
+  const float u = exp_fast(-fabsf(x));
+  const float w = 1.0f + u;
+  const float lp = __builtin_amdgcn_logf(w) * 0.693147180559945309f * (u * __builtin_amdgcn_rcpf(w - 1.0f));
+  return fmaxf(x, 0.0f) + (w == 1.0f ? u : lp);
 }
 
-__device__ __forceinline__ float sigmoid_f(float x) { return 1.0f / (1.0f + expf(-x)); }
+__device__ __forceinline__ float sigmoid_f(float x) { return __builtin_amdgcn_rcpf(1.0f + exp_fast(-x)); }
 
 // Gate encodings.  GF_ANY reads runtime dtypes (and GDN_GATES_PRE); the
 // typed formats cover the usual layouts with plain typed loads, which keeps
@@ -179,14 +228,16 @@ __device__ __forceinline__ void gate_load(const GateArgs& ga, int64_t gi, float&
 }
 
 // Per-head parameters (raw mode): exp(A_log[hv]) and dt_bias[hv].
+// The loads of param_load without the exponential: A_log[hv] (0 for
+// pre-transformed gates) and dt_bias[hv].  A caller that issues more loads
+// after these applies expf(al) at its use, so nothing waits here.
 template <int GF, int DT>
-__device__ __forceinline__ void param_load(const GateArgs& ga, int hv, float& ea, float& db) {
-  if (ga.mode == GDN_GATES_PRE) {
-    ea = 0.0f;
+__device__ __forceinline__ void param_load_raw(const GateArgs& ga, int hv, float& al, float& db) {
+  if (GF == GF_ANY && ga.mode == GDN_GATES_PRE) {  // typed formats are raw gates
+    al = 0.0f;
     db = 0.0f;
     return;
   }
-  float al;
   if constexpr (GF == GF_ANY) {
     al = load_any(ga.A_log, ga.pdt, hv);
     db = load_any(ga.dt_bias, ga.pdt, hv);
@@ -197,7 +248,13 @@ __device__ __forceinline__ void param_load(const GateArgs& ga, int hv, float& ea
     al = IO<DT>::load1(ga.A_log, hv);
     db = IO<DT>::load1(ga.dt_bias, hv);
   }
-  ea = expf(al);
+}
+
+template <int GF, int DT>
+__device__ __forceinline__ void param_load(const GateArgs& ga, int hv, float& ea, float& db) {
+  float al;
+  param_load_raw<GF, DT>(ga, hv, al, db);
+  ea = GF == GF_ANY && ga.mode == GDN_GATES_PRE ? 0.0f : exp_fast(al);
 }
 
 // g = exp(-exp(A_log) softplus(a + dt_bias)), beta = sigmoid(b)  (raw mode).
@@ -208,7 +265,7 @@ __device__ __forceinline__ void gate_transform(int mode, float x, float y, float
     g = x;
     beta = y;
   } else {
-    g = expf(-ea * softplus_f(x + db));
+    g = exp_fast(-ea * softplus_f(x + db));
     beta = sigmoid_f(y);
   }
 }
@@ -253,7 +310,7 @@ __device__ __forceinline__ void log_gates(const GateArgs& ga, const GateRaw& r, 
   } else {
     const float al = raw_any_value(ga.pdt, r.lo[2], r.hi[2]);
     const float db = raw_any_value(ga.pdt, r.lo[3], r.hi[3]);
-    logg = -expf(al) * softplus_f(x + db);
+    logg = -exp_fast(al) * softplus_f(x + db);
     beta = sigmoid_f(y);
   }
 }

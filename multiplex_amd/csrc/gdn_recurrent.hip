@@ -6,16 +6,21 @@
 // optional per-token snapshots).  Rows of S (one dv index each) are
 // independent in the recurrence, so the kernel parallelises over dv:
 //
-//   * 8 lanes own one state row of Dk floats; lane `sub` holds the float4s
-//     at offsets i*32 + sub*4 (i < Dk/32), so one load instruction of a wave
-//     covers 8 rows x 128 contiguous bytes (whole cache lines).
-//   * the two dot products per token (S k and S q) are 8-lane DPP sums.
-//   * a workgroup holds 8 rows per wave; the grid is (dv blocks, Hv, rows).
+//   * LPR lanes own one state row of Dk floats; lane `sub` holds the float4s
+//     at offsets i*4*LPR + sub*4 (i < Dk/(4*LPR)).  The decode kernel uses
+//     LPR = Dk/4 (one float4 per lane, 1 KB of contiguous state per load
+//     instruction); the multi-token kernels use LPR = 8 (8 rows x 128
+//     contiguous bytes per instruction, 32 rows per 4-wave workgroup, so a
+//     token tile in LDS serves 32 rows).
+//   * the two dot products per token (S k and S q) are summed over the row's
+//     lanes in one order for both layouts (row_dot): a state steps
+//     bit-identically in the decode and the multi-token kernels.
+//   * the grid is (dv blocks, Hv, rows).
 //
 // Every load is branch-free (clamped addresses; a device-resident zero row
-// for a missing state, a constant 1 for a missing mask), and a token's
-// inputs are issued ahead of the state stream, so one memory latency covers
-// both.  Algorithmic traffic per (row, head): Dv*Dk*4 bytes read + the same
+// for a missing state, a constant 1 for a missing mask), and the state load
+// is issued first with a token's inputs right behind it, none of them used
+// before all are issued, so one memory latency covers both.  Algorithmic traffic per (row, head): Dv*Dk*4 bytes read + the same
 // written (once), plus q/k/v/y/gates per token; the kernel is HBM-bound.
 #include "gdn_common.hpp"
 
@@ -30,30 +35,43 @@ constexpr int kMaxDk = 256;
 __device__ const float kZeroRow[kMaxDk] = {};
 __device__ const uint8_t kActive = 1;
 
+// Global-memory views of a pointer that may be either a kernel argument or
+// one of the stand-ins above: a select between the two is a generic pointer,
+// whose loads would be flat loads, and a flat load also counts on the
+// scalar-load counter, so the gate parameters' scalar loads would wait for it.
+typedef __attribute__((address_space(1))) const f32x4 gbl_f32x4;
+typedef __attribute__((address_space(1))) const uint8_t gbl_u8;
+
 struct RecParams {
+  // the fields the decode kernel reads come first (two 64-byte parameter loads)
   const void* q;
   const void* k;
   const void* v;
-  GateArgs ga;
   const float* state_in;
   float* state_out;
-  float* snapshots;
   void* y;
+  GateArgs ga;
+  int Hk, Hv, Dv, group;     // group = Hv / Hk
+  unsigned group_magic;      // ceil(2^31 / group): hv / group = (hv * magic) >> 31
+  int wg_rows;               // state rows per workgroup (decode kernel)
+  int T, n_slots;
+  const int32_t* state_index;  // slot of each row in pooled states, or NULL
+  float* snapshots;
   const uint8_t* mask;
   const int32_t* cu_seqlens;
   const int32_t* commit_len;
-  const int32_t* state_index;  // slot of each row in pooled states, or NULL
-  int n_slots;
-  int T, Hk, Hv, Dv, group;  // group = Hv / Hk
 };
 
-template <int EPL>
+// A state row of Dk floats is spread over LPR lanes: lane `sub` holds the
+// float4s at offsets i*4*LPR + sub*4, so one load instruction covers
+// 64/LPR rows x 16*LPR contiguous bytes.
+template <int EPL, int LPR = kLanesPerRow>
 __device__ __forceinline__ void store_row(float* dst, int sub, const float (&s)[EPL]) {
   constexpr int NV = EPL / 4;
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
     f32x4 x = {s[4 * i], s[4 * i + 1], s[4 * i + 2], s[4 * i + 3]};
-    __builtin_nontemporal_store(x, reinterpret_cast<f32x4*>(dst + i * 32 + sub * 4));
+    __builtin_nontemporal_store(x, reinterpret_cast<f32x4*>(dst + i * 4 * LPR + sub * 4));
   }
 }
 
@@ -67,28 +85,28 @@ struct TokenIn {
   uint8_t m;
 };
 
-template <int DK, int DT, int GF, bool WANT_Q>
-__device__ __forceinline__ void load_token(const RecParams& p, int64_t tok, int hv, int hk, int dv_c, int sub,
-                                           TokenIn<DK / kLanesPerRow>& in) {
-  constexpr int NV = DK / kLanesPerRow / 4;
+// q is read from `qp`: the kernel passes k there when no output is wanted,
+// so the load stays unconditional and its value is never used.
+template <int DK, int DT, int GF, int LPR>
+__device__ __forceinline__ void load_token(const RecParams& p, const void* qp, int64_t tok, int hv, int hk,
+                                           int dv_c, int sub, TokenIn<DK / LPR>& in) {
+  constexpr int NV = DK / LPR / 4;
   const uint8_t* mp = p.mask != nullptr ? p.mask + tok : &kActive;
-  in.m = *mp;
+  in.m = *(gbl_u8*)mp;
   gate_load<GF, DT>(p.ga, tok * p.ga.ld + hv, in.gx, in.gy);
   const int64_t kq = (tok * p.Hk + hk) * DK + sub * 4;
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
-    const f32x4 x = IO<DT>::load4(p.k, kq + i * 32);
+    const f32x4 x = IO<DT>::load4(p.k, kq + i * 4 * LPR);
+    const f32x4 z = IO<DT>::load4(qp, kq + i * 4 * LPR);
     in.k[4 * i] = x.x;
     in.k[4 * i + 1] = x.y;
     in.k[4 * i + 2] = x.z;
     in.k[4 * i + 3] = x.w;
-    if (WANT_Q) {
-      const f32x4 z = IO<DT>::load4(p.q, kq + i * 32);
-      in.q[4 * i] = z.x;
-      in.q[4 * i + 1] = z.y;
-      in.q[4 * i + 2] = z.z;
-      in.q[4 * i + 3] = z.w;
-    }
+    in.q[4 * i] = z.x;
+    in.q[4 * i + 1] = z.y;
+    in.q[4 * i + 2] = z.z;
+    in.q[4 * i + 3] = z.w;
   }
   in.v = IO<DT>::load1(p.v, (tok * p.Hv + hv) * p.Dv + dv_c);
 }
@@ -101,11 +119,11 @@ struct RowCtx {
   int64_t tok0, srow, srow_c;
 };
 
-template <int DK>
+template <int DK, int LPR = kLanesPerRow>
 __device__ __forceinline__ RowCtx row_ctx(const RecParams& p) {
   RowCtx c;
-  c.sub = threadIdx.x & (kLanesPerRow - 1);
-  c.dv = blockIdx.x * (blockDim.x / kLanesPerRow) + threadIdx.x / kLanesPerRow;
+  c.sub = threadIdx.x & (LPR - 1);
+  c.dv = blockIdx.x * (blockDim.x / LPR) + threadIdx.x / LPR;
   c.row_ok = c.dv < p.Dv;
   c.dv_c = c.row_ok ? c.dv : p.Dv - 1;  // loads use a valid row; stores check row_ok
   c.hv = blockIdx.y;
@@ -147,13 +165,13 @@ __device__ __forceinline__ RowCtx row_ctx(const RecParams& p) {
   return c;
 }
 
-template <int DK>
-__device__ __forceinline__ void load_state(const RecParams& p, const RowCtx& c, float (&s)[DK / kLanesPerRow]) {
-  constexpr int NV = DK / kLanesPerRow / 4;
+template <int DK, int LPR = kLanesPerRow>
+__device__ __forceinline__ void load_state(const RecParams& p, const RowCtx& c, float (&s)[DK / LPR]) {
+  constexpr int NV = DK / LPR / 4;
   const float* src = p.state_in != nullptr ? p.state_in + c.srow_c : kZeroRow;
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
-    const f32x4 x = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(src + i * 32 + c.sub * 4));
+    const f32x4 x = __builtin_nontemporal_load((gbl_f32x4*)(src + i * 4 * LPR + c.sub * 4));
     s[4 * i] = x.x;
     s[4 * i + 1] = x.y;
     s[4 * i + 2] = x.z;
@@ -161,76 +179,180 @@ __device__ __forceinline__ void load_state(const RecParams& p, const RowCtx& c, 
   }
 }
 
+// row_ror:8 inside a 16-lane row: lane l reads lane l ^ 8.
+#define GDN_DPP_ROW_ROR8 0x128
+
+// Dot product of a lane's slice of a state row with the matching slice of x,
+// summed over the row's LPR lanes in one fixed order for both lane layouts,
+// so that the decode kernel (LPR = Dk/4) and the multi-token kernels
+// (LPR = 8) step a state bit-identically.  The order: the row's Dk columns
+// form Dk/32 blocks of 32; inside a block, the 4 columns of each group g
+// (g = (column/4) % 8) are a 4-term fma chain; the blocks' chains of one
+// group are added in a balanced pairwise tree (blocks 2m and 2m+1 first);
+// the 8 group sums are then added by sum8.  With LPR = 8 a lane holds all
+// blocks of its group and the tree is in-lane; with LPR = Dk/4 lane
+// 8*block + g holds one chain, and blocks 2m, 2m+1 are 8 lanes apart (DPP
+// row_ror:8), pairs of those 16 lanes apart (permlane16 swap), quads 32
+// lanes apart (permlane32 swap).
+template <int EPL, int LPR>
+__device__ __forceinline__ float row_dot(const float (&s)[EPL], const float (&x)[EPL]) {
+  constexpr int NV = EPL / 4;
+  static_assert(LPR == 8 || NV == 1, "a row spans 8 lanes or holds one float4 per lane");
+  float part[NV];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    float c = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) c = fmaf(s[4 * i + j], x[4 * i + j], c);
+    part[i] = c;
+  }
+#pragma unroll
+  for (int w = 1; w < NV; w *= 2) {
+#pragma unroll
+    for (int i = 0; i + w < NV; i += 2 * w) part[i] += part[i + w];
+  }
+  float r = part[0];
+  if constexpr (LPR >= 16) r += dpp_f<GDN_DPP_ROW_ROR8>(r);
+  if constexpr (LPR >= 32) {
+    const auto h = __builtin_amdgcn_permlane16_swap(__float_as_uint(r), __float_as_uint(r), false, false);
+    r = __uint_as_float(h[0]) + __uint_as_float(h[1]);
+  }
+  if constexpr (LPR >= 64) {
+    const auto h = __builtin_amdgcn_permlane32_swap(__float_as_uint(r), __float_as_uint(r), false, false);
+    r = __uint_as_float(h[0]) + __uint_as_float(h[1]);
+  }
+  return sum8(r);
+}
+
 // One token of the recurrence on a lane's slice of a state row:
-// S <- g S;  kv = S k;  S <- S + beta (v - kv) k^T  (kv summed over 8 lanes).
-template <int EPL>
+// S <- g S;  kv = S k;  S <- S + beta (v - kv) k^T  (kv by row_dot).
+template <int EPL, int LPR = kLanesPerRow>
 __device__ __forceinline__ void step_row(float (&s)[EPL], const float (&k)[EPL], float v, float g,
                                           float beta) {
-  float kv = 0.0f;
 #pragma unroll
-  for (int e = 0; e < EPL; ++e) {
-    s[e] *= g;
-    kv = fmaf(s[e], k[e], kv);
-  }
-  kv = sum8(kv);
+  for (int e = 0; e < EPL; ++e) s[e] *= g;
+  const float kv = row_dot<EPL, LPR>(s, k);
   const float delta = beta * (v - kv);
 #pragma unroll
   for (int e = 0; e < EPL; ++e) s[e] = fmaf(k[e], delta, s[e]);
 }
 
-// Decode body (one token per row, T = 1): no LDS, no barriers; the token's
-// inputs are issued ahead of the state stream so one latency covers both.
-template <int DK, int DT, int GF>
+// Decode body (T <= 1 token per row, rows not packed): no LDS, no barriers,
+// no loop.  A state row is spread over Dk/4 lanes, one float4 each, so a
+// load instruction of a wave covers 1 KB of contiguous state (at Dk = 128:
+// two rows) and a wave streams exactly one such unit: that shape streams the
+// in-place read + write of a 128 MiB state at ~6.7-6.9 TB/s, against ~6.2
+// TB/s for waves that hold two or more units (8 lanes per row with four
+// float4 each, or one float4 per lane over several row pairs).  With that
+// many short waves the per-wave scalar work is what limits, so the body is
+// straight-line, indexes in 32 bits (the host bounds every tensor below 2^31
+// elements), divides hv by the group with a multiplier, and takes the rows
+// per workgroup from the parameters.  The state load is issued first and
+// the token's loads right behind it, so one latency covers both.  Dot
+// products over a row are row_dot, in the order of the multi-token kernels.
+//
+// MODE: kDecodeAny takes every option at run time.  kDecodeLean and
+// kDecodeLeanPooled are the serving step with every option fixed -- T = 1,
+// state_in and state_out given, y wanted, no mask, commit lengths or
+// snapshots, raw gates of a typed format -- without (with) a pool-slot
+// table: the same code with those checks removed, so the same results.
+enum DecodeMode { kDecodeAny = 0, kDecodeLean = 1, kDecodeLeanPooled = 2 };
+
+template <int DK, int DT, int GF, int MODE>
 __global__ __launch_bounds__(256) void recurrent_kernel(const RecParams p) {
-  constexpr int EPL = DK / kLanesPerRow;  // fp32 state elements per lane
-  constexpr int NV = EPL / 4;             // float4 per lane
-  const RowCtx c = row_ctx<DK>(p);
-  if (c.skip) return;  // uniform: a workgroup serves one row
-
-  TokenIn<EPL> cur;
-  if (c.steps > 0) load_token<DK, DT, GF, false>(p, c.tok0, c.hv, c.hk, c.dv_c, c.sub, cur);
-  float ea, db;
-  param_load<GF, DT>(p.ga, c.hv, ea, db);
-  float s[EPL];
-  load_state<DK>(p, c, s);
-  if (c.write_state && c.commit == 0 && c.row_ok) store_row<EPL>(p.state_out + c.srow, c.sub, s);
-
-  for (int t = 0; t < c.steps; ++t) {
-    const int64_t tok = c.tok0 + t;
-    float yv = 0.0f;
-    if (cur.m != 0) {
-      float g, beta;
-      gate_transform<GF>(p.ga.mode, cur.gx, cur.gy, ea, db, g, beta);
-      step_row<EPL>(s, cur.k, cur.v, g, beta);
-      if (c.want_y) {
-        float yp = 0.0f;
-        const int64_t kq = (tok * p.Hk + c.hk) * DK + c.sub * 4;
-#pragma unroll
-        for (int i = 0; i < NV; ++i) {
-          const f32x4 x = IO<DT>::load4(p.q, kq + i * 32);
-          yp = fmaf(s[4 * i], x.x, yp);
-          yp = fmaf(s[4 * i + 1], x.y, yp);
-          yp = fmaf(s[4 * i + 2], x.z, yp);
-          yp = fmaf(s[4 * i + 3], x.w, yp);
-        }
-        yv = sum8(yp);
-      }
-    }
-    if (c.want_y && c.row_ok && c.sub == 0) IO<DT>::store1(p.y, (tok * p.Hv + c.hv) * p.Dv + c.dv, yv);
-    if (p.snapshots != nullptr && c.row_ok) {
-      store_row<EPL>(p.snapshots + ((tok * p.Hv + c.hv) * p.Dv + c.dv) * DK, c.sub, s);
-    }
-    if (c.write_state && t + 1 == c.commit && c.row_ok) store_row<EPL>(p.state_out + c.srow, c.sub, s);
-    if (t + 1 < c.steps) load_token<DK, DT, GF, false>(p, tok + 1, c.hv, c.hk, c.dv_c, c.sub, cur);
+  constexpr int LPR = DK / 4;  // lanes per state row, one float4 each
+  constexpr bool lean = MODE != kDecodeAny;
+  static_assert(!lean || GF != GF_ANY, "the lean decode takes raw gates of a typed format");
+  float s[4];
+  const int sub = threadIdx.x & (LPR - 1);
+  const int row = blockIdx.z, hv = blockIdx.y;
+  const int hk = static_cast<int>((static_cast<uint64_t>(hv) * p.group_magic) >> 31);
+  const int dv = blockIdx.x * p.wg_rows + static_cast<int>(threadIdx.x) / LPR;
+  const bool row_ok = dv < p.Dv;
+  const int dv_c = row_ok ? dv : p.Dv - 1;  // loads use a valid row; stores check row_ok
+  int slot = row;
+  if (MODE == kDecodeLeanPooled || (MODE == kDecodeAny && p.state_index != nullptr)) {
+    slot = p.state_index[row];
+    if (slot < 0 || slot >= p.n_slots) return;  // uniform: not processed
   }
+  const unsigned srow_c = (static_cast<unsigned>(slot) * p.Hv + hv) * p.Dv + dv_c;
+  {
+    const float* src = lean || p.state_in != nullptr ? p.state_in + static_cast<size_t>(srow_c) * DK : kZeroRow;
+    const f32x4 x = __builtin_nontemporal_load((gbl_f32x4*)(src + sub * 4));
+    s[0] = x.x;
+    s[1] = x.y;
+    s[2] = x.z;
+    s[3] = x.w;
+  }
+  float al, db;
+  param_load_raw<GF, DT>(p.ga, hv, al, db);
+  // the output pointer is read with the other parameters, not at its store
+  // (a parameter read there would be one more wait at the end of every wave)
+  void* yp = p.y;
+  asm volatile("" : "+s"(yp));
+
+  // T is 0 or 1 here: the token of row `row` is token `row`.  A negative
+  // commit length skips the row: in place it is not written at all; into a
+  // separate state_out it is copied unchanged (commit 0).
+  const int L = lean ? 1 : p.T;
+  bool write_state = lean || p.state_out != nullptr;
+  int commit = L;
+  if (!lean && p.commit_len != nullptr) {
+    const int cl = p.commit_len[row];
+    if (cl < 0 && p.state_out == p.state_in) write_state = false;
+    commit = cl < 0 ? 0 : min(cl, L);
+  }
+  const bool want_y = lean || p.y != nullptr;
+  const bool snaps = !lean && p.snapshots != nullptr;
+  const bool step = lean || (L > 0 && (want_y || snaps || (write_state && commit > 0)));
+  const unsigned srow = srow_c + (dv - dv_c);  // the row the stores address (row_ok)
+
+  typename IO<DT>::raw4 kr = {}, qr = {};
+  typename IO<DT>::raw1 vr = {};
+  float gx = 0.0f, gy = 0.0f;
+  uint8_t m = 0;
+  if (step) {
+    const unsigned kq = (static_cast<unsigned>(row) * p.Hk + hk) * DK + sub * 4;
+    kr = IO<DT>::load4_raw(p.k, kq);
+    qr = IO<DT>::load4_raw(want_y ? p.q : p.k, kq);  // k stands in when no output is wanted
+    vr = IO<DT>::load1_raw(p.v, (static_cast<unsigned>(row) * p.Hv + hv) * p.Dv + dv_c);
+    gate_load<GF, DT>(p.ga, static_cast<unsigned>(row) * static_cast<unsigned>(p.ga.ld) + hv, gx, gy);
+    if (lean) {
+      m = 1;
+    } else {
+      const uint8_t* mp = p.mask != nullptr ? p.mask + row : &kActive;
+      m = *(gbl_u8*)mp;
+    }
+  }
+  if (!lean && write_state && commit == 0 && row_ok)
+    store_row<4, LPR>(p.state_out + static_cast<size_t>(srow) * DK, sub, s);
+  if (!step) return;
+
+  float yv = 0.0f;
+  if (m != 0) {
+    const float ea = GF == GF_ANY && p.ga.mode == GDN_GATES_PRE ? 0.0f : exp_fast(al);
+    float g, beta;
+    gate_transform<GF>(p.ga.mode, gx, gy, ea, db, g, beta);
+    const f32x4 k4 = IO<DT>::cvt4(kr);
+    const float kf[4] = {k4.x, k4.y, k4.z, k4.w};
+    step_row<4, LPR>(s, kf, IO<DT>::cvt1(vr), g, beta);
+    if (want_y) {
+      const f32x4 q4 = IO<DT>::cvt4(qr);
+      const float qf[4] = {q4.x, q4.y, q4.z, q4.w};
+      yv = row_dot<4, LPR>(s, qf);
+    }
+  }
+  const unsigned yi = (static_cast<unsigned>(row) * p.Hv + hv) * p.Dv + dv;
+  if (want_y && row_ok && sub == 0) IO<DT>::store1(yp, yi, yv);
+  if (snaps && row_ok) store_row<4, LPR>(p.snapshots + static_cast<size_t>(yi) * DK, sub, s);
+  if (write_state && commit == 1 && row_ok) store_row<4, LPR>(p.state_out + static_cast<size_t>(srow) * DK, sub, s);
 }
 
 // Multi-token body (verify, commit, packed rows): the workgroup (always 4
 // waves, 32 state rows) stages a tile of kTile tokens -- k and q as fp32, the
 // transformed gates, the mask and the v values of its rows -- in LDS, then
 // every wave walks the tile from LDS.  The first tile's global loads are
-// issued before the state stream: loads complete in issue order, so the tile
-// reaches LDS while the state is still arriving.
+// issued right behind the state stream, so both arrive within one latency.
 constexpr int kTile = 16;
 constexpr int kTileThreads = 256;
 constexpr int kTileRows = kTileThreads / kLanesPerRow;  // 32
@@ -253,13 +375,23 @@ __global__ __launch_bounds__(kTileThreads) void recurrent_tile_kernel(const RecP
   __shared__ float Gt[kTile], Bt[kTile];
   __shared__ uint8_t Mt[kTile];
 
-  float ea, db;
-  param_load<GF, DT>(p.ga, c.hv, ea, db);
+  // The state load is issued first, then the parameters' and the first
+  // tile's loads: loads complete in issue order, so the first use of a tile
+  // value waits for one latency covering all of them.  Every load is
+  // unconditional (q is read from k when no output is wanted): a load under
+  // a branch sits in a block of its own, whose use the compiler would wait
+  // for there, before the next load is issued.
+  float s[EPL];
+  load_state<DK>(p, c, s);
+  float al, db;
+  param_load_raw<GF, DT>(p.ga, c.hv, al, db);
+  const void* qp = c.want_y ? p.q : p.k;
 
-  f32x4 kr[KV4], qr[KV4];
-  float vr[VV];
+  typename IO<DT>::raw4 kr[KV4], qr[KV4];  // converted when written to LDS
+  typename IO<DT>::raw1 vr[VV];
   float gx = 0.0f, gy = 0.0f;
   uint8_t mm = 1;
+  float ea = 0.0f;
   // rows past the tile's n tokens re-read its last token (never used)
   auto issue_tile = [&](int t0, int n) {
 #pragma unroll
@@ -267,21 +399,23 @@ __global__ __launch_bounds__(kTileThreads) void recurrent_tile_kernel(const RecP
       const int i = tid + kTileThreads * it;
       const int j = i / (DK / 4), e = (i % (DK / 4)) * 4;
       const int64_t off = ((c.tok0 + t0 + min(j, n - 1)) * p.Hk + c.hk) * DK + e;
-      kr[it] = IO<DT>::load4(p.k, off);
-      if (c.want_y) qr[it] = IO<DT>::load4(p.q, off);
+      kr[it] = IO<DT>::load4_raw(p.k, off);
+      qr[it] = IO<DT>::load4_raw(qp, off);
     }
 #pragma unroll
     for (int it = 0; it < VV; ++it) {
       const int i = tid + kTileThreads * it;
       const int j = i / kTileRows, r = i % kTileRows;
       const int64_t tok = c.tok0 + t0 + min(j, n - 1);
-      vr[it] = IO<DT>::load1(p.v, (tok * p.Hv + c.hv) * p.Dv + min(dv0 + r, p.Dv - 1));
+      vr[it] = IO<DT>::load1_raw(p.v, (tok * p.Hv + c.hv) * p.Dv + min(dv0 + r, p.Dv - 1));
     }
-    if (tid < kTile) {
+    // threads tid < kTile keep token tid's gates and mask; the others load a
+    // valid token too (no branch) and never use it
+    {
       const int64_t tok = c.tok0 + t0 + min(tid, n - 1);
       gate_load<GF, DT>(p.ga, tok * p.ga.ld + c.hv, gx, gy);
       const uint8_t* mp = p.mask != nullptr ? p.mask + tok : &kActive;
-      mm = *mp;
+      mm = *(gbl_u8*)mp;
     }
   };
   auto store_tile = [&]() {
@@ -289,13 +423,13 @@ __global__ __launch_bounds__(kTileThreads) void recurrent_tile_kernel(const RecP
     for (int it = 0; it < KV4; ++it) {
       const int i = tid + kTileThreads * it;
       const int j = i / (DK / 4), e = (i % (DK / 4)) * 4;
-      *reinterpret_cast<f32x4*>(&Kt[j][e]) = kr[it];
-      if (c.want_y) *reinterpret_cast<f32x4*>(&Qt[j][e]) = qr[it];
+      *reinterpret_cast<f32x4*>(&Kt[j][e]) = IO<DT>::cvt4(kr[it]);
+      if (c.want_y) *reinterpret_cast<f32x4*>(&Qt[j][e]) = IO<DT>::cvt4(qr[it]);
     }
 #pragma unroll
     for (int it = 0; it < VV; ++it) {
       const int i = tid + kTileThreads * it;
-      Vt[i / kTileRows][i % kTileRows] = vr[it];
+      Vt[i / kTileRows][i % kTileRows] = IO<DT>::cvt1(vr[it]);
     }
     if (tid < kTile) {
       float g, beta;
@@ -307,8 +441,7 @@ __global__ __launch_bounds__(kTileThreads) void recurrent_tile_kernel(const RecP
   };
 
   if (c.steps > 0) issue_tile(0, min(kTile, c.steps));
-  float s[EPL];
-  load_state<DK>(p, c, s);
+  ea = GF == GF_ANY && p.ga.mode == GDN_GATES_PRE ? 0.0f : exp_fast(al);
   if (c.write_state && c.commit == 0 && c.row_ok) store_row<EPL>(p.state_out + c.srow, c.sub, s);
 
   for (int t0 = 0; t0 < c.steps; t0 += kTile) {
@@ -337,16 +470,16 @@ __global__ __launch_bounds__(kTileThreads) void recurrent_tile_kernel(const RecP
         }
         step_row<EPL>(s, kf, Vt[j][rloc], Gt[j], Bt[j]);
         if (c.want_y) {
-          float yp = 0.0f;
+          float qf[EPL];
 #pragma unroll
           for (int i = 0; i < NV; ++i) {
             const f32x4 x = *reinterpret_cast<const f32x4*>(&Qt[j][i * 32 + c.sub * 4]);
-            yp = fmaf(s[4 * i], x.x, yp);
-            yp = fmaf(s[4 * i + 1], x.y, yp);
-            yp = fmaf(s[4 * i + 2], x.z, yp);
-            yp = fmaf(s[4 * i + 3], x.w, yp);
+            qf[4 * i] = x.x;
+            qf[4 * i + 1] = x.y;
+            qf[4 * i + 2] = x.z;
+            qf[4 * i + 3] = x.w;
           }
-          yv = sum8(yp);
+          yv = row_dot<EPL, kLanesPerRow>(s, qf);
         }
       }
       if (c.want_y && c.row_ok && c.sub == 0) IO<DT>::store1(p.y, (tok * p.Hv + c.hv) * p.Dv + c.dv, yv);
@@ -391,46 +524,52 @@ __global__ __launch_bounds__(kTileThreads) void verify_wy_kernel(const RecParams
   __shared__ float Ckk[TM][TM], Ckq[TM][TM];
   __shared__ uint8_t Ms[TM];
 
-  float ea, db;
-  param_load<GF, DT>(p.ga, c.hv, ea, db);
+  // The state row is issued first, then every token load (all
+  // unconditional, with clamped addresses, kept as loaded bits until all are
+  // issued): loads complete in issue order, so one latency covers them all.
+  float s[EPL];
+  load_state<DK>(p, c, s);
+  float al, db;
+  param_load_raw<GF, DT>(p.ga, c.hv, al, db);
 
-  // token loads first (memory returns in issue order), then the state row
   constexpr int NK4 = TM * DK / 4;  // float4 of k (and of q) in the tile
   constexpr int KV4 = (NK4 + kTileThreads - 1) / kTileThreads;
-  f32x4 kr[KV4], qr[KV4];
+  typename IO<DT>::raw4 kr[KV4], qr[KV4];
   static_for<KV4>([&](auto it) {
     const int i = min(tid + kTileThreads * it.value, NK4 - 1);
     const int j = i / (DK / 4), e = (i % (DK / 4)) * 4;
     const int64_t off = ((c.tok0 + min(j, T - 1)) * p.Hk + c.hk) * DK + e;
-    kr[it.value] = IO<DT>::load4(p.k, off);
-    qr[it.value] = IO<DT>::load4(p.q, off);
+    kr[it.value] = IO<DT>::load4_raw(p.k, off);
+    qr[it.value] = IO<DT>::load4_raw(p.q, off);
   });
-  float vr = 0.0f, gx = 0.0f, gy = 0.0f;
-  uint8_t mm = 1;
+  typename IO<DT>::raw1 vr;
+  float gx, gy;
+  uint8_t mm;
   {
     const int j = min(tid / kTileRows, TM - 1), r = tid % kTileRows;
     const int64_t tok = c.tok0 + min(j, T - 1);
-    vr = IO<DT>::load1(p.v, (tok * p.Hv + c.hv) * p.Dv + min(dv0 + r, p.Dv - 1));
+    vr = IO<DT>::load1_raw(p.v, (tok * p.Hv + c.hv) * p.Dv + min(dv0 + r, p.Dv - 1));
   }
-  if (tid < TM) {
+  // threads tid < TM keep token tid's gates and mask; the others load a
+  // valid token too and never use it
+  {
     const int64_t tok = c.tok0 + min(tid, T - 1);
     gate_load<GF, DT>(p.ga, tok * p.ga.ld + c.hv, gx, gy);
     const uint8_t* mp = p.mask != nullptr ? p.mask + tok : &kActive;
-    mm = *mp;
+    mm = *(gbl_u8*)mp;
   }
-  float s[EPL];
-  load_state<DK>(p, c, s);
 
   static_for<KV4>([&](auto it) {
     const int i = tid + kTileThreads * it.value;
     if (i < NK4) {
       const int j = i / (DK / 4), e = (i % (DK / 4)) * 4;
-      *reinterpret_cast<f32x4*>(&Ks[j][e]) = kr[it.value];
-      *reinterpret_cast<f32x4*>(&Qs[j][e]) = qr[it.value];
+      *reinterpret_cast<f32x4*>(&Ks[j][e]) = IO<DT>::cvt4(kr[it.value]);
+      *reinterpret_cast<f32x4*>(&Qs[j][e]) = IO<DT>::cvt4(qr[it.value]);
     }
   });
-  if (tid < TM * kTileRows) Vs[tid / kTileRows][tid % kTileRows] = vr;
+  if (tid < TM * kTileRows) Vs[tid / kTileRows][tid % kTileRows] = IO<DT>::cvt1(vr);
   if (tid < TM) {
+    const float ea = GF == GF_ANY && p.ga.mode == GDN_GATES_PRE ? 0.0f : exp_fast(al);
     float g, beta;
     gate_transform<GF>(p.ga.mode, gx, gy, ea, db, g, beta);
     const bool on = mm != 0 && tid < T;
@@ -577,61 +716,76 @@ __global__ __launch_bounds__(256) void verify_mfma_kernel(const RecParams p) {
 
   __shared__ __align__(16) uint16_t KQ[16][KP];  // k_0..k_{TM-1}, q_0..q_{TM-1}, then zero rows
   __shared__ float Vs[TM][kVmRows];
-  __shared__ float Gs[TM], Bs[TM];  // g_t, beta_t (1 and 0 when masked)
-  __shared__ uint8_t Ms[TM];
+  // g_t, beta_t (1 and 0 when masked), mask; slot TM is written by the
+  // threads tid >= TM and never read
+  __shared__ float Gs[TM + 1], Bs[TM + 1];
+  __shared__ uint8_t Ms[TM + 1];
   __shared__ float Cf[4][2][TM][TM];  // per wave: r(t,s) k_s.k_t (s < t), r(t,s) k_s.q_t (s <= t)
 
-  float ea, db;
-  param_load<GF, DT>(p.ga, hv, ea, db);
-
-  // token loads first (memory returns in issue order), then the state rows
-  u32x4 kq;
-  {
-    const int m = tid >> 4, e = (tid & 15) * 8;  // 16 bytes a thread, row m
-    const int t = m < TM ? m : m - TM;
-    const uint16_t* src = static_cast<const uint16_t*>(m < TM ? p.k : p.q);
-    kq = *reinterpret_cast<const u32x4*>(src + ((tok0 + min(t, T - 1)) * p.Hk + hk) * DK + e);
-    const bool keep = m < 2 * TM && t < T;
-    kq = u32x4{keep ? kq.x : 0u, keep ? kq.y : 0u, keep ? kq.z : 0u, keep ? kq.w : 0u};
-  }
-  constexpr int NVS = (TM * kVmRows + 255) / 256;
-  float vr[NVS];
-#pragma unroll
-  for (int j = 0; j < NVS; ++j) {
-    const int i = min(tid + 256 * j, TM * kVmRows - 1);
-    const int t = i / kVmRows, r = i % kVmRows;
-    vr[j] = IO<DT>::load1(p.v, ((tok0 + min(t, T - 1)) * p.Hv + hv) * p.Dv + min(dv0 + r, p.Dv - 1));
-  }
-  float gx = 0.0f, gy = 0.0f;
-  uint8_t mm = 1;
-  if (tid < TM) {
-    const int64_t tok = tok0 + min(tid, T - 1);
-    gate_load<GF, DT>(p.ga, tok * p.ga.ld + hv, gx, gy);
-    mm = p.mask != nullptr ? p.mask[tok] : kActive;
-  }
+  // The state rows are issued first, then every token load (all
+  // unconditional, with clamped addresses, and none used before the last is
+  // issued): loads complete in issue order, so one latency covers them all.
   const int rown = dv0 + 16 * wave + lr;
   const int64_t srow = ((static_cast<int64_t>(slot) * p.Hv + hv) * p.Dv + min(rown, p.Dv - 1)) * DK;
   const float* src = p.state_in != nullptr ? p.state_in + srow : kZeroRow;
   f32x4 x0[4], x1[4];
 #pragma unroll
   for (int s = 0; s < 4; ++s) {
-    x0[s] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(src + 32 * s + 4 * lg));
-    x1[s] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(src + 32 * s + 16 + 4 * lg));
+    x0[s] = __builtin_nontemporal_load((gbl_f32x4*)(src + 32 * s + 4 * lg));
+    x1[s] = __builtin_nontemporal_load((gbl_f32x4*)(src + 32 * s + 16 + 4 * lg));
+  }
+  float al, db;
+  param_load_raw<GF, DT>(p.ga, hv, al, db);
+
+  const int kq_m = tid >> 4, kq_e = (tid & 15) * 8;  // 16 bytes a thread, row kq_m
+  const int kq_t = kq_m < TM ? kq_m : kq_m - TM;
+  u32x4 kq;
+  {
+    const uint16_t* ks = static_cast<const uint16_t*>(kq_m < TM ? p.k : p.q);
+    kq = *reinterpret_cast<const u32x4*>(ks + ((tok0 + min(kq_t, T - 1)) * p.Hk + hk) * DK + kq_e);
+  }
+  constexpr int NVS = (TM * kVmRows + 255) / 256;
+  IO<DT>::raw1 vr[NVS];
+#pragma unroll
+  for (int j = 0; j < NVS; ++j) {
+    const int i = min(tid + 256 * j, TM * kVmRows - 1);
+    const int t = i / kVmRows, r = i % kVmRows;
+    vr[j] = IO<DT>::load1_raw(p.v, ((tok0 + min(t, T - 1)) * p.Hv + hv) * p.Dv + min(dv0 + r, p.Dv - 1));
+  }
+  // threads tid < TM keep token tid's gates and mask; the others load a
+  // valid token too and never use it
+  float gx, gy;
+  uint8_t mm;
+  {
+    const int64_t tok = tok0 + min(tid, T - 1);
+    gate_load<GF, DT>(p.ga, tok * p.ga.ld + hv, gx, gy);
+    const uint8_t* mp = p.mask != nullptr ? p.mask + tok : &kActive;
+    mm = *(gbl_u8*)mp;
   }
 
-  *reinterpret_cast<u32x4*>(&KQ[tid >> 4][(tid & 15) * 8]) = kq;
+  {
+    const bool keep = kq_m < 2 * TM && kq_t < T;  // zero rows past the k and q rows
+    *reinterpret_cast<u32x4*>(&KQ[kq_m][kq_e]) =
+        u32x4{keep ? kq.x : 0u, keep ? kq.y : 0u, keep ? kq.z : 0u, keep ? kq.w : 0u};
+  }
+  // every thread stores (no branch the v loads could be sunk into)
+  static_assert(TM * kVmRows % 256 == 0, "the v values fill whole passes of the workgroup");
 #pragma unroll
   for (int j = 0; j < NVS; ++j) {
     const int i = tid + 256 * j;
-    if (i < TM * kVmRows) Vs[i / kVmRows][i % kVmRows] = vr[j];
+    Vs[i / kVmRows][i % kVmRows] = IO<DT>::cvt1(vr[j]);
   }
-  if (tid < TM) {
+  {
+    // every thread transforms and stores (a use under a branch would have
+    // the gate loads sunk into it, behind the first wait)
+    const float ea = GF == GF_ANY && p.ga.mode == GDN_GATES_PRE ? 0.0f : exp_fast(al);
     float g, beta;
     gate_transform<GF>(p.ga.mode, gx, gy, ea, db, g, beta);
     const bool on = mm != 0 && tid < T;
-    Gs[tid] = on ? g : 1.0f;
-    Bs[tid] = on ? beta : 0.0f;
-    Ms[tid] = on ? 1 : 0;
+    const int slot_g = min(tid, TM);
+    Gs[slot_g] = on ? g : 1.0f;
+    Bs[slot_g] = on ? beta : 0.0f;
+    Ms[slot_g] = on ? 1 : 0;
   }
   __syncthreads();
 
@@ -728,11 +882,24 @@ int launch_verify_mfma(hipStream_t st, const RecParams& p, int64_t B) {
 
 template <int DK, int DT, int GF>
 int launch_pf(int kind, dim3 grid, dim3 block, hipStream_t st, const RecParams& p) {
+  if constexpr (GF != GF_ANY) {
+    // the serving step: every option fixed (see DecodeMode)
+    const bool lean = kind == K_DECODE && p.T == 1 && p.state_in != nullptr && p.state_out != nullptr &&
+                      p.y != nullptr && p.mask == nullptr && p.commit_len == nullptr && p.snapshots == nullptr;
+    if (lean && p.state_index != nullptr) {
+      hipLaunchKernelGGL((recurrent_kernel<DK, DT, GF, kDecodeLeanPooled>), grid, block, 0, st, p);
+      return gdn_host::check_launch("gdn_recurrent");
+    }
+    if (lean) {
+      hipLaunchKernelGGL((recurrent_kernel<DK, DT, GF, kDecodeLean>), grid, block, 0, st, p);
+      return gdn_host::check_launch("gdn_recurrent");
+    }
+  }
   if (kind == K_VERIFY && p.T <= 4) hipLaunchKernelGGL((verify_wy_kernel<DK, DT, GF, 4>), grid, block, 0, st, p);
   else if (kind == K_VERIFY)
     hipLaunchKernelGGL((verify_wy_kernel<DK, DT, GF, kVerifyMaxT>), grid, block, 0, st, p);
   else if (kind == K_TILE) hipLaunchKernelGGL((recurrent_tile_kernel<DK, DT, GF>), grid, block, 0, st, p);
-  else hipLaunchKernelGGL((recurrent_kernel<DK, DT, GF>), grid, block, 0, st, p);
+  else hipLaunchKernelGGL((recurrent_kernel<DK, DT, GF, kDecodeAny>), grid, block, 0, st, p);
   return gdn_host::check_launch("gdn_recurrent");
 }
 
@@ -826,6 +993,9 @@ int run_recurrent(const gdn_recurrent_args* a) {
   p.Hv = static_cast<int>(a->Hv);
   p.Dv = static_cast<int>(a->Dv);
   p.group = static_cast<int>(a->Hv / a->Hk);
+  // hv / group = (hv * ceil(2^31 / group)) >> 31 exactly while hv * group <= 2^31
+  // (hv < 2^16, and the decode kernel is only used for group < 2^15)
+  p.group_magic = static_cast<unsigned>(((1ull << 31) + p.group - 1) / p.group);
 
   int gf = GF_ANY;
   if (a->gate_mode == GDN_GATES_RAW && a->gate_dtype == a->qkv_dtype) {
@@ -842,20 +1012,32 @@ int run_recurrent(const gdn_recurrent_args* a) {
   const bool verify = a->state_out == nullptr && a->snapshots == nullptr && a->y != nullptr &&
                       a->cu_seqlens == nullptr && a->commit_len == nullptr && a->T >= 1 &&
                       a->T <= kVerifyMaxT;
-  const bool pf = a->T > 1 || a->cu_seqlens != nullptr;
+  // The decode kernel indexes in 32 bits: state rows (pool slots or B, times
+  // Hv*Dv), q/k/v/y elements and gate entries must stay below 2^31 (and the
+  // group below 2^15, for its division); larger launches take the tile
+  // kernel, whose steps are bit-identical.
+  const int64_t state_rows = (a->state_index != nullptr ? a->n_slots : a->B) * a->Hv * a->Dv;
+  const bool idx32 = state_rows < (int64_t{1} << 31) && a->B * a->Hv * a->Dv < (int64_t{1} << 31) &&
+                     a->B * a->Hk * a->Dk < (int64_t{1} << 31) && a->B * p.ga.ld < (int64_t{1} << 31) &&
+                     p.group < (1 << 15);
+  const bool pf = a->T > 1 || a->cu_seqlens != nullptr || !idx32;
   const int kind = verify ? K_VERIFY : (pf ? K_TILE : K_DECODE);
   // the tile and verify kernels assume workgroups of 4 waves (32 rows)
   const bool four = kind != K_DECODE;
+  // state rows per wave: 8 in the tile and verify kernels, 256/Dk in the
+  // decode kernel (Dk/4 lanes per row)
+  const int rows_per_wave = four ? 8 : static_cast<int>(256 / a->Dk);
   int waves = four ? 4 : 1;
   for (int w = 4; w >= 1 && !four; w >>= 1) {
-    const int64_t rows_per_wg = 8 * w;
+    const int64_t rows_per_wg = rows_per_wave * w;
     const int64_t wgs = a->B * a->Hv * ((a->Dv + rows_per_wg - 1) / rows_per_wg);
     if (wgs >= 1024 || w == 1) {
       waves = w;
       break;
     }
   }
-  const int rows_per_wg = 8 * waves;
+  const int rows_per_wg = rows_per_wave * waves;
+  p.wg_rows = rows_per_wg;
   dim3 block(64 * waves);
   dim3 grid(static_cast<unsigned>((a->Dv + rows_per_wg - 1) / rows_per_wg),
             static_cast<unsigned>(a->Hv), static_cast<unsigned>(a->B));

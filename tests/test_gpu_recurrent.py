@@ -264,6 +264,24 @@ def test_packed_ragged_rows():
     np.testing.assert_array_equal(S[2].cpu().numpy(), S0[2])
 
 
+@pytest.mark.parametrize("Dk,Dv", [(128, 128), (64, 64), (256, 256), (128, 96)])
+def test_decode_step_bitwise_equals_tile_step(Dk, Dv):
+    """The decode kernel (one token per row, Dk/4 lanes per state row) and the
+    multi-token kernel (8 lanes per row; taken here through the packed form
+    with one token per sequence) sum a row's dot products in one order, so
+    the same token gives bit-identical outputs and states."""
+    B = 5
+    d = draw(120 + Dk + Dv, B, 1, 2, 4, Dk, Dv)
+    t, r = to_torch(d, DEV)
+    y1, S1 = run_update(t)
+    assert_close(y1, S1, *oracle_update(r))
+    flat = lambda x: x.reshape(1, B, *x.shape[2:]).contiguous()
+    cu = torch.arange(B + 1, dtype=torch.int32)
+    y2, S2 = mx.gated_delta_update(flat(t["q"]), flat(t["k"]), flat(t["v"]), flat(t["a"]), flat(t["b"]),
+                                   t["A_log"], t["dt_bias"], t["state"], cu_seqlens=cu, chunked=False)
+    assert torch.equal(y2.reshape(y1.shape), y1) and torch.equal(S2, S1)
+
+
 def test_carried_state_many_steps():
     B, steps = 4, 40
     d = draw(14, B, steps, 16, 32, 128, 128)
