@@ -13,14 +13,19 @@ those rows are independent launches of the same layer:
 * the decode, verify and commit launches of the other rows
   (``prepare_recurrent``) are HBM-bound state streams.
 
-:class:`MixedStep` issues the prep on the caller's stream, records an event,
-issues the scan behind it, and runs the other launches on a second stream
-(default priority) that waits for that event, so the HBM-bound launches
-overlap the scan rather than the prep.  The caller's stream then waits for
-the second stream, so work issued after ``launch()`` sees every output.
-Every launch writes disjoint outputs (separate rows and states), so the
-order between the two streams does not change any result:
-``launch_serial()`` issues the same launches on one stream, bit-identically.
+:class:`MixedStep` has two schedules.  ``launch_serial()`` issues prep,
+scan and the other launches in order on the caller's stream.
+``launch_overlapped()`` issues the prep on the caller's stream, records an
+event, issues the scan behind it, and runs the other launches on a second
+stream (default priority) that waits for that event, so the HBM-bound
+launches overlap the scan rather than the prep; the caller's stream then
+waits for the second stream, so work issued after it sees every output.
+Every launch writes disjoint outputs (separate rows and states), so the two
+schedules give bit-identical results.
+
+``launch()`` takes the schedule chosen at construction, overlapped by
+default (the step of 1024 + 2560 + 7168 prefill tokens, 48 decode rows and
+16 verify rows: 0.338 ms overlapped, 0.354 ms on one stream).
 """
 
 from __future__ import annotations
@@ -39,22 +44,32 @@ class MixedStep:
 
     ``prefill``: a :class:`PreparedChunked` (the packed prefills), or None.
     ``others``: prepared recurrent launches (decode, verify, commit), issued
-    in order on the side stream.  ``side``: the second stream (created with
-    default priority when not given).
+    in order after the prefill (on the side stream when overlapped).
+    ``side``: the second stream of the overlapped schedule (created with
+    default priority when not given).  ``overlap``: whether ``launch()``
+    takes the overlapped schedule.
     """
 
     def __init__(self, prefill: Optional[PreparedChunked], others: Sequence[PreparedRecurrent],
-                 side: Optional[torch.cuda.Stream] = None):
+                 side: Optional[torch.cuda.Stream] = None, overlap: bool = True):
         self.prefill = prefill
         self.others = list(others)
         devs = {p.device for p in self.others} | ({prefill.device} if prefill is not None else set())
         if len(devs) != 1:
             raise ValueError("a mixed step runs on one device")
         self.device = devs.pop()
+        self.overlap = bool(overlap)
         self.side = side if side is not None else torch.cuda.Stream(self.device)
         self._prep_done = torch.cuda.Event()
 
     def launch(self, stream=None):
+        """Enqueues the step with the schedule chosen at construction."""
+        if self.overlap:
+            self.launch_overlapped(stream)
+        else:
+            self.launch_serial(stream)
+
+    def launch_overlapped(self, stream=None):
         """Enqueues the step: prep, then scan on ``stream`` (default: the
         current stream); the other launches on the side stream once the prep
         is done; ``stream`` waits for the side stream at the end."""

@@ -122,7 +122,7 @@ def test_mixed_step_two_streams():
     (tp, rp), (td, rd), (tv, rv) = (to_torch(x, DEV) for x in (pf, dec, ver))
     dec_state0 = td["state"].clone()
     step, plans = _build_step(cu, tp, td, tv, n_b)
-    step.launch()
+    step.launch_overlapped()
     torch.cuda.synchronize()
     two = [t.clone() for t in _outputs(plans)]
 
