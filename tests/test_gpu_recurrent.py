@@ -282,6 +282,56 @@ def test_decode_step_bitwise_equals_tile_step(Dk, Dv):
     assert torch.equal(y2.reshape(y1.shape), y1) and torch.equal(S2, S1)
 
 
+@pytest.mark.parametrize("param_dtype,mask_p", [("bf16", None), ("bf16", 0.5), ("f32", 0.5)])
+def test_decode_gate_formats_and_mask(param_dtype, mask_p):
+    """One-token steps through the decode kernel's lean body (bf16 A_log /
+    dt_bias: the all-bf16 gate format) and its general body (a mask), against
+    the oracle and bit-identical to the multi-token kernel on the same token."""
+    B = 6
+    d = draw(130 + (mask_p is not None), B, 1, 2, 4, 128, 128, mask_p=mask_p)
+    t, r = to_torch(d, DEV, param_dtype=param_dtype)
+    y, S = run_update(t)
+    assert_close(y, S, *oracle_update(r))
+    if mask_p is not None:
+        off = ~r["mask"][:, 0]
+        assert off.any() and (~off).any()
+        assert torch.equal(S[torch.tensor(off, device=DEV)], t["state"][torch.tensor(off, device=DEV)])
+    flat = lambda x: x.reshape(1, B, *x.shape[2:]).contiguous()
+    cu = torch.arange(B + 1, dtype=torch.int32)
+    m = None if t["mask"] is None else t["mask"].reshape(1, B)
+    y2, S2 = mx.gated_delta_update(flat(t["q"]), flat(t["k"]), flat(t["v"]), flat(t["a"]), flat(t["b"]),
+                                   t["A_log"], t["dt_bias"], t["state"], m, cu_seqlens=cu, chunked=False)
+    assert torch.equal(y2.reshape(y.shape), y) and torch.equal(S2, S)
+
+
+def test_decode_snapshot_commit_and_zero_state():
+    """The decode kernel's other one-token options: a verify with snapshots
+    (the snapshot is the stepped state, the input state is not written), a
+    commit of n in {-1, 0, 1} into a separate state, and no input state."""
+    B = 5
+    d = draw(140, B, 1, 2, 4, 128, 128)
+    t, r = to_torch(d, DEV)
+    before = t["state"].clone()
+    y_ref, S_ref = oracle_update(r)
+    y, snaps = mx.gated_delta_verify(t["q"], t["k"], t["v"], t["a"], t["b"], t["A_log"], t["dt_bias"],
+                                     t["state"], snapshots=True)
+    assert torch.equal(t["state"], before)
+    assert_close(y, snaps[:, 0], y_ref, S_ref)
+    n = [1, 0, -1, 1, 0]
+    out = torch.full_like(t["state"], 7.0)
+    S_c = mx.gated_delta_commit(t["k"], t["v"], t["a"], t["b"], t["A_log"], t["dt_bias"], t["state"], n,
+                                state_out=out)
+    for b_, nb in enumerate(n):
+        if nb == 1:
+            assert head_errs_state(S_c[b_:b_ + 1].cpu().numpy(), S_ref[b_:b_ + 1]).max() <= STATE_TOL
+        else:  # 0 keeps the state; a negative n copies it unchanged into a separate state_out
+            assert torch.equal(S_c[b_], before[b_])
+    d0 = draw(141, B, 1, 2, 4, 128, 128, state=False)
+    t0, r0 = to_torch(d0, DEV, dtype="f16", gate_dtype="f16")
+    y0, S0 = run_update(t0)
+    assert_close(y0, S0, *oracle_update(r0))
+
+
 def test_carried_state_many_steps():
     B, steps = 4, 40
     d = draw(14, B, steps, 16, 32, 128, 128)
