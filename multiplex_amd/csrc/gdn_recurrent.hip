@@ -349,31 +349,35 @@ __global__ __launch_bounds__(256) void recurrent_kernel(const RecParams p) {
 }
 
 // Multi-token body (verify, commit, packed rows): the workgroup (always 4
-// waves, 32 state rows) stages a tile of kTile tokens -- k and q as fp32, the
+// waves, 32 state rows) stages a tile of TILE tokens -- k and q as fp32, the
 // transformed gates, the mask and the v values of its rows -- in LDS, then
 // every wave walks the tile from LDS.  The first tile's global loads are
 // issued right behind the state stream, so both arrive within one latency.
-constexpr int kTile = 16;
+// TILE is 4, 8 or 16, the smallest that holds the launch's tokens per row
+// (16 for longer or packed rows): a larger tile than the tokens would re-read
+// the last token into the unused slots.
+constexpr int kTileMax = 16;
 constexpr int kTileThreads = 256;
 constexpr int kTileRows = kTileThreads / kLanesPerRow;  // 32
 
-template <int DK, int DT, int GF>
+template <int DK, int DT, int GF, int TILE>
 __global__ __launch_bounds__(kTileThreads) void recurrent_tile_kernel(const RecParams p) {
   constexpr int EPL = DK / kLanesPerRow;
   constexpr int NV = EPL / 4;
-  constexpr int KV4 = kTile * DK / 4 / kTileThreads;  // float4 of k (and q) per thread
-  constexpr int VV = kTile * kTileRows / kTileThreads;  // v values per thread
-  static_assert(KV4 >= 1 && VV >= 1, "tile must cover the workgroup");
+  constexpr int NK = TILE * DK / 4;                             // float4 of k (and q) in the tile
+  constexpr int KV4 = (NK + kTileThreads - 1) / kTileThreads;   // ... per thread
+  constexpr int NVV = TILE * kTileRows;                         // v values in the tile
+  constexpr int VV = (NVV + kTileThreads - 1) / kTileThreads;   // ... per thread
   const RowCtx c = row_ctx<DK>(p);
   if (c.skip) return;  // uniform: a workgroup serves one row, before any barrier
   const int tid = threadIdx.x;
   const int dv0 = blockIdx.x * kTileRows;
 
-  __shared__ __align__(16) float Kt[kTile][DK];
-  __shared__ __align__(16) float Qt[kTile][DK];
-  __shared__ float Vt[kTile][kTileRows];
-  __shared__ float Gt[kTile], Bt[kTile];
-  __shared__ uint8_t Mt[kTile];
+  __shared__ __align__(16) float Kt[TILE][DK];
+  __shared__ __align__(16) float Qt[TILE][DK];
+  __shared__ float Vt[TILE][kTileRows];
+  __shared__ float Gt[TILE], Bt[TILE];
+  __shared__ uint8_t Mt[TILE];
 
   // The state load is issued first, then the parameters' and the first
   // tile's loads: loads complete in issue order, so the first use of a tile
@@ -396,7 +400,7 @@ __global__ __launch_bounds__(kTileThreads) void recurrent_tile_kernel(const RecP
   auto issue_tile = [&](int t0, int n) {
 #pragma unroll
     for (int it = 0; it < KV4; ++it) {
-      const int i = tid + kTileThreads * it;
+      const int i = min(tid + kTileThreads * it, NK - 1);
       const int j = i / (DK / 4), e = (i % (DK / 4)) * 4;
       const int64_t off = ((c.tok0 + t0 + min(j, n - 1)) * p.Hk + c.hk) * DK + e;
       kr[it] = IO<DT>::load4_raw(p.k, off);
@@ -404,12 +408,12 @@ __global__ __launch_bounds__(kTileThreads) void recurrent_tile_kernel(const RecP
     }
 #pragma unroll
     for (int it = 0; it < VV; ++it) {
-      const int i = tid + kTileThreads * it;
+      const int i = min(tid + kTileThreads * it, NVV - 1);
       const int j = i / kTileRows, r = i % kTileRows;
       const int64_t tok = c.tok0 + t0 + min(j, n - 1);
       vr[it] = IO<DT>::load1_raw(p.v, (tok * p.Hv + c.hv) * p.Dv + min(dv0 + r, p.Dv - 1));
     }
-    // threads tid < kTile keep token tid's gates and mask; the others load a
+    // threads tid < TILE keep token tid's gates and mask; the others load a
     // valid token too (no branch) and never use it
     {
       const int64_t tok = c.tok0 + t0 + min(tid, n - 1);
@@ -422,16 +426,18 @@ __global__ __launch_bounds__(kTileThreads) void recurrent_tile_kernel(const RecP
 #pragma unroll
     for (int it = 0; it < KV4; ++it) {
       const int i = tid + kTileThreads * it;
-      const int j = i / (DK / 4), e = (i % (DK / 4)) * 4;
-      *reinterpret_cast<f32x4*>(&Kt[j][e]) = IO<DT>::cvt4(kr[it]);
-      if (c.want_y) *reinterpret_cast<f32x4*>(&Qt[j][e]) = IO<DT>::cvt4(qr[it]);
+      if (i < NK) {
+        const int j = i / (DK / 4), e = (i % (DK / 4)) * 4;
+        *reinterpret_cast<f32x4*>(&Kt[j][e]) = IO<DT>::cvt4(kr[it]);
+        if (c.want_y) *reinterpret_cast<f32x4*>(&Qt[j][e]) = IO<DT>::cvt4(qr[it]);
+      }
     }
 #pragma unroll
     for (int it = 0; it < VV; ++it) {
       const int i = tid + kTileThreads * it;
-      Vt[i / kTileRows][i % kTileRows] = IO<DT>::cvt1(vr[it]);
+      if (i < NVV) Vt[i / kTileRows][i % kTileRows] = IO<DT>::cvt1(vr[it]);
     }
-    if (tid < kTile) {
+    if (tid < TILE) {
       float g, beta;
       gate_transform<GF>(p.ga.mode, gx, gy, ea, db, g, beta);
       Gt[tid] = g;
@@ -440,12 +446,12 @@ __global__ __launch_bounds__(kTileThreads) void recurrent_tile_kernel(const RecP
     }
   };
 
-  if (c.steps > 0) issue_tile(0, min(kTile, c.steps));
+  if (c.steps > 0) issue_tile(0, min(TILE, c.steps));
   ea = GF == GF_ANY && p.ga.mode == GDN_GATES_PRE ? 0.0f : exp_fast(al);
   if (c.write_state && c.commit == 0 && c.row_ok) store_row<EPL>(p.state_out + c.srow, c.sub, s);
 
-  for (int t0 = 0; t0 < c.steps; t0 += kTile) {
-    const int n = min(kTile, c.steps - t0);
+  for (int t0 = 0; t0 < c.steps; t0 += TILE) {
+    const int n = min(TILE, c.steps - t0);
     if (t0 > 0) {
       __syncthreads();  // the previous tile is consumed
       issue_tile(t0, n);
@@ -915,7 +921,11 @@ int launch_pf(int kind, dim3 grid, dim3 block, hipStream_t st, const RecParams& 
   if (kind == K_VERIFY && p.T <= 4) hipLaunchKernelGGL((verify_wy_kernel<DK, DT, GF, 4>), grid, block, 0, st, p);
   else if (kind == K_VERIFY)
     hipLaunchKernelGGL((verify_wy_kernel<DK, DT, GF, kVerifyMaxT>), grid, block, 0, st, p);
-  else if (kind == K_TILE) hipLaunchKernelGGL((recurrent_tile_kernel<DK, DT, GF>), grid, block, 0, st, p);
+  else if (kind == K_TILE && p.cu_seqlens == nullptr && p.T <= 4)
+    hipLaunchKernelGGL((recurrent_tile_kernel<DK, DT, GF, 4>), grid, block, 0, st, p);
+  else if (kind == K_TILE && p.cu_seqlens == nullptr && p.T <= 8)
+    hipLaunchKernelGGL((recurrent_tile_kernel<DK, DT, GF, 8>), grid, block, 0, st, p);
+  else if (kind == K_TILE) hipLaunchKernelGGL((recurrent_tile_kernel<DK, DT, GF, kTileMax>), grid, block, 0, st, p);
   else hipLaunchKernelGGL((recurrent_kernel<DK, DT, GF, kDecodeAny>), grid, block, 0, st, p);
   return gdn_host::check_launch("gdn_recurrent");
 }
