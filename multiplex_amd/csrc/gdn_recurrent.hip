@@ -254,8 +254,9 @@ __device__ __forceinline__ void step_row(float (&s)[EPL], const float (&k)[EPL],
 // MODE: kDecodeAny takes every option at run time.  kDecodeLean and
 // kDecodeLeanPooled are the serving step with every option fixed -- T = 1,
 // state_in and state_out given, y wanted, no mask, commit lengths or
-// snapshots, raw gates of a typed format -- without (with) a pool-slot
-// table: the same code with those checks removed, so the same results.
+// snapshots, raw gates of a typed format (with 16-bit gates and v: 4-byte
+// aligned, even gate stride, Hv and Dv) -- without (with) a pool-slot table:
+// the same arithmetic with those checks removed, so the same results.
 enum DecodeMode { kDecodeAny = 0, kDecodeLean = 1, kDecodeLeanPooled = 2 };
 
 template <int DK, int DT, int GF, int MODE>
@@ -286,10 +287,6 @@ __global__ __launch_bounds__(256) void recurrent_kernel(const RecParams p) {
   }
   float al, db;
   param_load_raw<GF, DT>(p.ga, hv, al, db);
-  // the output pointer is read with the other parameters, not at its store
-  // (a parameter read there would be one more wait at the end of every wave)
-  void* yp = p.y;
-  asm volatile("" : "+s"(yp));
 
   // T is 0 or 1 here: the token of row `row` is token `row`.  A negative
   // commit length skips the row: in place it is not written at all; into a
@@ -315,8 +312,28 @@ __global__ __launch_bounds__(256) void recurrent_kernel(const RecParams p) {
     const unsigned kq = (static_cast<unsigned>(row) * p.Hk + hk) * DK + sub * 4;
     kr = IO<DT>::load4_raw(p.k, kq);
     qr = IO<DT>::load4_raw(want_y ? p.q : p.k, kq);  // k stands in when no output is wanted
-    vr = IO<DT>::load1_raw(p.v, (static_cast<unsigned>(row) * p.Hv + hv) * p.Dv + dv_c);
-    gate_load<GF, DT>(p.ga, static_cast<unsigned>(row) * static_cast<unsigned>(p.ga.ld) + hv, gx, gy);
+    const unsigned gi = static_cast<unsigned>(row) * static_cast<unsigned>(p.ga.ld) + hv;
+    if constexpr (lean && DT != GDN_DTYPE_F32) {
+      // The gates and the v of the wave's two rows are wave-uniform 16-bit
+      // values: each is read with a scalar load of the aligned dword holding
+      // it (the host takes this body only when the other half of each dword
+      // is inside the same tensor: 4-byte aligned pointers, even gate stride,
+      // Hv and Dv), which keeps three vector loads off every wave.
+      static_assert(LPR == 32, "two state rows per wave");
+      const int wave0 = static_cast<int>(blockIdx.x) * p.wg_rows +
+                        2 * static_cast<int>(__builtin_amdgcn_readfirstlane(threadIdx.x >> 6));
+      const int wdv = min(wave0, p.Dv - 2);
+      const uint32_t vw =
+          static_cast<const uint32_t*>(p.v)[((static_cast<unsigned>(row) * p.Hv + hv) * p.Dv + wdv) >> 1];
+      const uint32_t aw = static_cast<const uint32_t*>(p.ga.gx)[gi >> 1];
+      const uint32_t bw = static_cast<const uint32_t*>(p.ga.gy)[gi >> 1];
+      vr = static_cast<uint16_t>((threadIdx.x & 32) ? vw >> 16 : vw);
+      gx = IO<DT>::cvt1(static_cast<uint16_t>((gi & 1) ? aw >> 16 : aw));
+      gy = IO<DT>::cvt1(static_cast<uint16_t>((gi & 1) ? bw >> 16 : bw));
+    } else {
+      vr = IO<DT>::load1_raw(p.v, (static_cast<unsigned>(row) * p.Hv + hv) * p.Dv + dv_c);
+      gate_load<GF, DT>(p.ga, gi, gx, gy);
+    }
     if (lean) {
       m = 1;
     } else {
@@ -324,6 +341,13 @@ __global__ __launch_bounds__(256) void recurrent_kernel(const RecParams p) {
       m = *(gbl_u8*)mp;
     }
   }
+  // the output pointer is read here, with the loads in flight, not at its
+  // store (a parameter read there would be one more wait at the end of every
+  // wave); the empty asm pins it, and comes after the loads above because
+  // the compiler counts it as a possible memory write, after which no load
+  // may become a scalar load
+  void* yp = p.y;
+  asm volatile("" : "+s"(yp));
   if (!lean && write_state && commit == 0 && row_ok)
     store_row<4, LPR>(p.state_out + static_cast<size_t>(srow) * DK, sub, s);
   if (!step) return;
@@ -907,8 +931,12 @@ template <int DK, int DT, int GF>
 int launch_pf(int kind, dim3 grid, dim3 block, hipStream_t st, const RecParams& p) {
   if constexpr (GF != GF_ANY) {
     // the serving step: every option fixed (see DecodeMode)
+    const bool dwords = DT == GDN_DTYPE_F32 ||
+                        (gdn_host::aligned(p.v, 4) && gdn_host::aligned(p.ga.gx, 4) && gdn_host::aligned(p.ga.gy, 4) &&
+                         p.ga.ld % 2 == 0 && p.Hv % 2 == 0 && p.Dv % 2 == 0);
     const bool lean = kind == K_DECODE && p.T == 1 && p.state_in != nullptr && p.state_out != nullptr &&
-                      p.y != nullptr && p.mask == nullptr && p.commit_len == nullptr && p.snapshots == nullptr;
+                      p.y != nullptr && p.mask == nullptr && p.commit_len == nullptr && p.snapshots == nullptr &&
+                      dwords;
     if (lean && p.state_index != nullptr) {
       hipLaunchKernelGGL((recurrent_kernel<DK, DT, GF, kDecodeLeanPooled>), grid, block, 0, st, p);
       return gdn_host::check_launch("gdn_recurrent");
