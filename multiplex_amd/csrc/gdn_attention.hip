@@ -223,6 +223,10 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(const AttnParams p) {
   uint16_t(*Vs)[VP] = reinterpret_cast<uint16_t(*)[VP]>(smem + KB * KP * 2);
 
   // the next block, in flight: chunk c = tid + 256 i is row c / (D/8), columns (c % (D/8)) * 8 ..
+  // The cache is read with nontemporal loads: each step streams it once, and at
+  // decode sizes (1 GB at B=64 and 4096 positions) it cannot stay in the
+  // last-level cache, whose allocation on every read cost 15% (180.4 against
+  // 152.8 us at B=64).
   u32x4 kr[CPT], vr[CPT];
   const int64_t head_base = (static_cast<int64_t>(b) * p.Hkv + hkv) * p.cap * D;
   auto load_blk = [&](int kb) {
@@ -232,8 +236,8 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(const AttnParams p) {
       const int row = c / (D / 8), col = (c % (D / 8)) * 8;
       const int key = kb + row;
       const int64_t off = head_base + static_cast<int64_t>(min(key, k_hi - 1)) * D + col;  // in bounds: k_hi <= cap
-      kr[i] = *reinterpret_cast<const u32x4*>(p.kc + off);
-      vr[i] = *reinterpret_cast<const u32x4*>(p.vc + off);
+      kr[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p.kc + off));
+      vr[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p.vc + off));
     }
   };
   auto store_blk = [&](int kb) {
