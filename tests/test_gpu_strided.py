@@ -92,6 +92,23 @@ def test_recurrent_kernels_read_gate_slices(T):
     assert torch.equal(plan.outputs[0], y2)
 
 
+def test_decode_odd_gate_offsets_take_the_general_body():
+    """One-token gates at odd element offsets and an odd row stride (2-byte
+    aligned, so the lean decode body's dword reads of them are not taken):
+    the general body gives the results of the lean one, bit for bit."""
+    B = 3
+    g = torch.Generator().manual_seed(21)
+    buf = torch.randn(B, 1, 2 * Hv + 3, generator=g).to(torch.bfloat16).to(DEV)  # odd width
+    a, b = buf[..., 1:1 + Hv], buf[..., 1 + Hv:1 + 2 * Hv]  # odd offsets
+    assert a.data_ptr() % 4 == 2 and b.stride(1) % 2 == 1
+    qkv, _, _, _ = fused(B, 1, 22)
+    q, k, v = qkv_heads(qkv)
+    _, A_log, dt_bias, state = params(23)
+    y1, s1 = mx.gated_delta_update(q, k, v, a, b, A_log, dt_bias, state)
+    y2, s2 = mx.gated_delta_update(q, k, v, a.contiguous(), b.contiguous(), A_log, dt_bias, state)
+    assert torch.equal(y1, y2) and torch.equal(s1, s2)
+
+
 def test_chunked_kernel_reads_gate_slices():
     T = 200
     qkv, _, a, b = fused(1, T, 20)
