@@ -227,10 +227,9 @@ __device__ __forceinline__ void gate_load(const GateArgs& ga, int64_t gi, float&
   }
 }
 
-// Per-head parameters (raw mode): exp(A_log[hv]) and dt_bias[hv].
-// The loads of param_load without the exponential: A_log[hv] (0 for
-// pre-transformed gates) and dt_bias[hv].  A caller that issues more loads
-// after these applies expf(al) at its use, so nothing waits here.
+// Per-head parameters (raw mode): A_log[hv] (0 for pre-transformed gates)
+// and dt_bias[hv], loads only.  The caller applies exp(A_log) at its use, so
+// nothing waits here for the loads while it issues more.
 template <int GF, int DT>
 __device__ __forceinline__ void param_load_raw(const GateArgs& ga, int hv, float& al, float& db) {
   if (GF == GF_ANY && ga.mode == GDN_GATES_PRE) {  // typed formats are raw gates
@@ -248,13 +247,6 @@ __device__ __forceinline__ void param_load_raw(const GateArgs& ga, int hv, float
     al = IO<DT>::load1(ga.A_log, hv);
     db = IO<DT>::load1(ga.dt_bias, hv);
   }
-}
-
-template <int GF, int DT>
-__device__ __forceinline__ void param_load(const GateArgs& ga, int hv, float& ea, float& db) {
-  float al;
-  param_load_raw<GF, DT>(ga, hv, al, db);
-  ea = GF == GF_ANY && ga.mode == GDN_GATES_PRE ? 0.0f : exp_fast(al);
 }
 
 // g = exp(-exp(A_log) softplus(a + dt_bias)), beta = sigmoid(b)  (raw mode).

@@ -75,43 +75,8 @@ __device__ __forceinline__ void store_row(float* dst, int sub, const float (&s)[
   }
 }
 
-// Inputs of one token for the lanes of one state row (raw gate inputs; the
-// transform runs after the loads have been issued).
-template <int EPL>
-struct TokenIn {
-  float k[EPL];
-  float q[EPL];
-  float v, gx, gy;
-  uint8_t m;
-};
-
-// q is read from `qp`: the kernel passes k there when no output is wanted,
-// so the load stays unconditional and its value is never used.
-template <int DK, int DT, int GF, int LPR>
-__device__ __forceinline__ void load_token(const RecParams& p, const void* qp, int64_t tok, int hv, int hk,
-                                           int dv_c, int sub, TokenIn<DK / LPR>& in) {
-  constexpr int NV = DK / LPR / 4;
-  const uint8_t* mp = p.mask != nullptr ? p.mask + tok : &kActive;
-  in.m = *(gbl_u8*)mp;
-  gate_load<GF, DT>(p.ga, tok * p.ga.ld + hv, in.gx, in.gy);
-  const int64_t kq = (tok * p.Hk + hk) * DK + sub * 4;
-#pragma unroll
-  for (int i = 0; i < NV; ++i) {
-    const f32x4 x = IO<DT>::load4(p.k, kq + i * 4 * LPR);
-    const f32x4 z = IO<DT>::load4(qp, kq + i * 4 * LPR);
-    in.k[4 * i] = x.x;
-    in.k[4 * i + 1] = x.y;
-    in.k[4 * i + 2] = x.z;
-    in.k[4 * i + 3] = x.w;
-    in.q[4 * i] = z.x;
-    in.q[4 * i + 1] = z.y;
-    in.q[4 * i + 2] = z.z;
-    in.q[4 * i + 3] = z.w;
-  }
-  in.v = IO<DT>::load1(p.v, (tok * p.Hv + hv) * p.Dv + dv_c);
-}
-
-// Shared preamble of both kernels: row / head / sequence bookkeeping.
+// Shared preamble of the multi-token kernels: row / head / sequence
+// bookkeeping (8 lanes per state row).
 struct RowCtx {
   int sub, dv, dv_c, hv, hk, row, L, commit, steps;
   bool row_ok, write_state, want_y;
@@ -119,11 +84,11 @@ struct RowCtx {
   int64_t tok0, srow, srow_c;
 };
 
-template <int DK, int LPR = kLanesPerRow>
+template <int DK>
 __device__ __forceinline__ RowCtx row_ctx(const RecParams& p) {
   RowCtx c;
-  c.sub = threadIdx.x & (LPR - 1);
-  c.dv = blockIdx.x * (blockDim.x / LPR) + threadIdx.x / LPR;
+  c.sub = threadIdx.x & (kLanesPerRow - 1);
+  c.dv = blockIdx.x * (blockDim.x / kLanesPerRow) + threadIdx.x / kLanesPerRow;
   c.row_ok = c.dv < p.Dv;
   c.dv_c = c.row_ok ? c.dv : p.Dv - 1;  // loads use a valid row; stores check row_ok
   c.hv = blockIdx.y;
@@ -165,13 +130,13 @@ __device__ __forceinline__ RowCtx row_ctx(const RecParams& p) {
   return c;
 }
 
-template <int DK, int LPR = kLanesPerRow>
-__device__ __forceinline__ void load_state(const RecParams& p, const RowCtx& c, float (&s)[DK / LPR]) {
-  constexpr int NV = DK / LPR / 4;
+template <int DK>
+__device__ __forceinline__ void load_state(const RecParams& p, const RowCtx& c, float (&s)[DK / kLanesPerRow]) {
+  constexpr int NV = DK / kLanesPerRow / 4;
   const float* src = p.state_in != nullptr ? p.state_in + c.srow_c : kZeroRow;
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
-    const f32x4 x = __builtin_nontemporal_load((gbl_f32x4*)(src + i * 4 * LPR + c.sub * 4));
+    const f32x4 x = __builtin_nontemporal_load((gbl_f32x4*)(src + i * 4 * kLanesPerRow + c.sub * 4));
     s[4 * i] = x.x;
     s[4 * i + 1] = x.y;
     s[4 * i + 2] = x.z;
