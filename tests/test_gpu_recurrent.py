@@ -282,6 +282,17 @@ def test_decode_step_bitwise_equals_tile_step(Dk, Dv):
     assert torch.equal(y2.reshape(y1.shape), y1) and torch.equal(S2, S1)
 
 
+@pytest.mark.parametrize("Hk,Hv", [(4, 4), (2, 6), (3, 15)])
+def test_decode_head_groups(Hk, Hv):
+    """One-token steps with 1, 3 and 5 v-heads per k-head (the decode kernel
+    finds a head's k-head by a multiply and shift); an odd Hv takes the
+    general body (its gates are not read as dwords)."""
+    d = draw(150 + Hv, 3, 1, Hk, Hv, 128, 128)
+    t, r = to_torch(d, DEV)
+    y, S = run_update(t)
+    assert_close(y, S, *oracle_update(r))
+
+
 @pytest.mark.parametrize("param_dtype,mask_p", [("bf16", None), ("bf16", 0.5), ("f32", 0.5)])
 def test_decode_gate_formats_and_mask(param_dtype, mask_p):
     """One-token steps through the decode kernel's lean body (bf16 A_log /
