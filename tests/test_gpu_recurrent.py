@@ -42,7 +42,7 @@ def assert_close(y, S, y_ref, S_ref, y_tol=Y_TOL, s_tol=STATE_TOL):
 
 
 @pytest.mark.parametrize("dtype", ["bf16", "f16", "f32"])
-@pytest.mark.parametrize("Dk,Dv", [(128, 128), (64, 64), (256, 256), (128, 96)])
+@pytest.mark.parametrize("Dk,Dv", [(128, 128), (64, 64), (256, 256), (128, 96), (128, 97), (64, 33)])
 def test_decode_matches_oracle(dtype, Dk, Dv):
     d = draw(100 + Dk + Dv, 3, 1, 2, 4, Dk, Dv)
     t, r = to_torch(d, DEV, dtype=dtype, gate_dtype=dtype)
@@ -264,7 +264,7 @@ def test_packed_ragged_rows():
     np.testing.assert_array_equal(S[2].cpu().numpy(), S0[2])
 
 
-@pytest.mark.parametrize("Dk,Dv", [(128, 128), (64, 64), (256, 256), (128, 96)])
+@pytest.mark.parametrize("Dk,Dv", [(128, 128), (64, 64), (256, 256), (128, 96), (128, 97)])
 def test_decode_step_bitwise_equals_tile_step(Dk, Dv):
     """The decode kernel (one token per row, Dk/4 lanes per state row) and the
     multi-token kernel (8 lanes per row; taken here through the packed form
