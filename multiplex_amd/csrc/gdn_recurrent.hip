@@ -41,6 +41,7 @@ __device__ const uint8_t kActive = 1;
 // scalar-load counter, so the gate parameters' scalar loads would wait for it.
 typedef __attribute__((address_space(1))) const f32x4 gbl_f32x4;
 typedef __attribute__((address_space(1))) const uint8_t gbl_u8;
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 struct RecParams {
   // the fields the decode kernel reads come first (two 64-byte parameter loads)
@@ -269,14 +270,23 @@ __global__ __launch_bounds__(256) void recurrent_kernel(const RecParams p) {
   const bool step = lean || (L > 0 && (want_y || snaps || (write_state && commit > 0)));
   const unsigned srow = srow_c + (dv - dv_c);  // the row the stores address (row_ok)
 
+  // With two state rows per wave (Dk = 128) both rows read the same k and q:
+  // one load instruction brings k to the low half-wave and q to the high one
+  // (kq_merged), and a permlane32 swap of each dword then hands every lane
+  // both, when they are used.
+  constexpr bool kq_merged = LPR == 32 && DT != GDN_DTYPE_F32;
   typename IO<DT>::raw4 kr = {}, qr = {};
   typename IO<DT>::raw1 vr = {};
   float gx = 0.0f, gy = 0.0f;
   uint8_t m = 0;
   if (step) {
     const unsigned kq = (static_cast<unsigned>(row) * p.Hk + hk) * DK + sub * 4;
-    kr = IO<DT>::load4_raw(p.k, kq);
-    qr = IO<DT>::load4_raw(want_y ? p.q : p.k, kq);  // k stands in when no output is wanted
+    if constexpr (kq_merged) {
+      kr = IO<DT>::load4_raw((threadIdx.x & 32) && want_y ? p.q : p.k, kq);
+    } else {
+      kr = IO<DT>::load4_raw(p.k, kq);
+      qr = IO<DT>::load4_raw(want_y ? p.q : p.k, kq);  // k stands in when no output is wanted
+    }
     const unsigned gi = static_cast<unsigned>(row) * static_cast<unsigned>(p.ga.ld) + hv;
     if constexpr (lean && DT != GDN_DTYPE_F32) {
       // The gates and the v of the wave's two rows are wave-uniform 16-bit
@@ -319,6 +329,14 @@ __global__ __launch_bounds__(256) void recurrent_kernel(const RecParams p) {
 
   float yv = 0.0f;
   if (m != 0) {
+    if constexpr (kq_merged) {
+      // uniform here (step and m are per batch row), so every lane takes part
+      const u32x2 w = __builtin_bit_cast(u32x2, kr);
+      const auto lo = __builtin_amdgcn_permlane32_swap(w.x, w.x, false, false);
+      const auto hi = __builtin_amdgcn_permlane32_swap(w.y, w.y, false, false);
+      kr = __builtin_bit_cast(typename IO<DT>::raw4, u32x2{lo[0], hi[0]});
+      qr = __builtin_bit_cast(typename IO<DT>::raw4, u32x2{lo[1], hi[1]});
+    }
     const float ea = GF == GF_ANY && p.ga.mode == GDN_GATES_PRE ? 0.0f : exp_fast(al);
     float g, beta;
     gate_transform<GF>(p.ga.mode, gx, gy, ea, db, g, beta);
@@ -669,7 +687,6 @@ __global__ __launch_bounds__(kTileThreads) void verify_wy_kernel(const RecParams
 constexpr int kVmRows = 64;  // state rows per workgroup, 16 per wave
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ f32x4 mfma_bf16(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);

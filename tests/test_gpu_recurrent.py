@@ -429,6 +429,37 @@ def test_commit_verify_is_commit_then_verify(Tp, T):
 
 
 
+@pytest.mark.parametrize("T,Dv,gate_dtype,param_dtype", [(2, 128, "bf16", "f32"), (4, 96, "bf16", "bf16"),
+                                                         (5, 128, "f32", "f32"), (8, 80, "bf16", "f32")])
+def test_ragged_commit_matches_oracle(T, Dv, gate_dtype, param_dtype):
+    """Commits of 2-8 tokens: ragged n (T, 0, negative, 1, past T, T - 1)
+    with a mask, Dv not a multiple of the 32-row workgroup, the typed and the
+    runtime gate formats; into a fresh state, in place, into pool slots, and
+    from no input state."""
+    B = 6
+    d = draw(300 + 10 * T + Dv, B, T, 2, 4, 128, Dv, mask_p=0.25)
+    t, r = to_torch(d, DEV, gate_dtype=gate_dtype, param_dtype=param_dtype)
+    g, beta = gdn.compute_g(r["A_log"], r["a"], r["dt_bias"]), gdn.compute_beta(r["b"])
+    n = np.array([T, 0, -1, 1, T + 3, T - 1], dtype=np.int32)
+    args = (t["k"], t["v"], t["a"], t["b"], t["A_log"], t["dt_bias"])
+    S = mx.gated_delta_commit(*args, t["state"], torch.tensor(n), t["mask"])
+    S_ref = gdn.commit(r["q"], r["k"], r["v"], g, beta, r["state"], np.clip(n, 0, T), r["mask"])
+    assert head_errs_state(S.cpu().numpy(), S_ref).max() <= STATE_TOL
+    assert torch.equal(S[1], t["state"][1]) and torch.equal(S[2], t["state"][2])
+    st = t["state"].clone()
+    mx.gated_delta_commit(*args, st, torch.tensor(n), t["mask"], state_out=st)
+    assert torch.equal(st, S)
+    idx = torch.tensor([3, 0, 5, 1, 7, 2], dtype=torch.int32, device=DEV)
+    pool = torch.zeros(8, *t["state"].shape[1:], device=DEV)
+    pool[idx.long()] = t["state"]
+    mx.gated_delta_commit(*args, pool, torch.tensor(n), t["mask"], state_index=idx)
+    assert torch.equal(pool[idx.long()], S) and not pool[[4, 6]].any()
+    S0 = mx.gated_delta_commit(*args, None, torch.tensor(n), t["mask"])
+    S0_ref = gdn.commit(r["q"], r["k"], r["v"], g, beta, None, np.clip(n, 0, T), r["mask"])
+    assert head_errs_state(S0.cpu().numpy()[[0, 3, 4, 5]], S0_ref[[0, 3, 4, 5]]).max() <= STATE_TOL
+    assert not S0[[1, 2]].any()
+
+
 def test_skipped_commit_row_into_a_fresh_state():
     """A negative commit length skips the row; with no ``state_out`` (a
     fresh output tensor) the row is the unchanged input state, not
