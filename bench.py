@@ -328,7 +328,10 @@ def bench_mixed(torch, mx, dev, timer, iters=50):
                                  ver["state"], y=False, commit_len=n_b, state_out=torch.empty_like(ver["state"]))
     pplan = mx.prepare_chunked(pf["q"], pf["k"], pf["v"], pf["a"], pf["b"], pf["A_log"], pf["dt_bias"], pf_state,
                                cu_seqlens=cu, workspace=ws, state_out=torch.empty_like(pf_state))
-    step = mx.MixedStep(pplan, [dplan, vplan, cplan])
+    # verify and commit first, the decode last: with the decode first the
+    # step took about 3 us longer (332.5 against 329.4 us, four alternating
+    # runs); the launches are independent, so the outputs are the same
+    step = mx.MixedStep(pplan, [vplan, cplan, dplan])
 
     for _ in range(3):
         step.launch()
