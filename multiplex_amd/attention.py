@@ -140,6 +140,42 @@ def attn_qk(qg: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor, q_norm_w
     return q_out
 
 
+def _check_attn_fwd(q, k_cache, v_cache, pos0, kv_len_max, gate, out):
+    """Shapes, dtypes and layouts of :func:`attn_fwd`'s arguments, checked
+    before anything is launched (a mismatch would otherwise read outside
+    the caches).  Returns ``(B, T, Hq, D, Hkv, cap, gate token stride)``."""
+    _bf16(q, "q")
+    if q.dim() != 4:
+        raise ValueError(f"q must be [B, T, Hq, D] (got {tuple(q.shape)})")
+    B, T, Hq, D = q.shape
+    for c, n in ((k_cache, "k_cache"), (v_cache, "v_cache")):
+        _bf16(c, n)
+        if c.dim() != 4 or not c.is_contiguous():
+            raise ValueError(f"{n} must be a contiguous [B, Hkv, cap, D] tensor")
+    if v_cache.shape != k_cache.shape:
+        raise ValueError(f"v_cache {tuple(v_cache.shape)} and k_cache {tuple(k_cache.shape)} differ")
+    Bc, Hkv, cap, Dc = k_cache.shape
+    if Bc != B or Dc != D:
+        raise ValueError(f"caches [{Bc}, {Hkv}, {cap}, {Dc}] do not match q's batch {B} and head dim {D}")
+    if Hkv == 0 or Hq % Hkv != 0:
+        raise ValueError(f"Hq={Hq} is not a multiple of Hkv={Hkv}")
+    if not isinstance(pos0, torch.Tensor) or pos0.dtype != torch.int32 or tuple(pos0.shape) != (B,):
+        raise ValueError(f"pos0 must be an int32 tensor of shape [{B}]")
+    if not T <= int(kv_len_max) <= cap:
+        raise ValueError(f"kv_len_max={kv_len_max} must lie in [T={T}, cap={cap}]")
+    qg_ld = 0
+    if gate is not None:
+        _bf16(gate, "gate")
+        if gate.dim() != 3 or tuple(gate.shape[:2]) != (B, T):
+            raise ValueError(f"gate must be [B={B}, T={T}, {Hq * 2 * D}]")
+        qg_ld = _token_stride(gate, Hq * 2 * D, "gate")
+    if out is not None:
+        _bf16(out, "out")
+        if tuple(out.shape) != (B, T, Hq, D) or not out.is_contiguous():
+            raise ValueError(f"out must be a contiguous [{B}, {T}, {Hq}, {D}] tensor")
+    return B, T, Hq, D, Hkv, cap, qg_ld
+
+
 def attn_fwd(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, pos0: torch.Tensor, kv_len_max: int,
              *, gate: Optional[torch.Tensor] = None, scale: Optional[float] = None, n_split: int = 1,
              workspace: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None) -> torch.Tensor:
@@ -147,14 +183,8 @@ def attn_fwd(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, pos0
     (``gdn_attn_fwd``), times sigmoid of the gate half of ``gate``
     (``[B, T, Hq*2D]``, the q_proj output) when given.  ``kv_len_max`` bounds
     ``pos0[b] + T`` (host value; keys beyond it are not read)."""
-    dev = _require_device([q, k_cache, v_cache, pos0, gate], ["q", "k_cache", "v_cache", "pos0", "gate"])
-    _bf16(q, "q")
-    B, T, Hq, D = q.shape
-    Hkv, cap = k_cache.shape[1], k_cache.shape[2]
-    qg_ld = 0
-    if gate is not None:
-        _bf16(gate, "gate")
-        qg_ld = _token_stride(gate, Hq * 2 * D, "gate")
+    B, T, Hq, D, Hkv, cap, qg_ld = _check_attn_fwd(q, k_cache, v_cache, pos0, kv_len_max, gate, out)
+    dev = _require_device([q, k_cache, v_cache, pos0, gate, out], ["q", "k_cache", "v_cache", "pos0", "gate", "out"])
     if out is None:
         out = torch.empty(B, T, Hq, D, dtype=torch.bfloat16, device=dev)
     need = int(_lib.load().gdn_attn_workspace_bytes(B, T, Hq, Hkv, D, n_split))
@@ -174,11 +204,13 @@ def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float, *, residual: Opt
     ``h = x`` or, given ``residual``, ``h = x + residual`` (one launch; then
     returns ``(h, y)``).  ``out`` may be a column slice of a wider buffer
     (rows one stride apart), e.g. one half of a concatenation."""
-    dev = _require_device([x, weight, residual, out], ["x", "weight", "residual", "out"])
     _bf16(x, "x")
     D = x.shape[-1]
     if tuple(weight.shape) != (D,):
         raise ValueError(f"weight must be [{D}]")
+    if residual is not None and residual.shape != x.shape:
+        raise ValueError(f"residual {tuple(residual.shape)} must have x's shape {tuple(x.shape)}")
+    dev = _require_device([x, weight, residual, out], ["x", "weight", "residual", "out"])
     x = x.contiguous()
     rows = x.numel() // D
     if out is None:
@@ -215,21 +247,28 @@ def silu_mul(gate_up: torch.Tensor) -> torch.Tensor:
 class KVCache:
     """One attention layer's KV cache, ``[B, Hkv, capacity, D]`` bf16.
 
-    Rows advance together (the drafter keeps its rows aligned, as the
-    reference's plain ``KVCache`` with one scalar ``offset`` does); the
-    device copy of the offsets (``pos0``) is what the kernels read, so a
-    step never reads the host value back.  ``capacity`` grows by
-    reallocation (in steps of 256 positions) when a call would overflow it.
+    Row b holds its keys left-aligned at positions ``[0, lengths[b])``; the
+    device copy of the lengths (``pos0``) is what the kernels read (a row's
+    new tokens go to ``pos0[b]`` on, and it attends to keys ``[0, pos0[b] +
+    T)``), so a step never reads the host value back.  Rows of a batch join
+    may differ in length (:meth:`merge`), as the reference drafter's
+    ``BatchKVCache.merge`` allows (``mtp.py:505-511``); ``offset`` and
+    ``size()`` are the longest row's length, and :meth:`trim` drops the last
+    ``n`` positions of every row.  ``capacity`` grows by reallocation (in
+    steps of 256 positions) when a call would overflow it.
     """
 
     step = 256
 
     def __init__(self, batch: int, n_kv_heads: int, head_dim: int, capacity: int = 256,
                  device: Optional[torch.device] = None):
+        self._alloc(batch, n_kv_heads, head_dim, capacity, device)
+
+    def _alloc(self, batch, n_kv_heads, head_dim, capacity, device):
         capacity = max(self.step, -(-int(capacity) // self.step) * self.step)
         self.keys = torch.empty(batch, n_kv_heads, capacity, head_dim, dtype=torch.bfloat16, device=device)
         self.values = torch.empty_like(self.keys)
-        self.offset = 0
+        self.lengths = [0] * batch
         self.pos0 = torch.zeros(batch, dtype=torch.int32, device=device)
 
     @property
@@ -240,64 +279,96 @@ class KVCache:
     def capacity(self) -> int:
         return self.keys.shape[2]
 
+    @property
+    def offset(self) -> int:
+        """The longest row's length."""
+        return max(self.lengths, default=0)
+
     def size(self) -> int:
         return self.offset
 
     @property
     def state(self):
-        """The valid keys and values, ``[B, Hkv, offset, D]`` views."""
+        """Keys and values up to the longest row, ``[B, Hkv, offset, D]``
+        views (past a shorter row's length its entries are unset)."""
         return self.keys[..., : self.offset, :], self.values[..., : self.offset, :]
+
+    @state.setter
+    def state(self, kv) -> None:
+        """Replaces the contents by ``[keys, values]`` ``[B, Hkv, L, D]``: every
+        row then holds L positions (a prefix-cache restore of MTP blocks,
+        ``mtp.py:608``).  The cache is reallocated when its batch, head
+        layout or capacity does not fit."""
+        keys, values = kv
+        if keys.dim() != 4 or values.shape != keys.shape:
+            raise ValueError("state must be [keys, values] of one [B, Hkv, L, D] shape")
+        B, Hkv, L, D = keys.shape
+        if (B, Hkv, D) != (self.batch, self.keys.shape[1], self.keys.shape[3]) or L > self.capacity:
+            self._alloc(B, Hkv, D, max(L, self.capacity), self.keys.device)
+        self.keys[..., :L, :] = keys
+        self.values[..., :L, :] = values
+        self.lengths = [L] * B
+        self.pos0.fill_(L)
 
     def reserve(self, T: int) -> None:
         need = self.offset + int(T)
         if need <= self.capacity:
             return
         cap = -(-need // self.step) * self.step
+        n = self.offset
         for name in ("keys", "values"):
             old = getattr(self, name)
             new = torch.empty(*old.shape[:2], cap, old.shape[3], dtype=old.dtype, device=old.device)
-            new[..., : self.offset, :] = old[..., : self.offset, :]
+            new[..., :n, :] = old[..., :n, :]
             setattr(self, name, new)
 
     def advance(self, T: int) -> None:
-        self.offset += int(T)
+        self.lengths = [n + int(T) for n in self.lengths]
         self.pos0.add_(int(T))
 
     def trim(self, n: int) -> int:
-        """Drops the last ``n`` positions (the drafter's rollback)."""
+        """Drops the last ``n`` positions of every row (the drafter's rollback)."""
         n = min(int(n), self.offset)
-        self.offset -= n
-        self.pos0.sub_(n)
+        self.lengths = [max(0, m - n) for m in self.lengths]
+        self.pos0.sub_(n).clamp_(min=0)
         return n
 
     def filter(self, keep: Sequence[int]) -> None:
         """Keeps rows ``keep`` (a batch leave)."""
-        idx = torch.as_tensor(list(keep), dtype=torch.long, device=self.keys.device)
+        keep = [int(i) for i in keep]
+        idx = torch.as_tensor(keep, dtype=torch.long, device=self.keys.device)
         self.keys = self.keys.index_select(0, idx)
         self.values = self.values.index_select(0, idx)
         self.pos0 = self.pos0.index_select(0, idx)
+        self.lengths = [self.lengths[i] for i in keep]
 
     def extract(self, row: int) -> "KVCache":
         """A one-row copy of row ``row``."""
+        n = self.lengths[row]
         c = KVCache(1, self.keys.shape[1], self.keys.shape[3], self.capacity, self.keys.device)
-        c.keys[..., : self.offset, :] = self.keys[row : row + 1, :, : self.offset, :]
-        c.values[..., : self.offset, :] = self.values[row : row + 1, :, : self.offset, :]
-        c.advance(self.offset)
+        c.keys[..., :n, :] = self.keys[row : row + 1, :, :n, :]
+        c.values[..., :n, :] = self.values[row : row + 1, :, :n, :]
+        c.advance(n)
         return c
 
     @classmethod
     def merge(cls, caches: Sequence["KVCache"]) -> "KVCache":
-        """Rows of several caches of one length as one batch (a batch join)."""
-        lens = {c.offset for c in caches}
-        if len(lens) != 1:
-            raise ValueError("caches of different lengths cannot be merged into aligned rows")
+        """Rows of several caches as one batch (a batch join); rows keep
+        their own lengths."""
         first = caches[0]
+        Hkv, D = first.keys.shape[1], first.keys.shape[3]
+        if any(c.keys.shape[1] != Hkv or c.keys.shape[3] != D for c in caches):
+            raise ValueError("caches of different head layouts cannot be merged")
         cap = max(c.capacity for c in caches)
-        out = cls(sum(c.batch for c in caches), first.keys.shape[1], first.keys.shape[3], cap, first.keys.device)
-        n = first.offset
-        out.keys[..., :n, :] = torch.cat([c.keys[..., :n, :] for c in caches])
-        out.values[..., :n, :] = torch.cat([c.values[..., :n, :] for c in caches])
-        out.advance(n)
+        out = cls(sum(c.batch for c in caches), Hkv, D, cap, first.keys.device)
+        r = 0
+        for c in caches:
+            n = c.offset
+            out.keys[r : r + c.batch, :, :n, :] = c.keys[..., :n, :]
+            out.values[r : r + c.batch, :, :n, :] = c.values[..., :n, :]
+            r += c.batch
+        out.lengths = [m for c in caches for m in c.lengths]
+        out.pos0 = torch.tensor(out.lengths, dtype=torch.int32).to(first.keys.device)
         return out
 
 

@@ -529,14 +529,14 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnParams p) {
   // keys past the range re-read the last one (in bounds; they are masked)
   auto k_dma = [&](int kb, int st, int i) {
     const int key = min(kb + i * KR + k_row0, k_hi - 1);
-    lds_dma16(kc_head + key * D + (k_off - k_row0 * D), k_lds + st * KSTAGE + i * 4096);
+    lds_dma16(kc_head + static_cast<int64_t>(key) * D + (k_off - k_row0 * D), k_lds + st * KSTAGE + i * 4096);
   };
   // V block kb -> registers: pair i is key quad tid % 16 (4 rows) x d octet i * 16 + tid / 16
   const int v_kq = tid % (KB / 4), v_dq = tid / (KB / 4);
   u32x4 vr[VPAIRS][4];
   auto v_load = [&](int kb, int i, int e) {
     const int key = min(kb + 4 * v_kq + e, k_hi - 1);
-    vr[i][e] = *reinterpret_cast<const u32x4*>(vc_head + key * D + (v_dq + i * 16) * 8);
+    vr[i][e] = *reinterpret_cast<const u32x4*>(vc_head + static_cast<int64_t>(key) * D + (v_dq + i * 16) * 8);
   };
   // registers -> Vt stage st: for each of the octet's 8 d, the quad's 4 keys as one 8-byte write
   const int v_pos = 32 * (v_kq >> 3) + 8 * (v_kq & 3) + 4 * ((v_kq >> 2) & 1);

@@ -229,13 +229,17 @@ def _cu_seqlens(cu: Optional[IntSeq], n_tok: int, dev) -> Optional[torch.Tensor]
 
 def _packed_max_len(cu: IntSeq, n_tok: int, max_seqlen: Optional[int]) -> int:
     """Longest packed sequence, for choosing a kernel: exact for host
-    offsets; for a device table ``max_seqlen`` when given, else the mean
-    length (no device read, so no synchronisation)."""
+    offsets.  A device table is not read back (that would synchronise): with
+    one sequence its length is ``n_tok``; with several the caller must give
+    ``max_seqlen`` -- a length guessed from the mean would step one long
+    prompt packed with many short ones through the recurrent kernel."""
     if _is_device(cu, None):
         if max_seqlen is not None:
             return int(max_seqlen)
-        n_seqs = cu.numel() - 1
-        return -(-n_tok // n_seqs) if n_seqs > 0 else 0
+        if cu.numel() <= 2:
+            return n_tok
+        raise ValueError("a device cu_seqlens of several sequences needs max_seqlen (its longest sequence) "
+                         "or an explicit chunked=True / chunked=False to choose the kernel")
     host = torch.as_tensor(cu).to("cpu", torch.int64)
     return int((host[1:] - host[:-1]).max()) if host.numel() > 1 else 0
 
@@ -625,8 +629,9 @@ def gated_delta_update(q, k, v, a, b, A_log, dt_bias, state=None, mask=None, use
     Keyword-only additions: ``cu_seqlens`` packs ragged sequences in a
     ``[1, N_tok, ...]`` layout (state then has one row per sequence); host
     offsets are validated, a device tensor is used without a host copy (the
-    call never synchronises; ``max_seqlen``, when given, is its longest
-    sequence, which picks the kernel -- by default the mean length does);
+    call never synchronises, so with several sequences it needs
+    ``max_seqlen``, the longest one, to pick the kernel, unless ``chunked``
+    picks it);
     ``state_out`` receives the new state (may be ``state``); ``chunked``
     forces the chunked MFMA prefill kernel on/off (default: long unmasked
     bf16 rows with Dk = 128); ``workspace`` is a reusable uint8 buffer for it.
@@ -646,7 +651,7 @@ def gated_delta_update(q, k, v, a, b, A_log, dt_bias, state=None, mask=None, use
             s = state_out
         return y, s
     T = k.shape[1]
-    if cu_seqlens is not None:
+    if cu_seqlens is not None and chunked is None:
         T = _packed_max_len(cu_seqlens, k.shape[1], max_seqlen)
     if _use_chunked(chunked, q, k, v, mask, T):
         if mask is not None:

@@ -252,3 +252,24 @@ def test_prep_and_scan_launched_apart():
     torch.cuda.synchronize()
     y, S = plan.outputs
     assert torch.equal(y, y_ref) and torch.equal(S, S_ref)
+
+
+def test_device_offsets_need_max_seqlen_to_pick_a_kernel():
+    """One 500-token prompt packed with nine short ones (mean 51 tokens):
+    a device ``cu_seqlens`` is never read back, so without ``max_seqlen``
+    the call refuses to guess the kernel (the mean would step the long
+    prompt through the recurrent kernel); with it, the chunked kernel runs,
+    bit for bit as when forced."""
+    lens = [500, 3, 5, 1, 1, 1, 1, 1, 1, 1]
+    cu = torch.tensor(np.concatenate([[0], np.cumsum(lens)]), dtype=torch.int32, device=DEV)
+    d = draw(313, 1, int(sum(lens)), 2, 4, 128, 128, state=False)
+    t, r = to_torch(d, DEV)
+    args = (t["q"], t["k"], t["v"], t["a"], t["b"], t["A_log"], t["dt_bias"], None)
+    with pytest.raises(ValueError, match="max_seqlen"):
+        mx.gated_delta_update(*args, cu_seqlens=cu)
+    y, S = mx.gated_delta_update(*args, cu_seqlens=cu, max_seqlen=max(lens))
+    y_c, S_c = chunked(t, None, cu=cu)
+    assert torch.equal(y, y_c) and torch.equal(S, S_c)
+    y_ref, S_ref = oracle_heads(r, [0, 1, 2, 3], 4, 2, None, cu=cu.cpu().numpy())
+    assert rel_err(y.float().cpu().numpy(), y_ref) <= Y_TOL
+    assert head_errs_state(S.cpu().numpy(), S_ref).max() <= STATE_TOL
