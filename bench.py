@@ -483,21 +483,24 @@ def bench_prefix_state(torch, mx, dev, layers=24):
 def bench_mixer_layer(torch, mx, dev, timer, iters=20, hidden=2048):
     """One whole GatedDeltaNet mixer layer at the benchmark head layout with
     hidden size 2048 (in_proj GEMMs, fused prologue, GDN kernel, fused gated
-    RMSNorm, out_proj GEMM), eager from Python: decode B=64 (one token per
-    row, states in a StatePool updated in place) and prefill T=4096."""
+    RMSNorm, out_proj GEMM), eager from Python and graph-replayed: decode
+    B=64 and B=8 (one token per row, states in a StatePool updated in place;
+    at B=8 the norm runs inside out_proj, and the unfused B=8 step is timed
+    beside it) and prefill T=4096."""
     gen = torch.Generator().manual_seed(1008)
     m = mx.GatedDeltaNet(hidden, Hk, Hv, Dk, Dv, device=dev)
     m.reset_parameters(gen)
     res = {"hidden": hidden}
-    with torch.no_grad():
-        pool = mx.StatePool(64, Hv, Dv, Dk, device=dev)
+
+    def decode(B, tag):
+        pool = mx.StatePool(B, Hv, Dv, Dk, device=dev)
         cache = mx.ArraysCache()
-        cache[1] = mx.PooledBatch.new(pool, 64)
-        x = torch.randn(64, 1, hidden, generator=gen).to(torch.bfloat16).to(dev)
+        cache[1] = mx.PooledBatch.new(pool, B)
+        x = torch.randn(B, 1, hidden, generator=gen).to(torch.bfloat16).to(dev)
         for _ in range(3):
             m(x, None, cache)
         t = timer.total_ms(lambda i: m(x, None, cache), iters) / iters
-        res["decode_b64_us"] = round(1e3 * t, 2)
+        res[f"decode_{tag}_us"] = round(1e3 * t, 2)
         # the same step captured once in a HIP graph and replayed (the conv
         # state is handed back to the buffer the captured step reads)
         cs_in = cache[0]
@@ -509,7 +512,17 @@ def bench_mixer_layer(torch, mx, dev, timer, iters=20, hidden=2048):
         for _ in range(3):
             graph.replay()
         t = timer.total_ms(lambda i: graph.replay(), iters) / iters
-        res["decode_b64_graph_us"] = round(1e3 * t, 2)
+        res[f"decode_{tag}_graph_us"] = round(1e3 * t, 2)
+
+    with torch.no_grad():
+        decode(64, "b64")
+        # at 8 rows the gated norm runs inside out_proj's operand load; the
+        # same step with the separate norm kernel and the library GEMM beside it
+        decode(8, "b8")
+        fused = m.fused_norm_max_rows
+        m.fused_norm_max_rows = 0
+        decode(8, "b8_unfused")
+        m.fused_norm_max_rows = fused
         xp = torch.randn(1, 4096, hidden, generator=gen).to(torch.bfloat16).to(dev)
         for _ in range(2):
             m(xp, None, mx.ArraysCache())

@@ -345,6 +345,41 @@ int gdn_rms_norm(const void* x, const void* res, void* h_out, const void* w, int
  * (bf16; gate_up is one [rows, 2I] product of the gate and up projections). */
 int gdn_silu_mul(const void* gate_up, void* out, int64_t rows, int64_t I, void* stream);
 
+/* ---------------------------------------------------------------------
+ * Decode-shape projections of the GatedDeltaNet mixer (in_proj,
+ * dflash.py:348-350; norm(out, z) then out_proj, dflash.py:377-378) for at
+ * most 64 rows, where the weight read bounds the GEMM.
+ * --------------------------------------------------------------------- */
+
+/* Workspace bytes of gdn_linear_decode (0 for shapes it does not take): a
+ * 16 KiB region of 32-bit tickets, one per 64-column output tile (N up to
+ * 262144), then the fp32 partials of the K slices.  The ticket region must be
+ * zero before the first call; every call leaves it zero, so one workspace,
+ * sized for the largest shape, serves calls of any shape in turn.  Calls that
+ * overlap (several streams) need one workspace each. */
+size_t gdn_linear_decode_workspace_bytes(int64_t M, int64_t N, int64_t K);
+
+/*
+ * out[M, N] = A[M, K] W[N, K]^T in bf16 with fp32 accumulation, 1 <= M <= 64,
+ * K a multiple of 512, N a multiple of 8:
+ *   gate == NULL  A = x (rows ldx elements apart);
+ *   gate != NULL  A = gated RMSNorm of x per head of head_dim (64 or 128)
+ *                 columns, with gdn_gated_rmsnorm's arithmetic and rounding:
+ *                 n = bf16(x / sqrt(mean(x^2) + eps)), m = bf16(w n) (w bf16)
+ *                 or w n (w fp32; NULL = ones), A = bf16(m silu(gate)); gate
+ *                 rows ldg elements apart, w [head_dim].
+ *   W [N, K] row-major; out rows ldo elements apart.
+ * Strides are multiples of 8 elements; pointers 16-byte aligned.  The K
+ * slices of one output tile are summed in slice order, so results do not
+ * depend on scheduling.  With the norm fused it is faster than the separate
+ * norm plus a library GEMM up to 16 rows, and slower beyond (at hidden 2048,
+ * graph-replayed); without the norm the library GEMM is faster.
+ */
+int gdn_linear_decode(const void* x, int64_t ldx, const void* gate, int64_t ldg, const void* norm_w,
+                      int norm_w_dtype, float eps, int64_t head_dim, const void* W, void* out,
+                      int64_t ldo, int64_t M, int64_t N, int64_t K, void* workspace,
+                      size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

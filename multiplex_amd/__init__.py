@@ -25,6 +25,7 @@ from .cache import ArraysCache, clone_ssm, merge_layer, restore_ssm, restore_ssm
 from .state_pool import PooledBatch, StatePool
 from . import prefix_state
 from .epilogue import gated_rms_norm, prepare_gated_rms_norm
+from .linear import DecodeWorkspace, gated_norm_linear_decode, linear_decode
 from .mixer import GatedDeltaNet, commit_verified
 from .mixed_step import MixedStep
 from .attention import Attention, AttentionArgs, DecoderLayer, KVCache, MTPHead
@@ -36,6 +37,7 @@ __all__ = [
     "KVCache",
     "MTPHead",
     "ArraysCache",
+    "DecodeWorkspace",
     "GatedDeltaNet",
     "MixedStep",
     "PooledBatch",
@@ -60,6 +62,8 @@ __all__ = [
     "gated_delta_update",
     "gated_delta_verify",
     "gdn_conv_prologue",
+    "gated_norm_linear_decode",
+    "linear_decode",
     "prepare_chunked",
     "prepare_conv_prologue",
     "prepare_recurrent",

@@ -47,6 +47,8 @@ EXPORTS = (
     "gdn_attn_fwd",
     "gdn_rms_norm",
     "gdn_silu_mul",
+    "gdn_linear_decode_workspace_bytes",
+    "gdn_linear_decode",
 )
 
 
@@ -159,6 +161,11 @@ _SIGNATURES = {
     ),
     "gdn_rms_norm": (c_int, [_P, _P, _P, _P, c_int, _P, _I64, _I64, _I64, c_float, _P]),
     "gdn_silu_mul": (c_int, [_P, _P, _I64, _I64, _P]),
+    "gdn_linear_decode_workspace_bytes": (c_size_t, [_I64, _I64, _I64]),
+    "gdn_linear_decode": (
+        c_int,
+        [_P, _I64, _P, _I64, _P, c_int, c_float, _I64, _P, _P, _I64, _I64, _I64, _I64, _P, c_size_t, _P],
+    ),
 }
 
 

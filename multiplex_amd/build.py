@@ -22,6 +22,7 @@ SOURCES = [
     "gdn_chunk.hip",
     "gdn_epilogue.hip",
     "gdn_attention.hip",
+    "gdn_linear.hip",
 ]
 ARCH = "gfx950"
 

@@ -14,8 +14,10 @@ Data path per call:
                                kernels below read its column slices in place
   gdn_conv_prologue            fused conv1d + SiLU + q/k norm (HIP)
   gated_delta_update           recurrent or chunked kernel (HIP)
-  gated_rms_norm               fused gated RMSNorm (HIP)
-  out_proj                     library GEMM (hipBLASLt through torch)
+  norm(out, z) + out_proj      up to 16 rows (decode of up to 16 rows) one
+                               ``gdn_linear_decode`` launch with the gated
+                               RMSNorm in its operand load (HIP); else the
+                               gated RMSNorm kernel (HIP) and the library GEMM
 
 Speculative rounds: ``mixer(inputs, mask, cache, verify=True)`` computes the
 outputs of all T draft tokens without touching ``cache`` and remembers what
@@ -39,6 +41,7 @@ from .conv import conv_state_commit, gdn_conv_prologue
 from .epilogue import gated_rms_norm
 from .state_pool import PooledBatch
 from .gated_delta import IntSeq, gated_delta_commit, gated_delta_update, gated_delta_verify
+from .linear import FUSED_NORM_MAX_ROWS, DecodeWorkspace, decode_shape_ok, gated_norm_linear_decode
 
 __all__ = ["GatedDeltaNet", "gated_rms_norm", "commit_verified"]
 
@@ -93,6 +96,10 @@ class GatedDeltaNet(torch.nn.Module):
         self.norm_weight = torch.nn.Parameter(torch.ones(head_v_dim, **kw))
         self.out_proj = torch.nn.Linear(self.value_dim, hidden_size, bias=False, **kw)
         self._pending: Optional[_Pending] = None
+        # the fused norm + out_proj runs up to this many rows (0: never), with
+        # its workspace (zeroed once, left zeroed by every call)
+        self.fused_norm_max_rows = FUSED_NORM_MAX_ROWS
+        self._ws_out = DecodeWorkspace()
         self.reset_parameters()
 
     @torch.no_grad()
@@ -154,6 +161,16 @@ class GatedDeltaNet(torch.nn.Module):
 
     def _epilogue(self, y, z):
         B, S = y.shape[:2]
+        M = B * S
+        W = self.out_proj.weight
+        if (M <= self.fused_norm_max_rows and y.dtype == torch.bfloat16 and self.out_proj.bias is None
+                and self.head_v_dim in (64, 128) and decode_shape_ok(M, W.shape[0], W.shape[1])
+                and z.stride(-2) == self.head_v_dim and (B == 1 or S == 1 or z.stride(0) == S * z.stride(1))):
+            # z [B, S, Hv, Dv] is a column slice of the in_proj output: rows one token stride apart
+            z_rows = z.as_strided((M, self.value_dim), (z.stride(1) if S > 1 else z.stride(0), 1))
+            out = gated_norm_linear_decode(y.reshape(M, -1), z_rows, self.norm_weight, self.rms_norm_eps,
+                                           self.head_v_dim, W, workspace=self._ws_out)
+            return out.view(B, S, -1)
         # y is this call's own buffer: normalise it in place
         out = gated_rms_norm(y, z, self.norm_weight, self.rms_norm_eps, out=y)
         return self.out_proj(out.reshape(B, S, -1))

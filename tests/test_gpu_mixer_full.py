@@ -7,6 +7,8 @@ The per-kernel tests check every kernel at full size; what these add is the
 full-width wiring: the fused in_proj output read in place as column slices
 (q|k|v at 8192 channels, z at 4096, b and a at 32), the strides the
 prologue, the GDN kernel and the norm take from it, and the pool slots.
+The decode step runs at B=64 (the separate norm kernel and the library
+out_proj) and at B=8 (the norm fused into out_proj's operand load).
 Each call is decomposed at the library GEMMs:
 
 * the prologue's q, k, v from the mixer's own projection against the
@@ -72,17 +74,18 @@ def _check(m, x, cs_before, s_before, out, s_after, cs_after):
     assert rel_err(out.float().cpu().numpy(), o_ref) <= Y_TOL
 
 
+@pytest.mark.parametrize("B", [64, 8])
 @torch.no_grad()
-def test_full_width_pooled_decode_b64():
+def test_full_width_pooled_decode(B):
     m = _mixer(81)
-    gen = torch.Generator().manual_seed(82)
+    gen = torch.Generator().manual_seed(82 + B)
     pool = mx.StatePool(80, HV, D, D, device=DEV)
     cache = mx.ArraysCache()
-    batch = mx.PooledBatch.new(pool, 64)  # zeroes its slots: nonzero states are set after
+    batch = mx.PooledBatch.new(pool, B)  # zeroes its slots: nonzero states are set after
     pool.states.copy_(torch.randn(pool.states.shape, generator=gen) * 0.02)
     cache[1] = batch
-    cache[0] = (torch.randn(64, 3, m.conv_dim, generator=gen) * 0.5).to(torch.bfloat16).to(DEV)
-    x = torch.randn(64, 1, HID, generator=gen).to(torch.bfloat16).to(DEV)
+    cache[0] = (torch.randn(B, 3, m.conv_dim, generator=gen) * 0.5).to(torch.bfloat16).to(DEV)
+    x = torch.randn(B, 1, HID, generator=gen).to(torch.bfloat16).to(DEV)
     cs_before = cache[0].clone()
     slots = batch.index.long()
     s_before = pool.states.index_select(0, slots).clone()
