@@ -273,8 +273,15 @@ def bench_prefill(torch, mx, dev, timer, iters=50):
     q, k, v, _ = pro.outputs
     gdn = mx.prepare_chunked(q, k, v, a, b, A_log, dt_bias, None, workspace=ws)
     out = {"S": gdn.outputs[1]}
+    # the mixer's path: the prologue inside the chunked pass's prep (one
+    # call, two launches), bit-identical to the two calls above
+    wsf = torch.empty(mx.conv_chunk_workspace_bytes(1, T, Hv, Dk, Dv), dtype=torch.uint8, device=dev)
+    fused = mx.prepare_conv_chunked(qkv, w, Hk, Hv, Dk, Dv, a, b, A_log, dt_bias, None, cs, workspace=wsf)
 
     def step(i):
+        fused.launch()
+
+    def unfused(i):
         pro.launch()
         gdn.launch()
 
@@ -286,13 +293,19 @@ def bench_prefill(torch, mx, dev, timer, iters=50):
 
     for _ in range(3):
         step(0)
+        unfused(0)
     t_all = timer.total_ms(step, iters) / iters
+    t_unfused = timer.total_ms(unfused, iters) / iters
     t_gdn = timer.total_ms(gdn_only, iters) / iters
     t_pro = timer.total_ms(pro_only, iters) / iters
     flops = prefill_flops([T])
-    return dict(ms_total=t_all, ms_gdn=t_gdn, ms_prologue=t_pro, tokens_per_s=T / (t_all * 1e-3),
+    torch.cuda.synchronize()
+    same = bool(torch.equal(fused.outputs[1], out["S"]))
+    return dict(ms_total=t_all, ms_unfused=t_unfused, ms_gdn=t_gdn, ms_prologue=t_pro,
+                tokens_per_s=T / (t_all * 1e-3),
                 gdn_tflops=flops / (t_gdn * 1e-3) / 1e12, mfma_frac=flops / (t_gdn * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS,
-                flops=flops, finite=bool(torch.isfinite(out["S"]).all()))
+                mfma_frac_with_prologue=flops / (t_all * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS,
+                flops=flops, finite=bool(torch.isfinite(out["S"]).all()), fused_equals_unfused=same)
 
 
 def mixed_bytes(lens, n_dec=48, n_ver=16, t_ver=4):
@@ -875,7 +888,8 @@ def main():
     if "prefill_t4096" in configs:
         p = configs["prefill_t4096"]
         line["prefill"] = {"tokens_per_s": round(p["tokens_per_s"], 1), "ms": round(p["ms_total"], 4),
-                           "gdn_ms": round(p["ms_gdn"], 4), "mfma_frac": round(p["mfma_frac"], 4),
+                           "unfused_ms": round(p["ms_unfused"], 4), "gdn_ms": round(p["ms_gdn"], 4),
+                           "mfma_frac": round(p["mfma_frac"], 4),
                            "cpu_tokens_per_s": None if base is None else round(base["prefill_tokens_per_s"], 1)}
     print(json.dumps(line), flush=True)
 

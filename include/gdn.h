@@ -201,6 +201,40 @@ int gdn_chunk_scan(const void* q, const void* k, const void* v, int qkv_dtype,
                    void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * The mixer's prefill from its mixed projection: the conv prologue
+ * (gdn_conv_prologue; dflash.py:351-370) fused into gdn_chunk_fwd's prep,
+ * then the scan (dflash.py:372-374).  Replaces gdn_conv_prologue followed by
+ * gdn_chunk_fwd: the prep forms its chunk's q and k (its k-head) and v (its
+ * v-head) from the qkv rows with the prologue's arithmetic, so y, the state
+ * and the new conv state are bit-identical to that pair's, and q and k are
+ * never written (v goes to the workspace, for the scan).
+ *   qkv [n_tok, C] bf16 rows (C = 2 Hk Dk + Hv Dv, q | k | v channels),
+ *       qkv_stride elements apart (0: C; else >= C, a multiple of 8);
+ *   conv_w [C][4] taps, bf16 or fp32 (conv_w_dtype);
+ *   conv_state_in [n_seqs][3][C] bf16 or NULL (zeros); conv_state_out the
+ *       same shape or NULL (not written), not aliasing conv_state_in;
+ *   eps: the q/k norms' epsilon.
+ * Gates, states, sequences and y as in gdn_chunk_fwd (no mask; Dk = Dv =
+ * 128).  The workspace must hold gdn_chunk_conv_workspace_bytes(...) bytes
+ * (256-B aligned): gdn_chunk_workspace_bytes(...), then n_tok Hv Dv bf16.
+ */
+size_t gdn_chunk_conv_workspace_bytes(int64_t n_seqs, int64_t n_tok, int64_t Hv,
+                                      int64_t Dk, int64_t Dv, int64_t chunk);
+
+int gdn_chunk_fwd_conv(const void* qkv, int64_t qkv_stride, const void* conv_w,
+                       int conv_w_dtype, const void* conv_state_in,
+                       void* conv_state_out, float eps, int gate_mode,
+                       const void* gx, const void* gy, int gate_dtype,
+                       int64_t gate_stride, const void* A_log,
+                       const void* dt_bias, int param_dtype,
+                       const float* state_in, void* y, float* state_out,
+                       const int32_t* state_index, int64_t n_slots,
+                       const int32_t* cu_seqlens, int64_t n_seqs, int64_t n_tok,
+                       int64_t Hk, int64_t Hv, int64_t Dk, int64_t Dv,
+                       int64_t chunk, void* workspace, size_t workspace_bytes,
+                       void* stream);
+
+/*
  * gdn_chunk_fwd without a workspace argument: the chunk records go to a
  * static device array of 64 MiB (67,108,864 bytes) inside the library,
  * one per GPU, held until the process ends.  No reference counterpart: it

@@ -20,7 +20,8 @@ from .gated_delta import (
     prepare_chunked,
     prepare_recurrent,
 )
-from .conv import conv_state_commit, gdn_conv_prologue, prepare_conv_prologue
+from .conv import (conv_chunk_workspace_bytes, conv_state_commit, gdn_conv_chunked, gdn_conv_prologue,
+                   prepare_conv_chunked, prepare_conv_prologue)
 from .cache import ArraysCache, clone_ssm, merge_layer, restore_ssm, restore_ssm_snapshot, snapshot_ssm
 from .state_pool import PooledBatch, StatePool
 from . import prefix_state
@@ -54,7 +55,9 @@ __all__ = [
     "chunk_workspace_bytes",
     "compute_beta",
     "compute_g",
+    "conv_chunk_workspace_bytes",
     "conv_state_commit",
+    "gdn_conv_chunked",
     "gated_delta_commit",
     "gated_delta_commit_verify",
     "gated_delta_kernel",
@@ -65,6 +68,7 @@ __all__ = [
     "gated_norm_linear_decode",
     "linear_decode",
     "prepare_chunked",
+    "prepare_conv_chunked",
     "prepare_conv_prologue",
     "prepare_recurrent",
 ]

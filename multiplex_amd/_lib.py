@@ -39,6 +39,8 @@ EXPORTS = (
     "gdn_chunk_prep",
     "gdn_chunk_scan",
     "gdn_chunk_fwd_noalloc",
+    "gdn_chunk_conv_workspace_bytes",
+    "gdn_chunk_fwd_conv",
     "gdn_conv_prologue",
     "gdn_conv_state_commit",
     "gdn_gated_rmsnorm",
@@ -135,6 +137,12 @@ _SIGNATURES = {
         c_int,
         [_P, _P, _P, c_int, c_int, _P, _P, c_int, _I64, _P, _P, c_int, _P, _P, _P, _P, _I64, _P,
          _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P],
+    ),
+    "gdn_chunk_conv_workspace_bytes": (c_size_t, [_I64, _I64, _I64, _I64, _I64, _I64]),
+    "gdn_chunk_fwd_conv": (
+        c_int,
+        [_P, _I64, _P, c_int, _P, _P, c_float, c_int, _P, _P, c_int, _I64, _P, _P, c_int, _P, _P, _P, _P, _I64, _P,
+         _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P, c_size_t, _P],
     ),
     "gdn_conv_prologue": (
         c_int,

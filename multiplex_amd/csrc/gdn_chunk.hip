@@ -88,6 +88,17 @@ struct ChunkParams {
   int Hk, Hv, group;
   unsigned char* ws;
   int32_t* order;     // [n_seqs] packed sequences longest first (in the workspace), or null
+  // The conv prologue fused into the prep (chunk_prep_kernel with CONV): q,
+  // k and v are formed from the mixed qkv rows; the prep writes v to v_out
+  // (p.v points at it, for the scan) and the sequences' new conv states.
+  const uint16_t* qkv;
+  int64_t qkv_ld;         // elements from one qkv row to the next
+  const void* conv_w;     // [C][4] taps, bf16 or fp32
+  const uint16_t* cs_in;  // [n_seqs][3][C], or null (zeros)
+  uint16_t* cs_out;       // [n_seqs][3][C], or null
+  uint16_t* v_out;        // [n_tok][Hv][DV]
+  int C;                  // qkv channels: 2 Hk DK + Hv DV
+  float conv_eps;
 };
 
 // Packed calls of 2..kOrderMax sequences order them by length, so the scan
@@ -201,29 +212,41 @@ __device__ __forceinline__ SeqRange seq_range(const ChunkParams& p, int n) {
   return r;
 }
 
-// Global chunk index -> (first token, valid length).  False past the end.
-__device__ __forceinline__ bool chunk_at(const ChunkParams& p, int c, int64_t& tok0, int& len) {
+// Where a chunk slot lies: its sequence, the sequence's first token and
+// length, the chunk's index in it, its first token and valid length.
+struct ChunkPos {
+  int seq, seq_len, ci, len;
+  int64_t seq_tok0, tok0;
+};
+
+// Global chunk index -> its position.  False for a slot past the end or one
+// no sequence uses; then `seq`, `seq_len` and `ci` still name the sequence
+// whose slots the index falls among (for packed calls).
+__device__ __forceinline__ bool chunk_at(const ChunkParams& p, int c, ChunkPos& cp) {
   if (p.cu == nullptr) {
     const int cps = n_chunks(p.T);
     if (cps == 0 || c >= p.n_seqs * cps) return false;
-    const int n = c / cps, i = c % cps;
-    tok0 = static_cast<int64_t>(n) * p.T + static_cast<int64_t>(i) * CH;
-    len = min(CH, p.T - i * CH);
-    return true;
+    cp.seq = c / cps;
+    cp.ci = c % cps;
+    cp.seq_len = p.T;
+    cp.seq_tok0 = static_cast<int64_t>(cp.seq) * p.T;
+  } else {
+    // the last sequence whose first slot is at or below c (first slots
+    // increase with n), by bisection
+    int lo = 0, hi = p.n_seqs - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (first_slot(p, mid) <= c) lo = mid;
+      else hi = mid - 1;
+    }
+    cp.seq = lo;
+    cp.seq_len = cu_len(p, lo);
+    cp.ci = c - first_slot(p, lo);
+    cp.seq_tok0 = cu_start(p, lo);
+    if (cp.ci < 0 || cp.ci >= n_chunks(cp.seq_len)) return false;  // a slot no sequence uses
   }
-  // the last sequence whose first slot is at or below c (first slots
-  // increase with n), by bisection
-  int lo = 0, hi = p.n_seqs - 1;
-  while (lo < hi) {
-    const int mid = (lo + hi + 1) >> 1;
-    if (first_slot(p, mid) <= c) lo = mid;
-    else hi = mid - 1;
-  }
-  const int l = cu_len(p, lo);
-  const int i = c - first_slot(p, lo);
-  if (i < 0 || i >= n_chunks(l)) return false;  // a slot no sequence uses
-  tok0 = cu_start(p, lo) + static_cast<int64_t>(i) * CH;
-  len = min(CH, l - i * CH);
+  cp.tok0 = cp.seq_tok0 + static_cast<int64_t>(cp.ci) * CH;
+  cp.len = min(CH, cp.seq_len - cp.ci * CH);
   return true;
 }
 
@@ -244,6 +267,114 @@ __device__ void order_sequences(const ChunkParams& p, int* lens) {
     }
     p.order[r] = i;
   }
+}
+
+// ------------------------------------------------------- fused conv prologue
+
+constexpr int KTAP = 4;  // conv taps
+
+// The conv prologue (prologue_kernel in gdn_prologue.hip) for one lane's 8
+// channels c0 .. c0+7 over the R tokens [t0, t0 + R) of a chunk, with that
+// kernel's arithmetic and rounding, so q, k and v are bit-identical to its:
+// o = silu(w[3] x_t + w[0] x_{t-3} + w[1] x_{t-2} + w[2] x_{t-1}) (fused in
+// that order) and, with NORM, o * rsqrt(mean over the head of o^2 + eps) *
+// post, the mean over this lane's 16-lane row (the head's 16 lanes, in the
+// prologue's lane order).  x runs over X = the sequence's conv state (3
+// rows; zeros without one) followed by its qkv rows.  Tokens past the
+// chunk's end repeat its last row.  Every load is issued before the first
+// conversion.
+template <int WDT, int R, bool NORM>
+__device__ __forceinline__ void conv_run(const ChunkParams& p, const ChunkPos& cp, int c0, int t0, float post,
+                                         u32x4 (&out)[R]) {
+  Raw8<WDT> wr[KTAP];
+#pragma unroll
+  for (int i = 0; i < KTAP; ++i) wr[i] = load_raw8<WDT>(p.conv_w, static_cast<int64_t>(c0) * KTAP + 8 * i);
+  const int pos = cp.ci * CH + t0;  // the run's first token within its sequence
+  Raw8<GDN_DTYPE_BF16> xw[KTAP - 1];
+  float wm[KTAP - 1];
+#pragma unroll
+  for (int i = 0; i < KTAP - 1; ++i) {
+    const int xi = pos + i;
+    const bool from_cs = xi < KTAP - 1;
+    const bool cs_row = from_cs && p.cs_in != nullptr;
+    // without a conv state the row is the sequence's first qkv row times 0;
+    // a run that starts past the chunk's end (outputs discarded) reads
+    // within the chunk's valid rows
+    const int tp = from_cs ? 0 : min(xi - (KTAP - 1), cp.ci * CH + cp.len - 1);
+    const int64_t off = cs_row ? (static_cast<int64_t>(cp.seq) * (KTAP - 1) + xi) * p.C + c0
+                               : (cp.seq_tok0 + tp) * p.qkv_ld + c0;
+    xw[i] = load_raw8<GDN_DTYPE_BF16>(cs_row ? static_cast<const void*>(p.cs_in) : p.qkv, off);
+    wm[i] = from_cs && !cs_row ? 0.0f : 1.0f;
+  }
+  Raw8<GDN_DTYPE_BF16> xs[R];
+#pragma unroll
+  for (int u = 0; u < R; ++u)
+    xs[u] = load_raw8<GDN_DTYPE_BF16>(p.qkv, (cp.tok0 + min(t0 + u, cp.len - 1)) * p.qkv_ld + c0);
+  float w[KTAP][CPL];
+  {
+    float wv[CPL * KTAP];
+#pragma unroll
+    for (int i = 0; i < KTAP; ++i) unpack8<WDT>(wr[i], *reinterpret_cast<float(*)[CPL]>(&wv[8 * i]));
+#pragma unroll
+    for (int j = 0; j < CPL; ++j)
+#pragma unroll
+      for (int i = 0; i < KTAP; ++i) w[i][j] = wv[j * KTAP + i];
+  }
+  float win[KTAP - 1][CPL];
+#pragma unroll
+  for (int i = 0; i < KTAP - 1; ++i) {
+    unpack8<GDN_DTYPE_BF16>(xw[i], win[i]);
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) win[i][j] *= wm[i];
+  }
+#pragma unroll
+  for (int u = 0; u < R; ++u) {
+    float x[CPL], o[CPL];
+    unpack8<GDN_DTYPE_BF16>(xs[u], x);
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+      float acc = w[KTAP - 1][j] * x[j];
+#pragma unroll
+      for (int i = 0; i < KTAP - 1; ++i) acc = fmaf(w[i][j], win[i][j], acc);
+      o[j] = silu(acc);
+      ss = fmaf(o[j], o[j], ss);
+    }
+#pragma unroll
+    for (int i = 0; i < KTAP - 2; ++i)
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) win[i][j] = win[i + 1][j];
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) win[KTAP - 2][j] = x[j];
+    if constexpr (NORM) {
+      ss = head_sum<16>(ss);
+      const float sc = rsqrtf(ss / static_cast<float>(DK) + p.conv_eps) * post;
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) o[j] *= sc;
+    }
+    out[u] = u32x4{pk_bf16(o[0], o[1]), pk_bf16(o[2], o[3]), pk_bf16(o[4], o[5]), pk_bf16(o[6], o[7])};
+  }
+}
+
+// The new conv state of a sequence whose last chunk this workgroup holds
+// (or of an empty sequence): X's last 3 rows, X[len + i], on the channels
+// of this v-head and, from the k-head's first v-head, of its q and k heads.
+// Thread i < 144 copies 8 channels of one row.
+__device__ __forceinline__ void conv_state_rows(const ChunkParams& p, int seq, int64_t seq_tok0, int seq_len,
+                                                int hk, int hv, bool first_v, int tid) {
+  if (p.cs_out == nullptr || tid >= 3 * 48) return;
+  const int row = tid / 48, grp = tid % 48;
+  if (grp < 32 && !first_v) return;
+  const int c0 = grp < 16 ? hk * DK + 8 * grp
+                          : (grp < 32 ? (p.Hk + hk) * DK + 8 * (grp - 16) : 2 * p.Hk * DK + hv * DV + 8 * (grp - 32));
+  const int xi = seq_len + row;
+  u32x4 v = {0u, 0u, 0u, 0u};
+  if (xi >= KTAP - 1) {
+    v = *reinterpret_cast<const u32x4*>(p.qkv + (seq_tok0 + xi - (KTAP - 1)) * p.qkv_ld + c0);
+  } else if (p.cs_in != nullptr) {
+    v = *reinterpret_cast<const u32x4*>(p.cs_in + (static_cast<int64_t>(seq) * (KTAP - 1) + xi) * p.C + c0);
+  }
+  *reinterpret_cast<u32x4*>(p.cs_out + (static_cast<int64_t>(seq) * (KTAP - 1) + row) * p.C + c0) = v;
 }
 
 // ------------------------------------------------------------ chunk_prep
@@ -285,7 +416,13 @@ __device__ __forceinline__ void wave_lds_sync() {
 // waves per SIMD; left to itself the compiler takes 137-138, which leaves
 // three).  At 4096 tokens x 32 heads the 2048 workgroups then run in two
 // full rounds instead of two and two thirds.
-template <bool KT_LDS>
+//
+// CONV (1: bf16 taps, 2: fp32 taps): the conv prologue is fused in.  The
+// workgroup forms its chunk's q and k rows (its k-head) and v rows (its
+// v-head) from the qkv rows with the conv prologue's arithmetic, writes v
+// for the scan and, at a sequence's last chunk, the new conv state; the
+// slot of an empty packed sequence passes its conv state through.
+template <bool KT_LDS, int CONV>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void chunk_prep_kernel(const ChunkParams p) {
   // Two 17 KB buffers, each reused once (LDS stays under 40 KB, so four
   // workgroups fit on a CU):  buf0 = K rows, then A;  buf1 = Q rows, then
@@ -305,10 +442,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void c
   const int w = xcd_work_index(gridDim.x - (p.order != nullptr ? 1 : 0));
   const int c = w / p.Hv;
   const int hv = w % p.Hv;
-  int64_t tok0;
-  int len;
-  if (!chunk_at(p, c, tok0, len)) return;
   const int hk = hv / p.group;
+  const bool first_v = hv % p.group == 0;  // writes the k-head's K^T, K and Q
+  ChunkPos cp;
+  if (!chunk_at(p, c, cp)) {
+    if constexpr (CONV != 0) {
+      if (p.cu != nullptr && cp.seq_len == 0 && cp.ci == 0)
+        conv_state_rows(p, cp.seq, cp.seq_tok0, 0, hk, hv, first_v, threadIdx.x);
+    }
+    return;
+  }
+  const int64_t tok0 = cp.tok0;
+  const int len = cp.len;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
   const int lr = lane & 15, lq = lane >> 4, lg8 = lq * 8;
@@ -332,13 +477,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void c
   float b_lane = 0.0f;
   asm volatile("" ::: "memory");  // keeps the gate loads issued ahead of the rows
   u32x4 kr[4], qr[4];
+  if constexpr (CONV == 0) {
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int i = tid + 256 * j;
-    const int r = i / (DK / 8), cc = (i % (DK / 8)) * 8;
-    const int64_t off = ((tok0 + min(r, len - 1)) * p.Hk + hk) * DK + cc;
-    kr[j] = *reinterpret_cast<const u32x4*>(p.k + off);
-    qr[j] = *reinterpret_cast<const u32x4*>(p.q + off);
+    for (int j = 0; j < 4; ++j) {
+      const int i = tid + 256 * j;
+      const int r = i / (DK / 8), cc = (i % (DK / 8)) * 8;
+      const int64_t off = ((tok0 + min(r, len - 1)) * p.Hk + hk) * DK + cc;
+      kr[j] = *reinterpret_cast<const u32x4*>(p.k + off);
+      qr[j] = *reinterpret_cast<const u32x4*>(p.q + off);
+    }
   }
   unsigned char* rec = p.ws + (static_cast<size_t>(c) * p.Hv + hv) * kRecBytes;
   if (wave == 0) {
@@ -352,18 +499,51 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void c
     Bs[lane] = bt;
     b_lane = bt;
   }
-  const bool first_v = hv % p.group == 0;  // writes the k-head's K^T, K and Q
+  if constexpr (CONV == 0) {
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int i = tid + 256 * j;
-    const int r = i / (DK / 8), cc = (i % (DK / 8)) * 8;
-    const u32x4 kv = keep_if(r < len, kr[j]), qv = keep_if(r < len, qr[j]);
-    *reinterpret_cast<u32x4*>(&Ks[r][cc]) = kv;
-    *reinterpret_cast<u32x4*>(&Qs[r][cc]) = qv;
-    if (first_v) {
-      *reinterpret_cast<u32x4*>(reinterpret_cast<uint16_t*>(rec + kOffKf) + frag_elem(r, cc, DK / 32)) = kv;
-      *reinterpret_cast<u32x4*>(reinterpret_cast<uint16_t*>(rec + kOffQf) + frag_elem(r, cc, DK / 32)) = qv;
+    for (int j = 0; j < 4; ++j) {
+      const int i = tid + 256 * j;
+      const int r = i / (DK / 8), cc = (i % (DK / 8)) * 8;
+      const u32x4 kv = keep_if(r < len, kr[j]), qv = keep_if(r < len, qr[j]);
+      *reinterpret_cast<u32x4*>(&Ks[r][cc]) = kv;
+      *reinterpret_cast<u32x4*>(&Qs[r][cc]) = qv;
+      if (first_v) {
+        *reinterpret_cast<u32x4*>(reinterpret_cast<uint16_t*>(rec + kOffKf) + frag_elem(r, cc, DK / 32)) = kv;
+        *reinterpret_cast<u32x4*>(reinterpret_cast<uint16_t*>(rec + kOffQf) + frag_elem(r, cc, DK / 32)) = qv;
+      }
     }
+  } else {
+    // 16-lane row rw of the workgroup takes 4 tokens, [4 rw, 4 rw + 4), of
+    // one head, lane g of the row channels 8 g .. 8 g + 7 of it: q, then k
+    // (to LDS and the records, as the loads above would), then v (for the
+    // scan).
+    constexpr int WDT = CONV == 2 ? GDN_DTYPE_F32 : GDN_DTYPE_BF16;
+    const int rw = 4 * wave + lq, g = lr, t0 = 4 * rw;
+#pragma unroll
+    for (int role = 0; role < 2; ++role) {
+      u32x4 o[4];
+      const float post = role == 0 ? 1.0f / static_cast<float>(DK) : rsqrtf(static_cast<float>(DK));
+      conv_run<WDT, 4, true>(p, cp, (role * p.Hk + hk) * DK + 8 * g, t0, post, o);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int r = t0 + u;
+        const u32x4 val = keep_if(r < len, o[u]);
+        *reinterpret_cast<u32x4*>(role == 0 ? &Qs[r][8 * g] : &Ks[r][8 * g]) = val;
+        if (first_v)
+          *reinterpret_cast<u32x4*>(reinterpret_cast<uint16_t*>(rec + (role == 0 ? kOffQf : kOffKf)) +
+                                    frag_elem(r, 8 * g, DK / 32)) = val;
+      }
+    }
+    {
+      u32x4 o[4];
+      conv_run<WDT, 4, false>(p, cp, 2 * p.Hk * DK + hv * DV + 8 * g, t0, 1.0f, o);
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        if (t0 + u < len)
+          *reinterpret_cast<u32x4*>(p.v_out + ((tok0 + t0 + u) * p.Hv + hv) * DV + 8 * g) = o[u];
+    }
+    if (cp.ci == n_chunks(cp.seq_len) - 1)
+      conv_state_rows(p, cp.seq, cp.seq_tok0, cp.seq_len, hk, hv, first_v, tid);
   }
   __syncthreads();
 
@@ -957,6 +1137,15 @@ extern "C" size_t gdn_chunk_workspace_bytes(int64_t n_seqs, int64_t n_tok, int64
   return record_bytes(n_seqs, n_tok, Hv) + order;
 }
 
+// The fused conv prologue's workspace: gdn_chunk_fwd's, then the v rows the
+// prep writes for the scan ([n_tok][Hv][Dv] bf16).
+extern "C" size_t gdn_chunk_conv_workspace_bytes(int64_t n_seqs, int64_t n_tok, int64_t Hv, int64_t Dk,
+                                                 int64_t Dv, int64_t chunk) {
+  const size_t base = gdn_chunk_workspace_bytes(n_seqs, n_tok, Hv, Dk, Dv, chunk);
+  if (base == 0 && !(n_seqs == 0 && chunk == CH && Dk == DK && Dv == DV && n_tok >= 0 && Hv > 0)) return 0;
+  return base + (static_cast<size_t>(n_tok) * Hv * DV * 2 + 255) / 256 * 256;
+}
+
 // ------------------------------------------------ no-allocation entry point
 //
 // gdn_chunk_fwd with the chunk records in a file-scope device array instead
@@ -1013,6 +1202,19 @@ size_t record_bytes(int64_t n_seqs, int64_t n_tok, int64_t Hv) {
 
 constexpr unsigned kPhasePrep = 1, kPhaseScan = 2;
 
+// The conv prologue's arguments, for the prep that fuses it (as in
+// gdn_conv_prologue: qkv rows of C = 2 Hk Dk + Hv Dv bf16 channels,
+// qkv_stride elements apart; taps [C][4]; conv states [n_seqs][3][C] bf16).
+struct ConvArgs {
+  const void* qkv;
+  int64_t qkv_stride;
+  const void* w;
+  int w_dtype;
+  const void* cs_in;
+  void* cs_out;
+  float eps;
+};
+
 // Validates the arguments and enqueues the phases selected by `phases`
 // (the same checks for every phase, so a prep and a scan issued separately
 // with the same arguments see the same records).  With `use_scratch` the
@@ -1023,7 +1225,7 @@ int chunk_fwd(const void* q, const void* k, const void* v, int qkv_dtype, int ga
               int param_dtype, const float* state_in, void* y, float* state_out, const int32_t* state_index,
               int64_t n_slots, const int32_t* cu_seqlens, int64_t n_seqs, int64_t n_tok, int64_t Hk, int64_t Hv,
               int64_t Dk, int64_t Dv, int64_t chunk, void* workspace, size_t workspace_bytes, void* stream,
-              unsigned phases, bool use_scratch = false) {
+              unsigned phases, bool use_scratch = false, const ConvArgs* conv = nullptr) {
   using gdn_host::fail;
   if (chunk != CH) return fail(GDN_ERR_UNSUPPORTED, "gdn_chunk_fwd: chunk must be 64 (got %lld)", (long long)chunk);
   if (qkv_dtype != GDN_DTYPE_BF16) return fail(GDN_ERR_UNSUPPORTED, "gdn_chunk_fwd: q/k/v must be bf16");
@@ -1041,8 +1243,24 @@ int chunk_fwd(const void* q, const void* k, const void* v, int qkv_dtype, int ga
   if (!packed && n_seqs > 0 && n_tok % n_seqs != 0)
     return fail(GDN_ERR_INVALID, "gdn_chunk_fwd: n_tok=%lld is not n_seqs=%lld rows of equal length",
                 (long long)n_tok, (long long)n_seqs);
-  if (n_tok > 0 && (!q || !k || !v || !gx || !gy || !y))
+  if (n_tok > 0 && ((conv == nullptr && (!q || !k || !v)) || !gx || !gy || !y))
     return fail(GDN_ERR_INVALID, "gdn_chunk_fwd: q, k, v, gates and y are required");
+  const int64_t C = 2 * Hk * DK + Hv * DV;
+  if (conv != nullptr) {
+    if ((n_tok > 0 && !conv->qkv) || !conv->w)
+      return fail(GDN_ERR_INVALID, "gdn_chunk_fwd_conv: qkv and the conv weight are required");
+    if (conv->w_dtype != GDN_DTYPE_BF16 && conv->w_dtype != GDN_DTYPE_F32)
+      return fail(GDN_ERR_UNSUPPORTED, "gdn_chunk_fwd_conv: the conv weight must be bf16 or fp32");
+    if (conv->qkv_stride != 0 && (conv->qkv_stride < C || conv->qkv_stride % 8 != 0))
+      return fail(GDN_ERR_INVALID, "gdn_chunk_fwd_conv: qkv_stride=%lld must be >= C=%lld and a multiple of 8",
+                  (long long)conv->qkv_stride, (long long)C);
+    if (conv->cs_out != nullptr && conv->cs_out == conv->cs_in)
+      return fail(GDN_ERR_INVALID, "gdn_chunk_fwd_conv: conv_state_out must not alias conv_state_in");
+    if (!(conv->eps >= 0.0f)) return fail(GDN_ERR_INVALID, "gdn_chunk_fwd_conv: eps must be >= 0");
+    if (!gdn_host::aligned(conv->qkv, 16) || !gdn_host::aligned(conv->w, 16) ||
+        !gdn_host::aligned(conv->cs_in, 16) || !gdn_host::aligned(conv->cs_out, 16))
+      return fail(GDN_ERR_INVALID, "gdn_chunk_fwd_conv: misaligned pointer");
+  }
   if (!state_out) return fail(GDN_ERR_INVALID, "gdn_chunk_fwd: state_out is required");
   if (gate_stride != 0 && gate_stride < Hv)
     return fail(GDN_ERR_INVALID, "gdn_chunk_fwd: gate_stride=%lld is below Hv=%lld", (long long)gate_stride,
@@ -1050,7 +1268,8 @@ int chunk_fwd(const void* q, const void* k, const void* v, int qkv_dtype, int ga
   if (state_index != nullptr && (n_slots < 0 || n_slots > INT32_MAX))
     return fail(GDN_ERR_INVALID, "gdn_chunk_fwd: n_slots=%lld out of range", (long long)n_slots);
   if (n_seqs == 0) return GDN_OK;
-  const size_t need = gdn_chunk_workspace_bytes(n_seqs, n_tok, Hv, Dk, Dv, chunk);
+  const size_t need = conv != nullptr ? gdn_chunk_conv_workspace_bytes(n_seqs, n_tok, Hv, Dk, Dv, chunk)
+                                      : gdn_chunk_workspace_bytes(n_seqs, n_tok, Hv, Dk, Dv, chunk);
   if (use_scratch) {
     if (need > kScratchBytes)
       return fail(GDN_ERR_UNSUPPORTED,
@@ -1061,9 +1280,9 @@ int chunk_fwd(const void* q, const void* k, const void* v, int qkv_dtype, int ga
     return fail(GDN_ERR_INVALID, "gdn_chunk_fwd: workspace of %zu bytes is below the %zu needed", workspace_bytes,
                 need);
   }
-  if ((!use_scratch && !gdn_host::aligned(workspace, 256)) || !gdn_host::aligned(q, 16) ||
-      !gdn_host::aligned(k, 16) || !gdn_host::aligned(v, 16) || !gdn_host::aligned(state_in, 16) ||
-      !gdn_host::aligned(state_out, 16))
+  if ((!use_scratch && !gdn_host::aligned(workspace, 256)) ||
+      (conv == nullptr && (!gdn_host::aligned(q, 16) || !gdn_host::aligned(k, 16) || !gdn_host::aligned(v, 16))) ||
+      !gdn_host::aligned(state_in, 16) || !gdn_host::aligned(state_out, 16))
     return fail(GDN_ERR_INVALID, "gdn_chunk_fwd: misaligned pointer");
   if (n_tok > INT32_MAX / 2 || n_seqs > 65535 || Hv > 65535 || max_chunks(n_seqs, n_tok, packed) * Hv >= INT32_MAX ||
       (DV / DVT) * (Hv * n_seqs + 8 * (Hv / Hk)) > INT32_MAX)
@@ -1099,17 +1318,54 @@ int chunk_fwd(const void* q, const void* k, const void* v, int qkv_dtype, int ga
   p.group = static_cast<int>(Hv / Hk);
   p.ws = static_cast<unsigned char*>(workspace);
   p.order = packed && ordered(n_seqs) ? reinterpret_cast<int32_t*>(p.ws + record_bytes(n_seqs, n_tok, Hv)) : nullptr;
+  p.qkv = nullptr;
+  p.conv_w = nullptr;
+  p.cs_in = nullptr;
+  p.cs_out = nullptr;
+  p.v_out = nullptr;
+  p.qkv_ld = 0;
+  p.C = static_cast<int>(C);
+  p.conv_eps = 0.0f;
+  if (conv != nullptr) {
+    // v rows after the records and the order table; the scan reads them as p.v
+    p.v_out = reinterpret_cast<uint16_t*>(p.ws + gdn_chunk_workspace_bytes(n_seqs, n_tok, Hv, Dk, Dv, chunk));
+    p.v = p.v_out;
+    p.q = p.k = nullptr;
+    p.qkv = static_cast<const uint16_t*>(conv->qkv);
+    p.qkv_ld = conv->qkv_stride > 0 ? conv->qkv_stride : C;
+    p.conv_w = conv->w;
+    p.cs_in = static_cast<const uint16_t*>(conv->cs_in);
+    p.cs_out = static_cast<uint16_t*>(conv->cs_out);
+    p.conv_eps = conv->eps;
+  }
 
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int64_t chunks = max_chunks(n_seqs, n_tok, packed);
+  if (conv != nullptr && chunks == 0 && (phases & kPhasePrep)) {
+    // rows of no tokens: the prologue alone passes the conv states through
+    // (it writes no q, k or v; the workspace stands in for them)
+    const void* qkv = conv->qkv != nullptr ? conv->qkv : workspace;  // not read without tokens
+    const int rc = gdn_conv_prologue(qkv, GDN_DTYPE_BF16, conv->qkv_stride, conv->cs_in, conv->w,
+                                     conv->w_dtype, nullptr, nullptr, workspace, workspace, workspace, conv->cs_out,
+                                     n_seqs, 0, Hk, Hv, Dk, Dv, KTAP, conv->eps, stream);
+    if (rc != GDN_OK) return rc;
+  }
   // More scan workgroups than CUs (several per CU): K^T from LDS (fewer
   // operand bytes per CU); else the record's K^T (a shorter chain per chunk).
   const bool kt_lds = static_cast<int64_t>(kTiles) * n_seqs * Hv > kCUs;
   if ((phases & kPhasePrep) && chunks > 0) {
     // one workgroup per (chunk slot, v-head), and one more that orders packed sequences
     const dim3 grid(static_cast<unsigned>(chunks * Hv + (p.order != nullptr ? 1 : 0)));
-    if (kt_lds) hipLaunchKernelGGL(chunk_prep_kernel<true>, grid, dim3(256), 0, st, p);
-    else hipLaunchKernelGGL(chunk_prep_kernel<false>, grid, dim3(256), 0, st, p);
+    const int cv = conv == nullptr ? 0 : (conv->w_dtype == GDN_DTYPE_F32 ? 2 : 1);
+    if (kt_lds) {
+      if (cv == 0) hipLaunchKernelGGL((chunk_prep_kernel<true, 0>), grid, dim3(256), 0, st, p);
+      else if (cv == 1) hipLaunchKernelGGL((chunk_prep_kernel<true, 1>), grid, dim3(256), 0, st, p);
+      else hipLaunchKernelGGL((chunk_prep_kernel<true, 2>), grid, dim3(256), 0, st, p);
+    } else {
+      if (cv == 0) hipLaunchKernelGGL((chunk_prep_kernel<false, 0>), grid, dim3(256), 0, st, p);
+      else if (cv == 1) hipLaunchKernelGGL((chunk_prep_kernel<false, 1>), grid, dim3(256), 0, st, p);
+      else hipLaunchKernelGGL((chunk_prep_kernel<false, 2>), grid, dim3(256), 0, st, p);
+    }
     const int rc = gdn_host::check_launch("gdn_chunk_fwd/prep");
     if (rc != GDN_OK) return rc;
   }
@@ -1148,6 +1404,20 @@ extern "C" int gdn_chunk_fwd(GDN_CHUNK_PARAMS) { return chunk_fwd(GDN_CHUNK_ARGS
 extern "C" int gdn_chunk_prep(GDN_CHUNK_PARAMS) { return chunk_fwd(GDN_CHUNK_ARGS, kPhasePrep); }
 
 extern "C" int gdn_chunk_scan(GDN_CHUNK_PARAMS) { return chunk_fwd(GDN_CHUNK_ARGS, kPhaseScan); }
+
+extern "C" int gdn_chunk_fwd_conv(const void* qkv, int64_t qkv_stride, const void* conv_w, int conv_w_dtype,
+                                  const void* conv_state_in, void* conv_state_out, float eps, int gate_mode,
+                                  const void* gx, const void* gy, int gate_dtype, int64_t gate_stride,
+                                  const void* A_log, const void* dt_bias, int param_dtype, const float* state_in,
+                                  void* y, float* state_out, const int32_t* state_index, int64_t n_slots,
+                                  const int32_t* cu_seqlens, int64_t n_seqs, int64_t n_tok, int64_t Hk, int64_t Hv,
+                                  int64_t Dk, int64_t Dv, int64_t chunk, void* workspace, size_t workspace_bytes,
+                                  void* stream) {
+  const ConvArgs conv{qkv, qkv_stride, conv_w, conv_w_dtype, conv_state_in, conv_state_out, eps};
+  return chunk_fwd(nullptr, nullptr, nullptr, GDN_DTYPE_BF16, gate_mode, gx, gy, gate_dtype, gate_stride, A_log,
+                   dt_bias, param_dtype, state_in, y, state_out, state_index, n_slots, cu_seqlens, n_seqs, n_tok, Hk,
+                   Hv, Dk, Dv, chunk, workspace, workspace_bytes, stream, kPhasePrep | kPhaseScan, false, &conv);
+}
 
 extern "C" int gdn_chunk_fwd_noalloc(const void* q, const void* k, const void* v, int qkv_dtype, int gate_mode,
                                      const void* gx, const void* gy, int gate_dtype, int64_t gate_stride,

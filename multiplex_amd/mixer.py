@@ -13,7 +13,10 @@ Data path per call:
   in_proj_qkv / z / b / a      one library GEMM (hipBLASLt through torch); the
                                kernels below read its column slices in place
   gdn_conv_prologue            fused conv1d + SiLU + q/k norm (HIP)
-  gated_delta_update           recurrent or chunked kernel (HIP)
+  gated_delta_update           recurrent or chunked kernel (HIP); where the
+                               chunked kernel runs (long unmasked rows) the
+                               prologue is fused into its prep instead
+                               (``gdn_conv_chunked``)
   norm(out, z) + out_proj      up to 16 rows (decode of up to 16 rows) one
                                ``gdn_linear_decode`` launch with the gated
                                RMSNorm in its operand load (HIP); else the
@@ -37,10 +40,10 @@ from typing import Optional, Sequence
 import torch
 
 from .cache import ArraysCache
-from .conv import conv_state_commit, gdn_conv_prologue
+from .conv import conv_state_commit, gdn_conv_chunked, gdn_conv_prologue
 from .epilogue import gated_rms_norm
 from .state_pool import PooledBatch
-from .gated_delta import IntSeq, gated_delta_commit, gated_delta_update, gated_delta_verify
+from .gated_delta import CHUNK_MIN_TOKENS, IntSeq, gated_delta_commit, gated_delta_update, gated_delta_verify
 from .linear import FUSED_NORM_MAX_ROWS, DecodeWorkspace, decode_shape_ok, gated_norm_linear_decode
 
 __all__ = ["GatedDeltaNet", "gated_rms_norm", "commit_verified"]
@@ -175,6 +178,14 @@ class GatedDeltaNet(torch.nn.Module):
         out = gated_rms_norm(y, z, self.norm_weight, self.rms_norm_eps, out=y)
         return self.out_proj(out.reshape(B, S, -1))
 
+    def _fused_prefill(self, qkv: torch.Tensor, mask) -> bool:
+        """Whether a call takes the chunked kernel (``gated_delta_update``'s
+        default rule: unmasked bf16 rows of at least ``CHUNK_MIN_TOKENS``
+        tokens at 128-wide heads), with a 4-tap conv to fuse into it."""
+        return (mask is None and qkv.dtype == torch.bfloat16 and qkv.shape[1] >= CHUNK_MIN_TOKENS
+                and self.head_k_dim == 128 and self.head_v_dim == 128 and self.conv_kernel_size == 4
+                and self.conv1d_weight.dtype in (torch.bfloat16, torch.float32))
+
     def forward(self, inputs: torch.Tensor, mask: Optional[torch.Tensor] = None,
                 cache: Optional[ArraysCache] = None, *, verify: bool = False) -> torch.Tensor:
         """``inputs [B, S, hidden]`` -> ``[B, S, hidden]``; updates ``cache`` unless ``verify``."""
@@ -183,10 +194,23 @@ class GatedDeltaNet(torch.nn.Module):
         qkv, z, a, b = self._project(inputs)
         conv_state = cache[0] if cache is not None else None
         state = cache[1] if cache is not None else None
+        pooled = isinstance(state, PooledBatch)
+        if not verify and self._fused_prefill(qkv, mask):
+            # long unmasked rows: the conv prologue runs inside the chunked
+            # pass's prep (bit-identical to the two launches below)
+            pool = state.pool.states if pooled else state
+            y, new_state, new_cs = gdn_conv_chunked(
+                qkv, self.conv1d_weight, self.num_k_heads, self.num_v_heads, self.head_k_dim, self.head_v_dim,
+                a, b, self.A_log, self.dt_bias, pool, conv_state, eps=self.rms_norm_eps,
+                state_index=state.index if pooled else None)
+            if cache is not None:
+                cache[0] = new_cs
+                if not pooled:
+                    cache[1] = new_state
+            return self._epilogue(y, z)
         q, k, v, new_cs = gdn_conv_prologue(
             qkv, self.conv1d_weight, self.num_k_heads, self.num_v_heads, self.head_k_dim, self.head_v_dim,
             conv_state, mask, eps=self.rms_norm_eps, write_conv_state=not verify)
-        pooled = isinstance(state, PooledBatch)
         if verify:
             if cache is None:
                 raise ValueError("verify needs the cache the round will be committed into")
