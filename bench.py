@@ -234,7 +234,7 @@ def bench_verify(torch, mx, dev, timer, iters=50):
                       torch.ones(B, T, dtype=torch.bool, device=dev)], dim=1)
     fused = mx.prepare_recurrent(cat["q"], cat["k"], cat["v"], cat["a"], cat["b"], d["A_log"], d["dt_bias"],
                                  d["state"], keep, commit_len=torch.full((B,), T, dtype=torch.int32, device=dev),
-                                 state_out=torch.empty_like(d["state"]))
+                                 state_out=torch.empty_like(d["state"]), y_from=T)
 
     def round_commit(i):
         verify.launch()

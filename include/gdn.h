@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define GDN_ABI_VERSION 3
+#define GDN_ABI_VERSION 4
 
 /* dtype codes for the void* operands */
 #define GDN_DTYPE_F32 0
@@ -138,6 +138,7 @@ typedef struct gdn_recurrent_args {
   int64_t n_slots;           /* pool size when state_index != NULL */
   int64_t gate_stride;       /* elements between tokens' gate rows (0 = Hv) */
   void* stream;
+  int64_t y_from;            /* tokens before it produce no y (not written); 0 = all */
 } gdn_recurrent_args;
 
 int gdn_recurrent(const gdn_recurrent_args* args);

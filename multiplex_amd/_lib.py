@@ -13,7 +13,7 @@ from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libgdn.so"
 
-GDN_ABI_VERSION = 3
+GDN_ABI_VERSION = 4
 
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
@@ -86,6 +86,7 @@ class RecurrentArgs(Structure):
         ("n_slots", c_int64),
         ("gate_stride", c_int64),
         ("stream", c_void_p),
+        ("y_from", c_int64),
     ]
 
 

@@ -61,6 +61,7 @@ struct RecParams {
   const uint8_t* mask;
   const int32_t* cu_seqlens;
   const int32_t* commit_len;
+  int y_from;  // tokens before it produce no y (tile kernel)
 };
 
 // A state row of Dk floats is spread over LPR lanes: lane `sub` holds the
@@ -457,6 +458,7 @@ __global__ __launch_bounds__(kTileThreads) void recurrent_tile_kernel(const RecP
   ea = GF == GF_ANY && p.ga.mode == GDN_GATES_PRE ? 0.0f : exp_fast(al);
   if (c.write_state && c.commit == 0 && c.row_ok) store_row<EPL>(p.state_out + c.srow, c.sub, s);
 
+  const int rloc = threadIdx.x / kLanesPerRow;
   for (int t0 = 0; t0 < c.steps; t0 += TILE) {
     const int n = min(TILE, c.steps - t0);
     if (t0 > 0) {
@@ -466,10 +468,10 @@ __global__ __launch_bounds__(kTileThreads) void recurrent_tile_kernel(const RecP
     store_tile();
     __syncthreads();
 
-    const int rloc = threadIdx.x / kLanesPerRow;
     for (int j = 0; j < n; ++j) {
       const int t = t0 + j;
       const int64_t tok = c.tok0 + t;
+      const bool y_here = c.want_y && t >= p.y_from;
       float yv = 0.0f;
       if (Mt[j] != 0) {
         float kf[EPL];
@@ -482,7 +484,7 @@ __global__ __launch_bounds__(kTileThreads) void recurrent_tile_kernel(const RecP
           kf[4 * i + 3] = x.w;
         }
         step_row<EPL>(s, kf, Vt[j][rloc], Gt[j], Bt[j]);
-        if (c.want_y) {
+        if (y_here) {
           float qf[EPL];
 #pragma unroll
           for (int i = 0; i < NV; ++i) {
@@ -495,7 +497,7 @@ __global__ __launch_bounds__(kTileThreads) void recurrent_tile_kernel(const RecP
           yv = row_dot<EPL, kLanesPerRow>(s, qf);
         }
       }
-      if (c.want_y && c.row_ok && c.sub == 0) IO<DT>::store1(p.y, (tok * p.Hv + c.hv) * p.Dv + c.dv, yv);
+      if (y_here && c.row_ok && c.sub == 0) IO<DT>::store1(p.y, (tok * p.Hv + c.hv) * p.Dv + c.dv, yv);
       if (p.snapshots != nullptr && c.row_ok) {
         store_row<EPL>(p.snapshots + ((tok * p.Hv + c.hv) * p.Dv + c.dv) * DK, c.sub, s);
       }
@@ -1001,6 +1003,8 @@ int run_recurrent(const gdn_recurrent_args* a) {
                 (long long)a->Hv);
   if (a->state_index != nullptr && (a->n_slots < 0 || a->n_slots > INT32_MAX))
     return fail(GDN_ERR_INVALID, "gdn_recurrent: n_slots=%lld out of range", (long long)a->n_slots);
+  if (a->y_from < 0 || (a->y_from > 0 && (a->y == nullptr || a->y_from > a->T)))
+    return fail(GDN_ERR_INVALID, "gdn_recurrent: y_from=%lld must be in [0, T] and needs y", (long long)a->y_from);
   if (a->B == 0) return GDN_OK;
   if (a->T > INT32_MAX) return fail(GDN_ERR_UNSUPPORTED, "gdn_recurrent: T too large");
 
@@ -1023,6 +1027,7 @@ int run_recurrent(const gdn_recurrent_args* a) {
   p.mask = a->mask;
   p.cu_seqlens = a->cu_seqlens;
   p.commit_len = a->commit_len;
+  p.y_from = static_cast<int>(a->y_from);
   p.state_index = a->state_index;
   p.n_slots = a->state_index != nullptr ? static_cast<int>(a->n_slots) : 0;
   p.T = static_cast<int>(a->T);
@@ -1046,9 +1051,10 @@ int run_recurrent(const gdn_recurrent_args* a) {
   // workgroups of 4 waves.
   // A verify of a few tokens without state writes or snapshots: the
   // unrolled form (verify_wy_kernel), same 32-row workgroups.
+  // (y_from > 0 takes the tile kernel: only it leaves tokens without y)
   const bool verify = a->state_out == nullptr && a->snapshots == nullptr && a->y != nullptr &&
                       a->cu_seqlens == nullptr && a->commit_len == nullptr && a->T >= 1 &&
-                      a->T <= kVerifyMaxT;
+                      a->T <= kVerifyMaxT && a->y_from == 0;
   // The decode kernel indexes in 32 bits: state rows (pool slots or B, times
   // Hv*Dv), q/k/v/y elements and gate entries must stay below 2^31 (and the
   // group below 2^15, for its division); larger launches take the tile
@@ -1057,7 +1063,7 @@ int run_recurrent(const gdn_recurrent_args* a) {
   const bool idx32 = state_rows < (int64_t{1} << 31) && a->B * a->Hv * a->Dv < (int64_t{1} << 31) &&
                      a->B * a->Hk * a->Dk < (int64_t{1} << 31) && a->B * p.ga.ld < (int64_t{1} << 31) &&
                      p.group < (1 << 15);
-  const bool pf = a->T > 1 || a->cu_seqlens != nullptr || !idx32;
+  const bool pf = a->T > 1 || a->cu_seqlens != nullptr || !idx32 || a->y_from > 0;
   const int kind = verify ? K_VERIFY : (pf ? K_TILE : K_DECODE);
   // the tile and verify kernels assume workgroups of 4 waves (32 rows)
   const bool four = kind != K_DECODE;

@@ -357,7 +357,7 @@ def gated_delta_ops(q, k, v, g, beta, state=None, mask=None):
 
 def _recurrent(q, k, v, gx, gy, gate_mode, A_log, dt_bias, state, mask, *,
                y=True, state_out=None, write_state=True, snapshots=False,
-               cu_seqlens=None, commit_len=None, state_index=None):
+               cu_seqlens=None, commit_len=None, state_index=None, y_from=0):
     names = ["q", "k", "v", "a/g", "b/beta", "A_log", "dt_bias", "state", "mask", "state_out"]
     dev = _require_device([q, k, v, gx, gy, A_log, dt_bias, state, mask, state_out], names)
     packed = cu_seqlens is not None
@@ -389,6 +389,7 @@ def _recurrent(q, k, v, gx, gy, gate_mode, A_log, dt_bias, state, mask, *,
         state_out=_ptr(out_state), snapshots=_ptr(snaps), y=_ptr(y_t), mask=_ptr(mask_u8),
         cu_seqlens=_ptr(cu), commit_len=_ptr(commit), state_index=_ptr(idx), B=n_rows, T=sh.T, Hk=sh.Hk,
         Hv=sh.Hv, Dk=sh.Dk, Dv=sh.Dv, n_slots=n_slots, gate_stride=g_ld, stream=_stream(dev),
+        y_from=int(y_from),
     )
     with torch.cuda.device(dev):
         _lib.call("gdn_recurrent", _lib.ctypes.byref(args))
@@ -428,8 +429,11 @@ class PreparedRecurrent:
 
 def prepare_recurrent(q, k, v, a, b, A_log, dt_bias, state, mask=None, *, y=True, state_out=None,
                       write_state=True, snapshots=False, commit_len=None, cu_seqlens=None,
-                      gates_precomputed=False, state_index=None) -> PreparedRecurrent:
-    """Validates once and returns a :class:`PreparedRecurrent` (same arguments as the entry points)."""
+                      gates_precomputed=False, state_index=None, y_from=0) -> PreparedRecurrent:
+    """Validates once and returns a :class:`PreparedRecurrent` (same arguments as the entry points).
+
+    ``y_from``: tokens before it produce no y (their rows of y are left unwritten).
+    """
     mode = _lib.GATES_PRE if gates_precomputed else _lib.GATES_RAW
     names = ["q", "k", "v", "a/g", "b/beta", "A_log", "dt_bias", "state", "mask", "state_out"]
     dev = _require_device([q, k, v, a, b, A_log, dt_bias, state, mask, state_out], names)
@@ -463,6 +467,7 @@ def prepare_recurrent(q, k, v, a, b, A_log, dt_bias, state, mask=None, *, y=True
         state_out=_ptr(out_state), snapshots=_ptr(snaps), y=_ptr(y_t), mask=_ptr(mask_u8),
         cu_seqlens=_ptr(cu), commit_len=_ptr(commit), state_index=_ptr(idx), B=n_rows, T=sh.T, Hk=sh.Hk,
         Hv=sh.Hv, Dk=sh.Dk, Dv=sh.Dv, n_slots=n_slots, gate_stride=g_ld, stream=_stream(dev),
+        y_from=int(y_from),
     )
     keep = dict(q=q, k=k, v=v, a=a, b=b, A_log=A_log, dt_bias=dt_bias, state=state, mask=mask_u8,
                 cu=cu, commit=commit, y=y_t, state_out=out_state, snapshots=snaps, state_index=idx)
@@ -731,6 +736,8 @@ def gated_delta_commit_verify(prev, n_prev: IntSeq, q, k, v, a, b, A_log, dt_bia
     new = torch.ones(B, k.shape[1], dtype=torch.bool, device=dev) if mask is None else mask.to(dev, torch.bool)
     cat = [torch.cat([x0, x1], dim=1) for x0, x1 in ((qp, q), (kp, k), (vp, v), (ap, a), (bp, b))]
     commit = torch.full((B,), Tp, dtype=torch.int32, device=dev)
+    # the previous tokens' y is not wanted: they are only stepped (to the
+    # committed state), and the new ones take y from it unrolled
     y, s, _ = _recurrent(*cat, _lib.GATES_RAW, A_log, dt_bias, state, torch.cat([keep, new], dim=1),
-                         state_out=state_out, commit_len=commit, state_index=state_index)
+                         state_out=state_out, commit_len=commit, state_index=state_index, y_from=Tp)
     return y[:, Tp:], s

@@ -37,15 +37,16 @@ def test_exports_match_header(lib):
 
 
 def test_abi_version(lib):
-    assert lib.gdn_abi_version() == _lib.GDN_ABI_VERSION == 3
+    assert lib.gdn_abi_version() == _lib.GDN_ABI_VERSION == 4
 
 
 def test_struct_layout_matches_header():
-    # gdn_recurrent_args: 28 fields; pointers 8 B, int32 fields packed in pairs.
-    assert ctypes.sizeof(_lib.RecurrentArgs) == 8 * 3 + 4 * 2 + 8 * 2 + 4 * 2 + 8 * 10 + 8 * 6 + 8 + 8 + 8
+    # gdn_recurrent_args: 29 fields; pointers 8 B, int32 fields packed in pairs.
+    assert ctypes.sizeof(_lib.RecurrentArgs) == 8 * 3 + 4 * 2 + 8 * 2 + 4 * 2 + 8 * 10 + 8 * 6 + 8 + 8 + 8 + 8
     assert _lib.RecurrentArgs.state_index.offset == _lib.RecurrentArgs.commit_len.offset + 8
     assert _lib.RecurrentArgs.n_slots.offset == _lib.RecurrentArgs.Dv.offset + 8
     assert _lib.RecurrentArgs.gate_stride.offset == _lib.RecurrentArgs.n_slots.offset + 8
+    assert _lib.RecurrentArgs.y_from.offset == _lib.RecurrentArgs.stream.offset + 8
 
 
 def _update(lib, **kw):
@@ -149,6 +150,15 @@ def test_recurrent_rejects_bad_pool_size(lib):
                            state_out=FAKE, state_index=FAKE, n_slots=-3, B=1, T=1, Hk=1, Hv=1, Dk=128, Dv=128)
     assert lib.gdn_recurrent(ctypes.byref(a)) == _lib.ERR_INVALID
     assert "n_slots" in _lib.last_error()
+
+
+def test_recurrent_rejects_bad_y_from(lib):
+    base = dict(q=FAKE, k=FAKE, v=FAKE, gx=FAKE, gy=FAKE, gate_mode=_lib.GATES_PRE, B=1, T=4, Hk=1, Hv=1, Dk=128,
+                Dv=128)
+    for bad in (dict(y=FAKE, y_from=5), dict(y=FAKE, y_from=-1), dict(y_from=2)):  # past T, negative, no y
+        a = _lib.RecurrentArgs(**base, **bad)
+        assert lib.gdn_recurrent(ctypes.byref(a)) == _lib.ERR_INVALID
+        assert "y_from" in _lib.last_error()
 
 
 def test_workspace_size_is_monotone(lib):

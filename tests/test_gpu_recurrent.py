@@ -377,6 +377,23 @@ def test_ops_path_on_device_matches_kernel():
     assert rel_err(S1.cpu().numpy(), S2.cpu().numpy()) < 1e-5
 
 
+@pytest.mark.parametrize("T,y_from", [(8, 4), (4, 1), (16, 9)])
+def test_y_from_leaves_earlier_tokens_out_and_the_rest_bit_identical(T, y_from):
+    """``y_from``: tokens before it produce no y; the state and the later
+    tokens' y equal the launch that forms every y, bit for bit."""
+    d = draw(700 + T, 3, T, 2, 4, 128, 128, mask_p=0.25)
+    t, _ = to_torch(d, DEV)
+    n = torch.tensor([T // 2, T, 1], dtype=torch.int32, device=DEV)
+    args = (t["q"], t["k"], t["v"], t["a"], t["b"], t["A_log"], t["dt_bias"], t["state"], t["mask"])
+    full = mx.prepare_recurrent(*args, commit_len=n, state_out=torch.empty_like(t["state"]))
+    part = mx.prepare_recurrent(*args, commit_len=n, state_out=torch.empty_like(t["state"]), y_from=y_from)
+    full.launch()
+    part.launch()
+    torch.cuda.synchronize()
+    assert torch.equal(part.outputs[1], full.outputs[1])
+    assert torch.equal(part.outputs[0][:, y_from:], full.outputs[0][:, y_from:])
+
+
 @pytest.mark.parametrize("Tp,T", [(4, 4), (3, 5), (1, 1), (4, 6)])
 def test_commit_verify_is_commit_then_verify(Tp, T):
     """One pass over the state: the commit of the previous round's accepted
