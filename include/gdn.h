@@ -153,8 +153,9 @@ int gdn_recurrent(const gdn_recurrent_args* args);
  * state_out may alias state_in.  state_index [n_seqs] int32 or NULL:
  * pooled states as in gdn_recurrent_args (state_in / state_out are pools of
  * n_slots states; sequence n uses slot state_index[n]; out-of-range slots
- * are skipped).  gate_stride as in gdn_recurrent_args.  No mask.  chunk
- * must be 64.
+ * are skipped).  gate_stride as in gdn_recurrent_args.  mask [n_tok] uint8 or
+ * NULL: a token whose byte is 0 keeps the state and its y is 0 (as in
+ * gdn_recurrent).  chunk must be 64.
  * workspace must hold gdn_chunk_workspace_bytes(...) bytes (256-B aligned).
  */
 size_t gdn_chunk_workspace_bytes(int64_t n_seqs, int64_t n_tok, int64_t Hv,
@@ -164,7 +165,7 @@ int gdn_chunk_fwd(const void* q, const void* k, const void* v, int qkv_dtype,
                   int gate_mode, const void* gx, const void* gy, int gate_dtype,
                   int64_t gate_stride,
                   const void* A_log, const void* dt_bias, int param_dtype,
-                  const float* state_in, void* y, float* state_out,
+                  const uint8_t* mask, const float* state_in, void* y, float* state_out,
                   const int32_t* state_index, int64_t n_slots,
                   const int32_t* cu_seqlens, int64_t n_seqs, int64_t n_tok,
                   int64_t Hk, int64_t Hv, int64_t Dk, int64_t Dv, int64_t chunk,
@@ -186,7 +187,7 @@ int gdn_chunk_prep(const void* q, const void* k, const void* v, int qkv_dtype,
                    int gate_mode, const void* gx, const void* gy, int gate_dtype,
                    int64_t gate_stride,
                    const void* A_log, const void* dt_bias, int param_dtype,
-                   const float* state_in, void* y, float* state_out,
+                   const uint8_t* mask, const float* state_in, void* y, float* state_out,
                    const int32_t* state_index, int64_t n_slots,
                    const int32_t* cu_seqlens, int64_t n_seqs, int64_t n_tok,
                    int64_t Hk, int64_t Hv, int64_t Dk, int64_t Dv, int64_t chunk,
@@ -195,7 +196,7 @@ int gdn_chunk_scan(const void* q, const void* k, const void* v, int qkv_dtype,
                    int gate_mode, const void* gx, const void* gy, int gate_dtype,
                    int64_t gate_stride,
                    const void* A_log, const void* dt_bias, int param_dtype,
-                   const float* state_in, void* y, float* state_out,
+                   const uint8_t* mask, const float* state_in, void* y, float* state_out,
                    const int32_t* state_index, int64_t n_slots,
                    const int32_t* cu_seqlens, int64_t n_seqs, int64_t n_tok,
                    int64_t Hk, int64_t Hv, int64_t Dk, int64_t Dv, int64_t chunk,
@@ -253,7 +254,8 @@ int gdn_chunk_fwd_noalloc(const void* q, const void* k, const void* v, int qkv_d
                           int gate_mode, const void* gx, const void* gy, int gate_dtype,
                           int64_t gate_stride,
                           const void* A_log, const void* dt_bias, int param_dtype,
-                          const float* state_in, void* y, float* state_out,
+                          const uint8_t* mask, const float* state_in, void* y,
+                          float* state_out,
                           const int32_t* state_index, int64_t n_slots,
                           const int32_t* cu_seqlens, int64_t n_seqs, int64_t n_tok,
                           int64_t Hk, int64_t Hv, int64_t Dk, int64_t Dv, int64_t chunk,

@@ -121,22 +121,22 @@ _SIGNATURES = {
     "gdn_chunk_workspace_bytes": (c_size_t, [_I64, _I64, _I64, _I64, _I64, _I64]),
     "gdn_chunk_fwd": (
         c_int,
-        [_P, _P, _P, c_int, c_int, _P, _P, c_int, _I64, _P, _P, c_int, _P, _P, _P, _P, _I64, _P,
+        [_P, _P, _P, c_int, c_int, _P, _P, c_int, _I64, _P, _P, c_int, _P, _P, _P, _P, _P, _I64, _P,
          _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P, c_size_t, _P],
     ),
     "gdn_chunk_prep": (
         c_int,
-        [_P, _P, _P, c_int, c_int, _P, _P, c_int, _I64, _P, _P, c_int, _P, _P, _P, _P, _I64, _P,
+        [_P, _P, _P, c_int, c_int, _P, _P, c_int, _I64, _P, _P, c_int, _P, _P, _P, _P, _P, _I64, _P,
          _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P, c_size_t, _P],
     ),
     "gdn_chunk_scan": (
         c_int,
-        [_P, _P, _P, c_int, c_int, _P, _P, c_int, _I64, _P, _P, c_int, _P, _P, _P, _P, _I64, _P,
+        [_P, _P, _P, c_int, c_int, _P, _P, c_int, _I64, _P, _P, c_int, _P, _P, _P, _P, _P, _I64, _P,
          _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P, c_size_t, _P],
     ),
     "gdn_chunk_fwd_noalloc": (
         c_int,
-        [_P, _P, _P, c_int, c_int, _P, _P, c_int, _I64, _P, _P, c_int, _P, _P, _P, _P, _I64, _P,
+        [_P, _P, _P, c_int, c_int, _P, _P, c_int, _I64, _P, _P, c_int, _P, _P, _P, _P, _P, _I64, _P,
          _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P],
     ),
     "gdn_chunk_conv_workspace_bytes": (c_size_t, [_I64, _I64, _I64, _I64, _I64, _I64]),

@@ -63,6 +63,11 @@ constexpr size_t kOffGam = kOffQf + CH * DK * 2;    // float[64]    exp(L_t)
 constexpr size_t kOffE = kOffGam + CH * 4;          // float[64]    exp(L_C - L_t)
 constexpr size_t kOffBeta = kOffE + CH * 4;         // float[64]
 constexpr size_t kRecBytes = kOffBeta + CH * 4;     // 82688 (multiple of 256)
+// float[64] exp(L_t) for y, 0 at a masked token: in fragment 1 of the P hi
+// plane (rows 0-15, columns 32-63: above the diagonal, so never written as
+// P nor read by the scan), which keeps the record at 323 x 256 bytes (a
+// stride of 81 KiB measurably slowed the fused prep).
+constexpr size_t kOffGy = kOffPh + 1024;
 
 // Element offset of (r, c) in the fragment layout of a matrix with ncb
 // 32-column blocks.
@@ -88,6 +93,7 @@ struct ChunkParams {
   int Hk, Hv, group;
   unsigned char* ws;
   int32_t* order;     // [n_seqs] packed sequences longest first (in the workspace), or null
+  const uint8_t* mask;  // [n_tok] token mask (0 = masked: the state is kept, y = 0), or null
   // The conv prologue fused into the prep (chunk_prep_kernel with CONV): q,
   // k and v are formed from the mixed qkv rows; the prep writes v to v_out
   // (p.v points at it, for the scan) and the sequences' new conv states.
@@ -100,6 +106,8 @@ struct ChunkParams {
   int C;                  // qkv channels: 2 Hk DK + Hv DV
   float conv_eps;
 };
+
+typedef __attribute__((address_space(1))) const uint8_t gbl_u8;
 
 // Packed calls of 2..kOrderMax sequences order them by length, so the scan
 // deals the longest chains out first; above that, sequence order.
@@ -422,7 +430,9 @@ __device__ __forceinline__ void wave_lds_sync() {
 // v-head) from the qkv rows with the conv prologue's arithmetic, writes v
 // for the scan and, at a sequence's last chunk, the new conv state; the
 // slot of an empty packed sequence passes its conv state through.
-template <bool KT_LDS, int CONV>
+//
+// MASK: a token mask is given (the unmasked kernels carry none of its code).
+template <bool KT_LDS, int CONV, bool MASK>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void chunk_prep_kernel(const ChunkParams p) {
   // Two 17 KB buffers, each reused once (LDS stays under 40 KB, so four
   // workgroups fit on a CU):  buf0 = K rows, then A;  buf1 = Q rows, then
@@ -461,6 +471,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void c
   __shared__ __align__(16) float Ms[4][16][20];
   __shared__ double Ld[CH];
   __shared__ float Bs[CH];
+  __shared__ float Ys[MASK ? CH : 1];  // 1, or 0 at a masked token (its row of P is zero)
   auto Ks = reinterpret_cast<uint16_t(*)[KP]>(buf0);
   auto Qs = reinterpret_cast<uint16_t(*)[KP]>(buf1);
   auto As = reinterpret_cast<float(*)[CH + 4]>(buf0);
@@ -473,8 +484,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void c
   // the rows (rows past the chunk's end read its last row and are zeroed at
   // the LDS store); the gate transforms only after every load is issued.
   const GateRaw gr = load_gate_raw(p.ga, (tok0 + min(lane, len - 1)) * p.ga.ld + hv, hv);
+  const uint8_t mk = MASK ? *(gbl_u8*)(p.mask + tok0 + min(lane, len - 1)) : 1;
   double L_lane = 0.0;  // wave 0: L_t of token `lane` (its record entries are written last)
   float b_lane = 0.0f;
+  bool on_lane = false;  // wave 0: token `lane` is real and not masked
   asm volatile("" ::: "memory");  // keeps the gate loads issued ahead of the rows
   u32x4 kr[4], qr[4];
   if constexpr (CONV == 0) {
@@ -491,12 +504,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void c
   if (wave == 0) {
     float lg, bt;
     log_gates(p.ga, gr, lg, bt);
-    // padding tokens: no decay, no write; g = 0 (pre-transformed) stays finite
-    lg = lane < len ? fmaxf(lg, -1.0e30f) : 0.0f;
-    bt = lane < len ? bt : 0.0f;
+    // padding and masked tokens: no decay, no write (a masked token keeps
+    // the state and its y is 0); g = 0 (pre-transformed) stays finite
+    on_lane = lane < len && mk != 0;
+    lg = on_lane ? fmaxf(lg, -1.0e30f) : 0.0f;
+    bt = on_lane ? bt : 0.0f;
     L_lane = wave_scan_d(lg);
     Ld[lane] = L_lane;
     Bs[lane] = bt;
+    if constexpr (MASK) Ys[lane] = on_lane ? 1.0f : 0.0f;
     b_lane = bt;
   }
   if constexpr (CONV == 0) {
@@ -593,11 +609,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void c
   // Decays, A (to LDS, fp32) and P (hi/lo bf16, staged in fragment order).
   {
     double Lt[4], Lc[4];
-    float bs[4];
+    float bs[4], ys[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       Lt[i] = Ld[16 * wave + 4 * lq + i];
       bs[i] = Bs[16 * wave + 4 * lq + i];
+      ys[i] = MASK ? Ys[16 * wave + 4 * lq + i] : 1.0f;
       Lc[i] = Ld[16 * i + lr];
     }
 #pragma unroll
@@ -609,7 +626,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void c
         const float dec = col <= t ? __builtin_amdgcn_exp2f(static_cast<float>((Lt[i] - Lc[j]) * kLog2e)) : 0.0f;
         As[t][col] = col < t ? bs[i] * dec * kk[j][i] : 0.0f;
         uint16_t h, l;
-        split_bf16(dec * qk[j][i], h, l);
+        split_bf16(MASK ? (dec * qk[j][i]) * ys[i] : dec * qk[j][i], h, l);
         Pst[frag_elem(t, col, CH / 32)] = h;
         Pst[CH * CH + frag_elem(t, col, CH / 32)] = l;
       }
@@ -721,6 +738,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void c
     reinterpret_cast<float*>(rec + kOffGam)[lane] = expf(static_cast<float>(L_lane));
     reinterpret_cast<float*>(rec + kOffE)[lane] = expf(static_cast<float>(LC - L_lane));
     reinterpret_cast<float*>(rec + kOffBeta)[lane] = b_lane;
+    reinterpret_cast<float*>(rec + kOffGy)[lane] = on_lane ? expf(static_cast<float>(L_lane)) : 0.0f;
   }
 }
 
@@ -852,7 +870,7 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(const ChunkParams p) {
   const uint32_t off_kt = rec_hk + kOffKT + (4 * wave * 64 + lane) * 16;  // K^T rows 32w + 16j + lr
   const uint32_t off_g4 = rec_hv + kOffGam + (16 * wave + 4 * lq) * 4;
   const uint32_t off_gq = off_g4 + (lr & 3) * 4;
-  const uint32_t off_g1 = rec_hv + kOffGam + (16 * wave + lr) * 4;
+  const uint32_t off_g1 = rec_hv + kOffGy + (16 * wave + lr) * 4;
 
   // Bases of the chunk whose descriptors come next, advanced by one chunk at
   // a time (a 64-bit add each) rather than recomputed from the chunk index.
@@ -1222,7 +1240,7 @@ struct ConvArgs {
 // instead of `workspace` (checked against its size before any HIP call).
 int chunk_fwd(const void* q, const void* k, const void* v, int qkv_dtype, int gate_mode, const void* gx,
               const void* gy, int gate_dtype, int64_t gate_stride, const void* A_log, const void* dt_bias,
-              int param_dtype, const float* state_in, void* y, float* state_out, const int32_t* state_index,
+              int param_dtype, const uint8_t* mask, const float* state_in, void* y, float* state_out, const int32_t* state_index,
               int64_t n_slots, const int32_t* cu_seqlens, int64_t n_seqs, int64_t n_tok, int64_t Hk, int64_t Hv,
               int64_t Dk, int64_t Dv, int64_t chunk, void* workspace, size_t workspace_bytes, void* stream,
               unsigned phases, bool use_scratch = false, const ConvArgs* conv = nullptr) {
@@ -1318,6 +1336,7 @@ int chunk_fwd(const void* q, const void* k, const void* v, int qkv_dtype, int ga
   p.group = static_cast<int>(Hv / Hk);
   p.ws = static_cast<unsigned char*>(workspace);
   p.order = packed && ordered(n_seqs) ? reinterpret_cast<int32_t*>(p.ws + record_bytes(n_seqs, n_tok, Hv)) : nullptr;
+  p.mask = mask;
   p.qkv = nullptr;
   p.conv_w = nullptr;
   p.cs_in = nullptr;
@@ -1356,15 +1375,19 @@ int chunk_fwd(const void* q, const void* k, const void* v, int qkv_dtype, int ga
   if ((phases & kPhasePrep) && chunks > 0) {
     // one workgroup per (chunk slot, v-head), and one more that orders packed sequences
     const dim3 grid(static_cast<unsigned>(chunks * Hv + (p.order != nullptr ? 1 : 0)));
+    // (the fused prologue takes no mask: conv != null implies mask == null)
     const int cv = conv == nullptr ? 0 : (conv->w_dtype == GDN_DTYPE_F32 ? 2 : 1);
+    const bool masked = mask != nullptr;
     if (kt_lds) {
-      if (cv == 0) hipLaunchKernelGGL((chunk_prep_kernel<true, 0>), grid, dim3(256), 0, st, p);
-      else if (cv == 1) hipLaunchKernelGGL((chunk_prep_kernel<true, 1>), grid, dim3(256), 0, st, p);
-      else hipLaunchKernelGGL((chunk_prep_kernel<true, 2>), grid, dim3(256), 0, st, p);
+      if (masked) hipLaunchKernelGGL((chunk_prep_kernel<true, 0, true>), grid, dim3(256), 0, st, p);
+      else if (cv == 0) hipLaunchKernelGGL((chunk_prep_kernel<true, 0, false>), grid, dim3(256), 0, st, p);
+      else if (cv == 1) hipLaunchKernelGGL((chunk_prep_kernel<true, 1, false>), grid, dim3(256), 0, st, p);
+      else hipLaunchKernelGGL((chunk_prep_kernel<true, 2, false>), grid, dim3(256), 0, st, p);
     } else {
-      if (cv == 0) hipLaunchKernelGGL((chunk_prep_kernel<false, 0>), grid, dim3(256), 0, st, p);
-      else if (cv == 1) hipLaunchKernelGGL((chunk_prep_kernel<false, 1>), grid, dim3(256), 0, st, p);
-      else hipLaunchKernelGGL((chunk_prep_kernel<false, 2>), grid, dim3(256), 0, st, p);
+      if (masked) hipLaunchKernelGGL((chunk_prep_kernel<false, 0, true>), grid, dim3(256), 0, st, p);
+      else if (cv == 0) hipLaunchKernelGGL((chunk_prep_kernel<false, 0, false>), grid, dim3(256), 0, st, p);
+      else if (cv == 1) hipLaunchKernelGGL((chunk_prep_kernel<false, 1, false>), grid, dim3(256), 0, st, p);
+      else hipLaunchKernelGGL((chunk_prep_kernel<false, 2, false>), grid, dim3(256), 0, st, p);
     }
     const int rc = gdn_host::check_launch("gdn_chunk_fwd/prep");
     if (rc != GDN_OK) return rc;
@@ -1391,11 +1414,11 @@ int chunk_fwd(const void* q, const void* k, const void* v, int qkv_dtype, int ga
 #define GDN_CHUNK_PARAMS                                                                                        \
   const void *q, const void *k, const void *v, int qkv_dtype, int gate_mode, const void *gx, const void *gy,   \
       int gate_dtype, int64_t gate_stride, const void *A_log, const void *dt_bias, int param_dtype,             \
-      const float *state_in, void *y, float *state_out, const int32_t *state_index, int64_t n_slots,            \
+      const uint8_t *mask, const float *state_in, void *y, float *state_out, const int32_t *state_index, int64_t n_slots,            \
       const int32_t *cu_seqlens, int64_t n_seqs, int64_t n_tok, int64_t Hk, int64_t Hv, int64_t Dk, int64_t Dv, \
       int64_t chunk, void *workspace, size_t workspace_bytes, void *stream
 #define GDN_CHUNK_ARGS                                                                                        \
-  q, k, v, qkv_dtype, gate_mode, gx, gy, gate_dtype, gate_stride, A_log, dt_bias, param_dtype, state_in, y,   \
+  q, k, v, qkv_dtype, gate_mode, gx, gy, gate_dtype, gate_stride, A_log, dt_bias, param_dtype, mask, state_in, y, \
       state_out, state_index, n_slots, cu_seqlens, n_seqs, n_tok, Hk, Hv, Dk, Dv, chunk, workspace,           \
       workspace_bytes, stream
 
@@ -1415,17 +1438,18 @@ extern "C" int gdn_chunk_fwd_conv(const void* qkv, int64_t qkv_stride, const voi
                                   void* stream) {
   const ConvArgs conv{qkv, qkv_stride, conv_w, conv_w_dtype, conv_state_in, conv_state_out, eps};
   return chunk_fwd(nullptr, nullptr, nullptr, GDN_DTYPE_BF16, gate_mode, gx, gy, gate_dtype, gate_stride, A_log,
-                   dt_bias, param_dtype, state_in, y, state_out, state_index, n_slots, cu_seqlens, n_seqs, n_tok, Hk,
+                   dt_bias, param_dtype, nullptr, state_in, y, state_out, state_index, n_slots, cu_seqlens, n_seqs, n_tok, Hk,
                    Hv, Dk, Dv, chunk, workspace, workspace_bytes, stream, kPhasePrep | kPhaseScan, false, &conv);
 }
 
 extern "C" int gdn_chunk_fwd_noalloc(const void* q, const void* k, const void* v, int qkv_dtype, int gate_mode,
                                      const void* gx, const void* gy, int gate_dtype, int64_t gate_stride,
-                                     const void* A_log, const void* dt_bias, int param_dtype, const float* state_in,
+                                     const void* A_log, const void* dt_bias, int param_dtype, const uint8_t* mask,
+                                     const float* state_in,
                                      void* y, float* state_out, const int32_t* state_index, int64_t n_slots,
                                      const int32_t* cu_seqlens, int64_t n_seqs, int64_t n_tok, int64_t Hk,
                                      int64_t Hv, int64_t Dk, int64_t Dv, int64_t chunk, void* stream) {
-  return chunk_fwd(q, k, v, qkv_dtype, gate_mode, gx, gy, gate_dtype, gate_stride, A_log, dt_bias, param_dtype,
+  return chunk_fwd(q, k, v, qkv_dtype, gate_mode, gx, gy, gate_dtype, gate_stride, A_log, dt_bias, param_dtype, mask,
                    state_in, y, state_out, state_index, n_slots, cu_seqlens, n_seqs, n_tok, Hk, Hv, Dk, Dv, chunk,
                    nullptr, 0, stream, kPhasePrep | kPhaseScan, true);
 }

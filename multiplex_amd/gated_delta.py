@@ -529,9 +529,9 @@ class PreparedChunked(PreparedCall):
 
 
 def _chunk_args(q, k, v, gx, gy, gate_mode, A_log, dt_bias, state, *, cu_seqlens=None,
-                state_out=None, workspace=None, state_index=None):
-    names = ["q", "k", "v", "a/g", "b/beta", "A_log", "dt_bias", "state", "state_out"]
-    dev = _require_device([q, k, v, gx, gy, A_log, dt_bias, state, state_out], names)
+                state_out=None, workspace=None, state_index=None, mask=None):
+    names = ["q", "k", "v", "a/g", "b/beta", "A_log", "dt_bias", "state", "state_out", "mask"]
+    dev = _require_device([q, k, v, gx, gy, A_log, dt_bias, state, state_out, mask], names)
     packed = cu_seqlens is not None
     sh = _Shapes(q, k, v, gx, gy, packed)
     q, k, v = (_contig(t) for t in (q, k, v))
@@ -548,30 +548,31 @@ def _chunk_args(q, k, v, gx, gy, gate_mode, A_log, dt_bias, state, *, cu_seqlens
     n_tok = sh.B * sh.T
     state, out_state, idx, n_slots = _state_operands(state, state_out, True, n_seqs, sh.Hv, sh.Dv, sh.Dk, dev,
                                                      state_index)
+    mask_u8 = _mask_u8(mask, (sh.B, sh.T))  # [B, T] row-major: one byte per token, in token order
     y_t = torch.empty(sh.B, sh.T, sh.Hv, sh.Dv, dtype=k.dtype, device=dev)
     ws_bytes = chunk_workspace_bytes(n_seqs, n_tok, sh.Hv, sh.Dk, sh.Dv, CHUNK)
     if workspace is None or workspace.numel() * workspace.element_size() < ws_bytes:
         workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
     args = (_ptr(q), _ptr(k), _ptr(v), qkv_code, gate_mode, _ptr(gx), _ptr(gy), gate_code, g_ld, _ptr(A_log),
-            _ptr(dt_bias), param_code, _ptr(state), _ptr(y_t), _ptr(out_state), _ptr(idx), n_slots, _ptr(cu),
-            n_seqs, n_tok, sh.Hk, sh.Hv, sh.Dk, sh.Dv, CHUNK, _ptr(workspace), ws_bytes, _stream(dev))
+            _ptr(dt_bias), param_code, _ptr(mask_u8), _ptr(state), _ptr(y_t), _ptr(out_state), _ptr(idx), n_slots,
+            _ptr(cu), n_seqs, n_tok, sh.Hk, sh.Hv, sh.Dk, sh.Dv, CHUNK, _ptr(workspace), ws_bytes, _stream(dev))
     keep = dict(q=q, k=k, v=v, gx=gx, gy=gy, A_log=A_log, dt_bias=dt_bias, state=state, cu=cu,
-                workspace=workspace, state_index=idx)
+                workspace=workspace, state_index=idx, mask=mask_u8)
     return args, keep, y_t, out_state, dev
 
 
 def _chunked(q, k, v, gx, gy, gate_mode, A_log, dt_bias, state, *, cu_seqlens=None,
-             state_out=None, workspace=None, state_index=None):
+             state_out=None, workspace=None, state_index=None, mask=None):
     args, _keep, y_t, out_state, dev = _chunk_args(q, k, v, gx, gy, gate_mode, A_log, dt_bias, state,
                                                    cu_seqlens=cu_seqlens, state_out=state_out,
-                                                   workspace=workspace, state_index=state_index)
+                                                   workspace=workspace, state_index=state_index, mask=mask)
     with torch.cuda.device(dev):
         _lib.call("gdn_chunk_fwd", *args)
     return y_t, out_state
 
 
 def prepare_chunked(q, k, v, a, b, A_log, dt_bias, state=None, *, cu_seqlens=None, state_out=None,
-                    workspace=None, gates_precomputed=False, state_index=None) -> "PreparedChunked":
+                    workspace=None, gates_precomputed=False, state_index=None, mask=None) -> "PreparedChunked":
     """Validates a chunked prefill once; ``launch()`` re-issues it.
 
     Same arguments as :func:`gated_delta_update` with ``chunked=True``;
@@ -581,7 +582,7 @@ def prepare_chunked(q, k, v, a, b, A_log, dt_bias, state=None, *, cu_seqlens=Non
     mode = _lib.GATES_PRE if gates_precomputed else _lib.GATES_RAW
     args, keep, y_t, out_state, dev = _chunk_args(q, k, v, a, b, mode, A_log, dt_bias, state,
                                                   cu_seqlens=cu_seqlens, state_out=state_out,
-                                                  workspace=workspace, state_index=state_index)
+                                                  workspace=workspace, state_index=state_index, mask=mask)
     for name in ("q", "k", "v", "gx", "gy"):
         if keep[name].data_ptr() != {"q": q, "k": k, "v": v, "gx": a, "gy": b}[name].data_ptr():
             raise ValueError(f"{name} must be contiguous (gates: or one-stride column slices) for a prepared launch")
@@ -595,12 +596,12 @@ def _aligned16(t: torch.Tensor) -> bool:
 
 
 def _use_chunked(chunked, q, k, v, mask, T):
-    """The chunked kernel by default for long unmasked bf16 rows at
+    """The chunked kernel by default for long bf16 rows (masked or not) at
     Dk = Dv = 128 with 16-byte aligned q/k/v; everything else steps the
     recurrent kernel, which takes any of those."""
     if chunked is not None:
         return bool(chunked)
-    if mask is not None or k.dtype != torch.bfloat16 or k.shape[-1] != 128 or v.shape[-1] != 128:
+    if k.dtype != torch.bfloat16 or k.shape[-1] != 128 or v.shape[-1] != 128:
         return False
     if not all(_aligned16(t) for t in (q, k, v)):
         return False
@@ -638,8 +639,9 @@ def gated_delta_update(q, k, v, a, b, A_log, dt_bias, state=None, mask=None, use
     ``max_seqlen``, the longest one, to pick the kernel, unless ``chunked``
     picks it);
     ``state_out`` receives the new state (may be ``state``); ``chunked``
-    forces the chunked MFMA prefill kernel on/off (default: long unmasked
-    bf16 rows with Dk = 128); ``workspace`` is a reusable uint8 buffer for it.
+    forces the chunked MFMA prefill kernel on/off (default: long bf16 rows
+    with Dk = Dv = 128, masked or not); ``workspace`` is a reusable uint8
+    buffer for it.
     ``state_index`` (int32 ``[rows]``) switches to pooled states: ``state``
     (and ``state_out``) are then pools ``[n_slots, Hv, Dv, Dk]``, row b reads
     and writes slot ``state_index[b]``, and without ``state_out`` the pool is
@@ -659,11 +661,9 @@ def gated_delta_update(q, k, v, a, b, A_log, dt_bias, state=None, mask=None, use
     if cu_seqlens is not None and chunked is None:
         T = _packed_max_len(cu_seqlens, k.shape[1], max_seqlen)
     if _use_chunked(chunked, q, k, v, mask, T):
-        if mask is not None:
-            raise ValueError("the chunked kernel does not take a mask")
         return _chunked(q, k, v, a, b, _lib.GATES_RAW, A_log, dt_bias, state,
                         cu_seqlens=cu_seqlens, state_out=state_out, workspace=workspace,
-                        state_index=state_index)
+                        state_index=state_index, mask=mask)
     y, s, _ = _recurrent(q, k, v, a, b, _lib.GATES_RAW, A_log, dt_bias, state, mask,
                          state_out=state_out, cu_seqlens=cu_seqlens, state_index=state_index)
     return y, s

@@ -124,7 +124,7 @@ def test_conv_commit_rejects_bad_arguments(lib):
 def test_chunk_rejects_bad_arguments(lib):
     def call(**kw):
         args = dict(q=FAKE, k=FAKE, v=FAKE, qkv=_lib.DTYPE_BF16, mode=_lib.GATES_RAW, gx=FAKE, gy=FAKE,
-                    gdt=_lib.DTYPE_BF16, g_ld=0, A_log=FAKE, dt_bias=FAKE, pdt=_lib.DTYPE_F32, s_in=None, y=FAKE,
+                    gdt=_lib.DTYPE_BF16, g_ld=0, A_log=FAKE, dt_bias=FAKE, pdt=_lib.DTYPE_F32, mask=None, s_in=None, y=FAKE,
                     s_out=FAKE, index=None, n_slots=0, cu=None, n_seqs=1, n_tok=4096, Hk=16, Hv=32, Dk=128, Dv=128, chunk=64,
                     ws=FAKE, ws_bytes=1 << 40)
         args.update(kw)
@@ -204,9 +204,9 @@ def test_python_rejects_host_tensors():
 def test_noalloc_chunk_rejects_calls_beyond_its_scratch(lib):
     """gdn_chunk_fwd_noalloc refuses, before any HIP call, a call whose chunk
     records exceed its 64 MiB static scratch (2048 tokens at Hv=32 need
-    (32 + 1) * 32 records of 82,688 B), and takes no workspace argument."""
+    (32 + 1) * 32 records of 82,944 B), and takes no workspace argument."""
     P, I = FAKE, _lib.DTYPE_BF16
-    st = lib.gdn_chunk_fwd_noalloc(P, P, P, I, _lib.GATES_RAW, P, P, I, 0, P, P, _lib.DTYPE_F32, P, P, P,
+    st = lib.gdn_chunk_fwd_noalloc(P, P, P, I, _lib.GATES_RAW, P, P, I, 0, P, P, _lib.DTYPE_F32, None, P, P, P,
                                    None, 0, None, 1, 2048, 16, 32, 128, 128, 64, None)
     assert st == _lib.ERR_UNSUPPORTED
     msg = lib.gdn_last_error().decode()

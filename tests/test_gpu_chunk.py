@@ -273,3 +273,65 @@ def test_device_offsets_need_max_seqlen_to_pick_a_kernel():
     y_ref, S_ref = oracle_heads(r, [0, 1, 2, 3], 4, 2, None, cu=cu.cpu().numpy())
     assert rel_err(y.float().cpu().numpy(), y_ref) <= Y_TOL
     assert head_errs_state(S.cpu().numpy(), S_ref).max() <= STATE_TOL
+
+
+def _masked(seed, B, T, kind, Hk=2, Hv=4):
+    d = draw(seed, B, T, Hk, Hv, 128, 128, mask_p=0.25 if kind == "random" else None)
+    if kind == "left_pad":  # batched prefills pad their rows on the left
+        m = np.ones((B, T), dtype=bool)
+        for b in range(B):
+            m[b, : (37 * (b + 1)) % T] = False
+        d["mask"] = m
+    elif kind == "whole_rows":  # row 0 masked throughout, row 1 not at all
+        m = np.ones((B, T), dtype=bool)
+        m[0] = False
+        d["mask"] = m
+    return d
+
+
+@pytest.mark.parametrize("T,kind", [(200, "random"), (130, "left_pad"), (64, "whole_rows"), (1, "random")])
+def test_masked_rows_match_oracle(T, kind):
+    """A masked token keeps the state and its y is 0 (the oracle's and the
+    recurrent kernel's rule): random masks, left padding and whole rows."""
+    d = _masked(910 + T, 2, T, kind)
+    t, r = to_torch(d, DEV)
+    y, S = mx.gated_delta_update(t["q"], t["k"], t["v"], t["a"], t["b"], t["A_log"], t["dt_bias"], t["state"],
+                                 t["mask"], chunked=True)
+    g = gdn.compute_g(r["A_log"], r["a"], r["dt_bias"])
+    y_ref, S_ref = gdn.recurrent(r["q"][:, :, [0, 0, 1, 1]], r["k"][:, :, [0, 0, 1, 1]], r["v"], g,
+                                 gdn.compute_beta(r["b"]), r["state"], r["mask"])
+    yn = y.float().cpu().numpy()
+    assert head_errs_state(S.cpu().numpy(), S_ref).max() <= STATE_TOL
+    on = r["mask"].any(axis=1)
+    if on.any():
+        assert row_errs_y(yn[on], y_ref[on]).max() <= Y_TOL
+    assert not yn[~r["mask"]].any(), "a masked token's y is not 0"
+    if kind == "whole_rows":
+        assert torch.equal(S[0], t["state"][0])
+    # the recurrent kernel, which steps the same rule
+    y2, S2 = mx.gated_delta_update(t["q"], t["k"], t["v"], t["a"], t["b"], t["A_log"], t["dt_bias"], t["state"],
+                                   t["mask"], chunked=False)
+    assert head_errs_state(S.cpu().numpy(), S2.cpu().numpy()).max() <= STATE_TOL
+    if on.any():
+        assert row_errs_y(yn[on], y2.float().cpu().numpy()[on]).max() <= Y_TOL
+
+
+def test_masked_packed_sequences_match_oracle():
+    """Packed sequences with a token mask, and masked rows take the chunked
+    kernel by default."""
+    lens = [70, 0, 1, 128, 63]
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    d = draw(930, 1, int(cu[-1]), 2, 4, 128, 128, state=False, mask_p=0.3)
+    t, r = to_torch(d, DEV)
+    S0 = np.random.default_rng(9).normal(0, 0.02, (len(lens), 4, 128, 128)).astype(np.float32)
+    y, S = mx.gated_delta_update(t["q"], t["k"], t["v"], t["a"], t["b"], t["A_log"], t["dt_bias"],
+                                 torch.tensor(S0, device=DEV), t["mask"], cu_seqlens=cu)
+    g = gdn.compute_g(r["A_log"], r["a"], r["dt_bias"])
+    y_ref, S_ref = gdn.recurrent_varlen(r["q"][:, :, [0, 0, 1, 1]], r["k"][:, :, [0, 0, 1, 1]], r["v"], g,
+                                        gdn.compute_beta(r["b"]), cu, S0.astype(np.float64), r["mask"])
+    yn = y.float().cpu().numpy()
+    assert rel_err(yn[r["mask"]], y_ref[r["mask"]]) <= Y_TOL
+    assert not yn[~r["mask"]].any()
+    assert head_errs_state(S.cpu().numpy(), S_ref).max() <= STATE_TOL
+    assert mx.gated_delta._use_chunked(None, t["q"], t["k"], t["v"], t["mask"], 128)
+
