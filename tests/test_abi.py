@@ -204,7 +204,7 @@ def test_python_rejects_host_tensors():
 def test_noalloc_chunk_rejects_calls_beyond_its_scratch(lib):
     """gdn_chunk_fwd_noalloc refuses, before any HIP call, a call whose chunk
     records exceed its 64 MiB static scratch (2048 tokens at Hv=32 need
-    (32 + 1) * 32 records of 82,944 B), and takes no workspace argument."""
+    (32 + 1) * 32 records of 82,688 B), and takes no workspace argument."""
     P, I = FAKE, _lib.DTYPE_BF16
     st = lib.gdn_chunk_fwd_noalloc(P, P, P, I, _lib.GATES_RAW, P, P, I, 0, P, P, _lib.DTYPE_F32, None, P, P, P,
                                    None, 0, None, 1, 2048, 16, 32, 128, 128, 64, None)
