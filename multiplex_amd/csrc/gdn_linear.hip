@@ -31,13 +31,16 @@
 // streams); the plain projection never beats the library.  Callers dispatch
 // on that.
 //
-// The slices of one tile are reduced without device-scope fences: block b
-// runs on XCD b % 8 (the dispatcher deals workgroups to the 8 XCDs round
-// robin), and the grid puts every slice of a tile on one XCD, so the
-// partials of a tile are written to, and read back from, one L2.  A
-// workgroup's stores complete at that L2 (s_waitcnt) before it takes its
-// ticket, and the last one reads the partials past its L1.  No workgroup
-// waits for another.
+// The slices of one tile meet without fences.  Each workgroup writes its
+// partial tile with device-coherent stores (cache policy sc1, the encoding
+// of an agent-scope store: not held back in the writer's L2) and waits for
+// them to complete before it takes the tile's ticket; the last workgroup
+// reads the partials with device-coherent loads (sc1).  So the sum is right
+// whichever XCDs the slices run on.  The grid still deals every slice of a
+// tile to one XCD by block index (block b normally runs on XCD b % 8), but
+// the hardware does not always keep to that: the XCC_ID register has shown
+// blocks of other kernels off that XCD in about one launch in seven.  No
+// workgroup waits for another.
 #include "gdn_common.hpp"
 
 namespace {
@@ -89,7 +92,7 @@ __device__ __forceinline__ float rows_sum4(float x) {
 
 typedef __amdgpu_buffer_rsrc_t BufRsrc;
 constexpr int kBufFlags = 0x00020000;  // raw buffer, 32-bit data format (gfx9)
-constexpr int kLoadPastL1 = 1;         // cache policy sc0: the load misses the L1 and reads the L2
+constexpr int kDeviceCoherent = 16;   // cache policy sc1: the access is coherent across the device's XCDs
 
 // out^T (64 columns x 64 rows) += W A^T over one wave's k-steps, into this
 // wave's slot of the LDS reduction buffer: accumulator (mb, nb) lane (lr, lq)
@@ -241,17 +244,19 @@ linear_decode_kernel(const LinParams p) {
   // w + 4, .. of the MB x NB and stores them (lane (lr, lq) of block
   // (mb, nb) holds out[16 mb + lr][n0 + 16 nb + 4 lq + i]).
   const int64_t prow = static_cast<int64_t>(p.NT) * LN;  // partial row stride (floats)
-  float* part = p.part + static_cast<int64_t>(ks) * RM * prow;
+  const BufRsrc pr = __builtin_amdgcn_make_buffer_rsrc(
+      p.part, 0, static_cast<int>(static_cast<int64_t>(p.KSL) * RM * prow * 4), kBufFlags);
 #pragma unroll
   for (int b = wave; b < MB * NB; b += 4) {
     const int mb = b / NB, nb = b % NB;
     f32x4 sum = *reinterpret_cast<const f32x4*>(red[0][mb][nb][lane]);
 #pragma unroll
     for (int w = 1; w < 4; ++w) sum += *reinterpret_cast<const f32x4*>(red[w][mb][nb][lane]);
-    *reinterpret_cast<f32x4*>(part + (16 * mb + lr) * prow + n0 + 16 * nb + 4 * lq) = sum;
+    const uint32_t off = static_cast<uint32_t>(((ks * RM + 16 * mb + lr) * prow + n0 + 16 * nb + 4 * lq) * 4);
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, sum), pr, off, 0, kDeviceCoherent);
   }
 
-  // every partial store of this workgroup complete (at the L2) before its ticket
+  // every partial store of this workgroup complete before its ticket
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if (tid == 0) s_last = atomicAdd(&p.tickets[nt], 1u) == static_cast<uint32_t>(p.KSL - 1);
@@ -260,8 +265,6 @@ linear_decode_kernel(const LinParams p) {
   if (tid == 0) atomicExch(&p.tickets[nt], 0u);  // ready for the next launch
 
   // Sum the slices in slice order: thread tid takes quads (row, 4 columns).
-  const BufRsrc pr = __builtin_amdgcn_make_buffer_rsrc(
-      p.part, 0, static_cast<int>(static_cast<int64_t>(p.KSL) * RM * prow * 4), kBufFlags);
 #pragma unroll
   for (int q = 0; q < (RM * LN / 4 + 255) / 256; ++q) {
     const int idx = tid + 256 * q;
@@ -277,7 +280,7 @@ linear_decode_kernel(const LinParams p) {
         if (k0 + k < p.KSL)
           v[k] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
                                                pr, off + static_cast<uint32_t>((k0 + k) * RM * prow * 4), 0,
-                                               kLoadPastL1));
+                                               kDeviceCoherent));
 #pragma unroll
       for (int k = 0; k < 8; ++k)
         if (k0 + k < p.KSL) sum += v[k];
