@@ -514,18 +514,34 @@ def bench_mixer_layer(torch, mx, dev, timer, iters=20, hidden=2048):
             m(x, None, cache)
         t = timer.total_ms(lambda i: m(x, None, cache), iters) / iters
         res[f"decode_{tag}_us"] = round(1e3 * t, 2)
-        # the same step captured once in a HIP graph and replayed (the conv
-        # state is handed back to the buffer the captured step reads)
+        # the same step captured once in a HIP graph and replayed (pooled
+        # decode updates the conv state in place, so the captured step reads
+        # and writes the same buffers every replay)
         cs_in = cache[0]
+
+        def step():
+            m(x, None, cache)
+            if cache[0] is not cs_in:  # a new conv state: hand it back to the captured buffer
+                cs_in.copy_(cache[0])
+                cache[0] = cs_in
+
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph):
-            m(x, None, cache)
-            cs_in.copy_(cache[0])
-        cache[0] = cs_in
+            step()
         for _ in range(3):
             graph.replay()
         t = timer.total_ms(lambda i: graph.replay(), iters) / iters
         res[f"decode_{tag}_graph_us"] = round(1e3 * t, 2)
+        # eight steps in one graph (as a captured multi-layer forward pass
+        # issues its layers): per-step time without a graph launch per step
+        graph8 = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph8):
+            for _ in range(8):
+                step()
+        for _ in range(3):
+            graph8.replay()
+        t8 = timer.total_ms(lambda i: graph8.replay(), iters) / (8 * iters)
+        res[f"decode_{tag}_graph8_us_per_step"] = round(1e3 * t8, 2)
 
     with torch.no_grad():
         decode(64, "b64")

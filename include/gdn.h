@@ -272,7 +272,8 @@ int gdn_chunk_fwd_noalloc(const void* q, const void* k, const void* v, int qkv_d
  *   weight         [C,Kt] w_dtype (mlx-lm's [C,Kt,1] squeezed)
  *   mask           [B,S] uint8 or NULL
  *   q_out, k_out   [B,S,Hk,Dk];  v_out [B,S,Hv,Dv]   (io_dtype)
- *   conv_state_out [B,Kt-1,C] or NULL; must not alias conv_state_in
+ *   conv_state_out [B,Kt-1,C] or NULL; may be conv_state_in (updated in
+ *                  place) only for unpacked rows of S <= 1 token (decode)
  *   qkv_stride     elements from one qkv row (token) to the next, >= C and
  *                  16-byte aligned; 0 = C.  Lets qkv be a column slice of one
  *                  fused in_proj output.

@@ -49,7 +49,7 @@ def _qkv_rows(qkv: torch.Tensor, C: int):
 
 
 def _prologue_args(qkv, conv_weight, num_k_heads, num_v_heads, head_k_dim, head_v_dim, conv_state, mask,
-                   cu_seqlens, eps, write_conv_state):
+                   cu_seqlens, eps, write_conv_state, conv_state_out=None):
     dev = _require_device([qkv, conv_weight, conv_state, mask], ["qkv", "conv_weight", "conv_state", "mask"])
     if qkv.dim() != 3:
         raise ValueError("qkv must be [B, S, C]")
@@ -65,16 +65,30 @@ def _prologue_args(qkv, conv_weight, num_k_heads, num_v_heads, head_k_dim, head_
     if cu is not None and B != 1:
         raise ValueError("packed sequences need qkv of shape [1, N_tok, C]")
     n_rows = (cu.numel() - 1) if cu is not None else B
+    in_place = conv_state_out is not None and conv_state is not None and conv_state_out is conv_state
     if conv_state is not None:
         if tuple(conv_state.shape) != (n_rows, Kt - 1, C) or conv_state.dtype != qkv.dtype:
             raise ValueError(f"conv_state must be {(n_rows, Kt - 1, C)} of dtype {qkv.dtype}")
+        if in_place and not conv_state.is_contiguous():
+            raise ValueError("an in-place conv state update needs a contiguous conv_state")
         conv_state = conv_state.contiguous()
+    if conv_state_out is not None:
+        if not write_conv_state:
+            raise ValueError("conv_state_out given with write_conv_state=False")
+        if (tuple(conv_state_out.shape) != (n_rows, Kt - 1, C) or conv_state_out.dtype != qkv.dtype
+                or not conv_state_out.is_contiguous() or conv_state_out.device != qkv.device):
+            raise ValueError(f"conv_state_out must be a contiguous {(n_rows, Kt - 1, C)} tensor of dtype {qkv.dtype}")
+        if in_place and (cu is not None or S > 1):
+            raise ValueError("the conv state is updated in place only for unpacked rows of one token")
     m = _mask_u8(mask, (B, S))
     qkv, ld = _qkv_rows(qkv, C)
     q = torch.empty(B, S, Hk, Dk, dtype=qkv.dtype, device=dev)
     k = torch.empty(B, S, Hk, Dk, dtype=qkv.dtype, device=dev)
     v = torch.empty(B, S, Hv, Dv, dtype=qkv.dtype, device=dev)
-    cs_out = torch.empty(n_rows, Kt - 1, C, dtype=qkv.dtype, device=dev) if write_conv_state else None
+    if conv_state_out is not None:
+        cs_out = conv_state_out
+    else:
+        cs_out = torch.empty(n_rows, Kt - 1, C, dtype=qkv.dtype, device=dev) if write_conv_state else None
     args = (_ptr(qkv), io, ld, _ptr(conv_state), _ptr(w), wdt, _ptr(m), _ptr(cu), _ptr(q), _ptr(k), _ptr(v),
             _ptr(cs_out), n_rows, S, Hk, Hv, Dk, Dv, Kt, float(eps), _stream(dev))
     keep = dict(qkv=qkv, conv_state=conv_state, w=w, mask=m, cu=cu)
@@ -85,7 +99,7 @@ def gdn_conv_prologue(qkv: torch.Tensor, conv_weight: torch.Tensor, num_k_heads:
                       num_v_heads: int, head_k_dim: int, head_v_dim: int,
                       conv_state: Optional[torch.Tensor] = None, mask: Optional[torch.Tensor] = None,
                       *, cu_seqlens: Optional[IntSeq] = None, eps: float = 1e-6,
-                      write_conv_state: bool = True):
+                      write_conv_state: bool = True, conv_state_out: Optional[torch.Tensor] = None):
     """Returns ``(q, k, v, new_conv_state)``.
 
     qkv ``[B,S,C]`` (C = 2*Hk*Dk + Hv*Dv, channels q | k | v), conv_weight
@@ -94,10 +108,12 @@ def gdn_conv_prologue(qkv: torch.Tensor, conv_weight: torch.Tensor, num_k_heads:
     ``[B,S,Hv,Dv]``, all in qkv's dtype; the new conv state is the last K-1
     rows of ``concat(conv_state, masked qkv)`` (None if not requested).
     With ``cu_seqlens`` the rows are packed ragged sequences (``B == 1``) and
-    conv_state has one row per sequence.
+    conv_state has one row per sequence.  ``conv_state_out`` receives the
+    new conv state (default: a new tensor); it may be ``conv_state`` itself
+    (updated in place) for unpacked rows of one token (decode).
     """
     args, _keep, outs, dev = _prologue_args(qkv, conv_weight, num_k_heads, num_v_heads, head_k_dim, head_v_dim,
-                                            conv_state, mask, cu_seqlens, eps, write_conv_state)
+                                            conv_state, mask, cu_seqlens, eps, write_conv_state, conv_state_out)
     with torch.cuda.device(dev):
         _lib.call("gdn_conv_prologue", *args)
     return outs

@@ -234,12 +234,19 @@ __global__ __launch_bounds__(256) void prologue_kernel(const ProParams p) {
   }
 
   // new conv state = the last KT-1 rows of X (the wave holding the
-  // sequence's last token writes it; the window itself has run past it)
+  // sequence's last token writes it).  With one-token runs the window has
+  // just shifted onto exactly those rows (masked, as load_x reads them);
+  // longer runs have run past them and read them again.
   if (t_end == len && p.cs_out != nullptr && active) {
 #pragma unroll
     for (int i = 0; i < KT - 1; ++i) {
       float r[CPL];
-      load_x(len + i, r);
+      if constexpr (R == 1) {
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) r[j] = win[i][j];
+      } else {
+        load_x(len + i, r);
+      }
       store8<DT>(p.cs_out, (static_cast<int64_t>(seq) * (KT - 1) + i) * C + c0, r);
     }
   }
@@ -290,8 +297,12 @@ extern "C" int gdn_conv_prologue(const void* qkv, int io_dtype, int64_t qkv_stri
     return fail(GDN_ERR_UNSUPPORTED, "gdn_conv_prologue: conv weight must be fp32 or the qkv dtype");
   if (qkv == nullptr || weight == nullptr || q_out == nullptr || k_out == nullptr || v_out == nullptr)
     return fail(GDN_ERR_INVALID, "gdn_conv_prologue: qkv, weight and q/k/v outputs are required");
-  if (conv_state_out != nullptr && conv_state_out == conv_state_in)
-    return fail(GDN_ERR_INVALID, "gdn_conv_prologue: conv_state_out must not alias conv_state_in");
+  // In place only for unpacked rows of at most one token: one wave then reads
+  // each row's whole window (its registers hold it) before it writes the
+  // row's new state, and no other wave touches that row.
+  if (conv_state_out != nullptr && conv_state_out == conv_state_in && (cu_seqlens != nullptr || S > 1))
+    return fail(GDN_ERR_INVALID,
+                "gdn_conv_prologue: conv_state_out may alias conv_state_in only for unpacked rows of one token");
   if (!(eps >= 0.0f)) return fail(GDN_ERR_INVALID, "gdn_conv_prologue: eps must be >= 0");
   if (qkv_stride != 0 && (qkv_stride < 2 * Hk * Dk + Hv * Dv || (qkv_stride * (io_dtype == GDN_DTYPE_F32 ? 4 : 2)) % 16 != 0))
     return fail(GDN_ERR_INVALID, "gdn_conv_prologue: qkv_stride=%lld must be >= C and keep rows 16-byte aligned",

@@ -7,7 +7,8 @@ and the engine calls it as ``mixer(inputs, mask=None, cache=None)`` through
 module keeps that class name and call signature, with ``cache[0]`` the conv
 state and ``cache[1]`` the recurrent state -- a dense ``[B, Hv, Dv, Dk]``
 array, or a :class:`~multiplex_amd.state_pool.PooledBatch` whose slots the
-kernels update in place.
+kernels update in place.  With pooled states a decode step (one token per
+row) also updates the conv state ``cache[0]`` in place.
 
 Data path per call:
   in_proj_qkv / z / b / a      one library GEMM (hipBLASLt through torch); the
@@ -208,9 +209,14 @@ class GatedDeltaNet(torch.nn.Module):
                 if not pooled:
                     cache[1] = new_state
             return self._epilogue(y, z)
+        # pooled decode advances the conv state in place too, as its states
+        # advance in their pool slots (no new tensor per step)
+        cs_in_place = (pooled and not verify and qkv.shape[1] == 1 and conv_state is not None
+                       and conv_state.is_contiguous())
         q, k, v, new_cs = gdn_conv_prologue(
             qkv, self.conv1d_weight, self.num_k_heads, self.num_v_heads, self.head_k_dim, self.head_v_dim,
-            conv_state, mask, eps=self.rms_norm_eps, write_conv_state=not verify)
+            conv_state, mask, eps=self.rms_norm_eps, write_conv_state=not verify,
+            conv_state_out=conv_state if cs_in_place else None)
         if verify:
             if cache is None:
                 raise ValueError("verify needs the cache the round will be committed into")

@@ -105,7 +105,9 @@ def test_prologue_rejects_bad_arguments(lib):
 
     assert call(Dk=64) == _lib.ERR_UNSUPPORTED
     assert call(Kt=3) == _lib.ERR_UNSUPPORTED
-    assert call(cs=FAKE, cso=FAKE) == _lib.ERR_INVALID
+    assert call(cs=FAKE, cso=FAKE) == _lib.ERR_INVALID           # in place over 4-token rows
+    assert call(cs=FAKE, cso=FAKE, S=1, cu=FAKE) == _lib.ERR_INVALID  # in place over packed rows
+    assert call(cs=FAKE, cso=FAKE, S=1, B=0) == _lib.OK          # in place over one-token rows
     assert call(q=None) == _lib.ERR_INVALID
     assert call(eps=-1.0) == _lib.ERR_INVALID
     assert call(B=0) == _lib.OK

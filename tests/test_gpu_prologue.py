@@ -159,3 +159,30 @@ def test_prepared_launch_equals_call():
         plan.launch()
         for got, want in zip(plan.outputs, ref):
             assert torch.equal(got, want)
+
+
+@pytest.mark.parametrize("masked", [False, True])
+def test_decode_updates_conv_state_in_place(masked):
+    """One-token rows may write the new conv state over the old one
+    (``conv_state_out=conv_state``): bit-identical to a separate output, in
+    three steps in a row; rows longer than one token refuse it."""
+    qkv, w, cs, mask = draw_prologue(171 + masked, 64, 1, 16, 32, 128, mask_p=0.3 if masked else None)
+    Hk, Hv, D = 16, 32, 128
+    w = w.to(DEV)
+    cs_ref = cs.to(DEV)
+    cs_live = cs_ref.clone()
+    ptr = cs_live.data_ptr()
+    g = torch.Generator().manual_seed(172)
+    for step in range(3):
+        x = (torch.randn(qkv.shape, generator=g) if step else qkv).to(torch.bfloat16).to(DEV)
+        m = None if mask is None else mask.to(DEV)
+        ref = mx.gdn_conv_prologue(x, w, Hk, Hv, D, D, cs_ref, m)
+        got = mx.gdn_conv_prologue(x, w, Hk, Hv, D, D, cs_live, m, conv_state_out=cs_live)
+        assert got[3] is cs_live and cs_live.data_ptr() == ptr
+        for a, b in zip(ref, got):
+            assert torch.equal(a, b), f"step {step}"
+        cs_ref = ref[3]
+    x2 = torch.zeros(4, 2, qkv.shape[2], dtype=torch.bfloat16, device=DEV)
+    cs2 = torch.zeros(4, 3, qkv.shape[2], dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(ValueError, match="in place"):
+        mx.gdn_conv_prologue(x2, w, Hk, Hv, D, D, cs2, conv_state_out=cs2)
