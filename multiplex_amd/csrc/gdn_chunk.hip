@@ -795,7 +795,8 @@ struct WaveOps {
   bf16x8 kt[2][2];       // K^T rows 32w + 16j + lr, columns 32s + 8lq ..
   uint16_t v[2][4];      // V[16w + 4lq + i][dv0 + 16t + lr] (bf16 bits) of tile t
   f32x4 g, b, e;         // gamma / beta / e of tokens 16w + 4lq + i (KT_LDS: .x of token 16w + 4lq + lr % 4)
-  float gy;              // gamma of token 16w + lr
+  float gy;              // KT_LDS: gamma of token 16w + lr
+  float gl;              // otherwise: the next chunk's gate value of this lane, until it goes to LDS
   float gC;              // gamma of the chunk's last token
 };
 
@@ -855,6 +856,7 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(const ChunkParams p) {
   __shared__ __align__(16) uint16_t Uh[NR][CP], Ul[NR][CP];  // U^T
   __shared__ __align__(16) uint16_t Eh[NR][CP], El[NR][CP];  // (diag(e) U)^T
   __shared__ __align__(16) uint16_t Kl[KT_LDS ? CH : 1][KP];   // K [token][dk] (KT_LDS)
+  __shared__ __align__(16) float Gs[4][KT_LDS ? 1 : CH];  // gamma, e, beta and the y gamma of the chunk
 
   // Loop-invariant lane offsets (bytes) into the per-chunk descriptors:
   // fragment (rb, cb) of a record matrix is 1 KB at (rb * n_cb + cb) KB.
@@ -868,9 +870,10 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(const ChunkParams p) {
   const uint32_t rec_hv = static_cast<uint32_t>(hv) * kRecBytes;
   const uint32_t off_rows = rec_hv + (2 * wave * 64 + lane) * 16;        // T, P rows 16w + lr
   const uint32_t off_kt = rec_hk + kOffKT + (4 * wave * 64 + lane) * 16;  // K^T rows 32w + 16j + lr
-  const uint32_t off_g4 = rec_hv + kOffGam + (16 * wave + 4 * lq) * 4;
-  const uint32_t off_gq = off_g4 + (lr & 3) * 4;
-  const uint32_t off_g1 = rec_hv + kOffGy + (16 * wave + lr) * 4;
+  const uint32_t off_gq = rec_hv + kOffGam + (16 * wave + 4 * lq + (lr & 3)) * 4;  // KT_LDS
+  const uint32_t off_g1 = rec_hv + kOffGy + (16 * wave + lr) * 4;                   // KT_LDS
+  // otherwise a lane loads array lq (gamma, e, beta, y gamma) of token 16w + lr
+  const uint32_t off_gl = rec_hv + (lq == 3 ? kOffGy : kOffGam + lq * CH * 4) + (16 * wave + lr) * 4;
 
   // Bases of the chunk whose descriptors come next, advanced by one chunk at
   // a time (a 64-bit add each) rather than recomputed from the chunk index.
@@ -912,12 +915,31 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(const ChunkParams p) {
     if constexpr (KT_LDS) {
       o.g.x = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(c.rec, off_gq, 0, 0));
       o.b.x = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(c.rec, off_gq + (kOffBeta - kOffGam), 0, 0));
+      o.gy = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(c.rec, off_g1, 0, 0));
     } else {
-      o.g = buf_f32x4(c.rec, off_g4);
-      o.b = buf_f32x4(c.rec, off_g4 + (kOffBeta - kOffGam));
+      o.gl = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(c.rec, off_gl, 0, 0));
     }
-    o.gy = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(c.rec, off_g1, 0, 0));
   };
+  auto load_e = [&](const ChunkBufs& c) {
+    if constexpr (KT_LDS)
+      o.e.x = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(c.rec, off_gq + (kOffE - kOffGam), 0, 0));
+  };
+  // The per-token gates.  With several workgroups per CU (KT_LDS) the texture
+  // path bounds the scan: a lane loads one value of its quad's four tokens
+  // and quad broadcasts hand it the others.  With one workgroup per CU the
+  // broadcasts would lengthen the chain; there the gates go through LDS:
+  // each wave loads its 16 tokens' four values once (one dword a lane) and
+  // stores them at the end of the chunk before; every lane reads its values
+  // right after the chunk's first barrier (their latency then hides behind
+  // X_K; read at their stages they cost the chain more), so every read of
+  // the buffer is done before the chunk's second barrier, long before the
+  // next store.
+  // Loaded as 16-byte vectors per lane instead, every value would cross the
+  // texture path 16 times.
+  auto store_gates = [&]() {
+    if constexpr (!KT_LDS) Gs[lq][16 * wave + lr] = o.gl;
+  };
+  auto gate4 = [&](int a) { return *reinterpret_cast<const f32x4*>(&Gs[a][16 * wave + 4 * lq]); };
   // T and P are lower triangular: the rows of waves 0 and 1 (tokens < 32)
   // have no entries in the second 32-column block, whose loads and products
   // those waves skip (wave-uniform branches; the prep does not write those
@@ -931,15 +953,6 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(const ChunkParams p) {
       }
     });
   };
-  auto load_e = [&](const ChunkBufs& c) {
-    if constexpr (KT_LDS)
-      o.e.x = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(c.rec, off_gq + (kOffE - kOffGam), 0, 0));
-    else
-      o.e = buf_f32x4(c.rec, off_g4 + (kOffE - kOffGam));
-  };
-  // Value i of a per-token gate vector: with several workgroups per CU the
-  // texture path is the bottleneck and the quad broadcasts pay; with one,
-  // they lengthen the chain.
   auto tok4 = [&](const f32x4& x, auto i) {
     if constexpr (KT_LDS) return quad_bcast<decltype(i)::value>(x.x);
     else return x[i.value];
@@ -996,6 +1009,7 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(const ChunkParams p) {
     load_p(c0);
   }
   write_state();
+  store_gates();
   const f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
 
   BufRsrc y_cur = c0.y;
@@ -1004,7 +1018,14 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(const ChunkParams p) {
     // around the loads, so their waits are not forced early)
     if (ci + 1 < nch) advance();
     const ChunkBufs cn = bufs_here();
-    __syncthreads();  // state hi/lo of this chunk is in LDS
+    __syncthreads();  // state hi/lo and gates of this chunk are in LDS
+    float gy_l = 0.0f;
+    if constexpr (!KT_LDS) {
+      o.g = gate4(0);
+      o.e = gate4(1);
+      o.b = gate4(2);
+      gy_l = Gs[3][16 * wave + lr];
+    }
 
     // ---- X_K = K S0^T (tokens x rows) and X_Q^T = S0 Q^T (rows x tokens)
     f32x4 xk0[TPW], xk1[TPW], xq0[TPW], xq1[TPW];
@@ -1039,9 +1060,10 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(const ChunkParams p) {
       });
       split4_store(r, &Rh[16 * t.value + lr][16 * wave + 4 * lq], &Rl[16 * t.value + lr][16 * wave + 4 * lq]);
     });
-    const float gy = o.gy;  // kept for Y
+    const float gy_k = KT_LDS ? o.gy : 0.0f;  // KT_LDS: this chunk's, before load_vg takes the next
     load_vg(cn);
     __syncthreads();  // R^T complete
+    const float gy = KT_LDS ? gy_k : gy_l;
 
     // K^T fragments of this wave's state columns (KT_LDS: from the K rows in
     // LDS since the barrier above, read here so their latency is off the update)
@@ -1123,6 +1145,7 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(const ChunkParams p) {
       __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, yb), y_cur, off_y + 32 * t.value, 0, 0);
     });
     y_cur = cn.y;
+    store_gates();  // the next chunk's
   }
 
 #pragma unroll
