@@ -411,16 +411,8 @@ __device__ __forceinline__ double wave_scan_d(double x) {
   return x;
 }
 
-// Orders this wave's LDS writes before its later LDS reads (no other wave
-// takes part).
-__device__ __forceinline__ void wave_lds_sync() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
 // KT_LDS: the scan forms K^T from K in LDS, so the record carries no K^T.
-// Four workgroups per CU: 40.7 KB of LDS each and at most 128 VGPRs (four
+// Four workgroups per CU: 35.6 KB of LDS each and at most 128 VGPRs (four
 // waves per SIMD; left to itself the compiler takes 137-138, which leaves
 // three).  At 4096 tokens x 32 heads the 2048 workgroups then run in two
 // full rounds instead of two and two thirds.
@@ -468,7 +460,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void c
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
   const int lr = lane & 15, lq = lane >> 4, lg8 = lq * 8;
 
-  __shared__ __align__(16) float Ms[4][16][20];
   __shared__ double Ld[CH];
   __shared__ float Bs[CH];
   __shared__ float Ys[MASK ? CH : 1];  // 1, or 0 at a masked token (its row of P is zero)
@@ -563,7 +554,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void c
   }
   __syncthreads();
 
-  // K K^T and Q K^T: wave w computes row block w (16 rows) x 4 column blocks.
+  // K K^T and Q K^T: wave w computes row block w (16 rows) x 4 column
+  // blocks, as the transposed products K_j K_w^T and K_j Q_w^T (an A and a
+  // B fragment have the same layout, so the operands swap roles): lane
+  // (r, q) of tile j then holds row 16w + r, columns 16j + 4q .. +3 (K K^T is
+  // symmetric) -- four consecutive columns of one row, which go to LDS as
+  // one 16-byte (A) or 8-byte (P hi, P lo) store.
   f32x4 kk[4], qk[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
@@ -590,8 +586,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void c
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const bf16x8 bk = lds8(&Ks[16 * j + lr][kc]);
-      kk[j] = mfma16(ak, bk, kk[j]);
-      qk[j] = mfma16(aq, bk, qk[j]);
+      kk[j] = mfma16(bk, ak, kk[j]);
+      qk[j] = mfma16(bk, aq, qk[j]);
     }
     if (!KT_LDS && first_v) {
 #pragma unroll
@@ -606,30 +602,28 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void c
   // are no longer read, so their buffers take A and the P planes
   __syncthreads();
 
-  // Decays, A (to LDS, fp32) and P (hi/lo bf16, staged in fragment order).
+  // Decays, A (to LDS, fp32) and P (hi/lo bf16, staged in fragment order):
+  // lane (r, q) takes row t = 16w + r, columns 16j + 4q .. +3.
   {
-    double Lt[4], Lc[4];
-    float bs[4], ys[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      Lt[i] = Ld[16 * wave + 4 * lq + i];
-      bs[i] = Bs[16 * wave + 4 * lq + i];
-      ys[i] = MASK ? Ys[16 * wave + 4 * lq + i] : 1.0f;
-      Lc[i] = Ld[16 * i + lr];
-    }
+    const int t = 16 * wave + lr;
+    const double Lt = Ld[t];
+    const float bt = Bs[t];
+    const float yt = MASK ? Ys[t] : 1.0f;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
+      const int c0 = 16 * j + 4 * lq;
+      f32x4 av;
+      float pv[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int t = 16 * wave + 4 * lq + i;
-        const int col = 16 * j + lr;
-        const float dec = col <= t ? __builtin_amdgcn_exp2f(static_cast<float>((Lt[i] - Lc[j]) * kLog2e)) : 0.0f;
-        As[t][col] = col < t ? bs[i] * dec * kk[j][i] : 0.0f;
-        uint16_t h, l;
-        split_bf16(MASK ? (dec * qk[j][i]) * ys[i] : dec * qk[j][i], h, l);
-        Pst[frag_elem(t, col, CH / 32)] = h;
-        Pst[CH * CH + frag_elem(t, col, CH / 32)] = l;
+        const int col = c0 + i;
+        const float dec = col <= t ? __builtin_amdgcn_exp2f(static_cast<float>((Lt - Ld[col]) * kLog2e)) : 0.0f;
+        av[i] = col < t ? bt * dec * kk[j][i] : 0.0f;
+        pv[i] = MASK ? (dec * qk[j][i]) * yt : dec * qk[j][i];
       }
+      *reinterpret_cast<f32x4*>(&As[t][c0]) = av;
+      split4_store(f32x4{pv[0], pv[1], pv[2], pv[3]}, Pst + frag_elem(t, c0, CH / 32),
+                   Pst + CH * CH + frag_elem(t, c0, CH / 32));
     }
   }
   __syncthreads();
@@ -669,49 +663,55 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void c
     for (int t = 0; t < 16; ++t) Ti[dbase + t][dbase + dcol] = x[t];
   }
   __syncthreads();
-  // Off-diagonal blocks by distance d from the diagonal.  Block (I, J=I-d)
-  // belongs to wave J:
+  // Off-diagonal blocks.  Block (I, J) belongs to wave J, which forms its
+  // column of blocks top-down:
   //   M = sum_{K=J}^{I-1} A_IK T_KJ,   T_IJ = -T_II M
-  // Each 16x16x16 block product is four fp32 MFMAs (16x16x4): lane l holds
-  // A[l % 16][4s + l / 16] and B[4s + l / 16][l % 16] for k-step s, and the
-  // accumulator rows 4 (l / 16) .. +3 of column l % 16.  M goes through LDS
-  // (this wave's Ms) to become the B operand of the second product.
+  // Each 16x16x16 block product is four fp32 MFMAs (16x16x4), with the k
+  // index of step s and lane l taken as 4 (l / 16) + s: lane l then supplies
+  // A[l % 16][4 (l / 16) .. +3] (one 16-byte read of a row) and
+  // B[4 (l / 16) .. +3][l % 16] -- which is what the lane holds of an
+  // accumulator tile (rows 4 (l / 16) .. +3 of column l % 16).  So M feeds
+  // the second product, and the wave's earlier blocks T_KJ (K > J) the
+  // first, straight from registers; only A, T_JJ and T_II come from LDS, and
+  // no wave reads another's off-diagonal blocks until the barrier below.
   {
     const int ln = lane & 15, lk = lane >> 4;
+    const int J = wave;
+    f32x4 tcol[3];  // T_{J+1,J} .. T_{J+3,J}
+    float tjj[4];
+#pragma unroll
+    for (int s4 = 0; s4 < 4; ++s4) tjj[s4] = Ti[16 * J + 4 * lk + s4][16 * J + ln];
+#pragma unroll
     for (int d = 1; d < 4; ++d) {
-      const int J = wave, I = wave + d;
-      if (I < 4) {
+      const int I = J + d;
+      if (I < 4) {  // wave-uniform
         f32x4 m = {0.0f, 0.0f, 0.0f, 0.0f};
-        for (int Kb = J; Kb < I; ++Kb) {
-          float a[4], b[4];
-#pragma unroll
-          for (int s4 = 0; s4 < 4; ++s4) {
-            a[s4] = As[16 * I + ln][16 * Kb + 4 * s4 + lk];
-            b[s4] = Ti[16 * Kb + 4 * s4 + lk][16 * J + ln];
-          }
-#pragma unroll
-          for (int s4 = 0; s4 < 4; ++s4) m = __builtin_amdgcn_mfma_f32_16x16x4f32(a[s4], b[s4], m, 0, 0, 0);
-        }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) Ms[wave][4 * lk + i][ln] = m[i];
-        wave_lds_sync();  // Ms is written and read by this wave only
-        f32x4 tv = {0.0f, 0.0f, 0.0f, 0.0f};
         {
-          float a[4], b[4];
+          const f32x4 a4 = *reinterpret_cast<const f32x4*>(&As[16 * I + ln][16 * J + 4 * lk]);
 #pragma unroll
-          for (int s4 = 0; s4 < 4; ++s4) {
-            a[s4] = Ti[16 * I + ln][16 * I + 4 * s4 + lk];
-            b[s4] = Ms[wave][4 * s4 + lk][ln];
-          }
-#pragma unroll
-          for (int s4 = 0; s4 < 4; ++s4) tv = __builtin_amdgcn_mfma_f32_16x16x4f32(a[s4], b[s4], tv, 0, 0, 0);
+          for (int s4 = 0; s4 < 4; ++s4) m = __builtin_amdgcn_mfma_f32_16x16x4f32(a4[s4], tjj[s4], m, 0, 0, 0);
         }
 #pragma unroll
-        for (int i = 0; i < 4; ++i) Ti[16 * I + 4 * lk + i][16 * J + ln] = -tv[i];
+        for (int e = 0; e < 2; ++e) {
+          const int Kb = J + 1 + e;
+          if (e < d - 1) {
+            const f32x4 a4 = *reinterpret_cast<const f32x4*>(&As[16 * I + ln][16 * Kb + 4 * lk]);
+#pragma unroll
+            for (int s4 = 0; s4 < 4; ++s4) m = __builtin_amdgcn_mfma_f32_16x16x4f32(a4[s4], tcol[e][s4], m, 0, 0, 0);
+          }
+        }
+        const f32x4 tii = *reinterpret_cast<const f32x4*>(&Ti[16 * I + ln][16 * I + 4 * lk]);
+        f32x4 tv = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int s4 = 0; s4 < 4; ++s4) tv = __builtin_amdgcn_mfma_f32_16x16x4f32(tii[s4], m[s4], tv, 0, 0, 0);
+        tv = -tv;
+        tcol[d - 1] = tv;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) Ti[16 * I + 4 * lk + i][16 * J + ln] = tv[i];
       }
-      __syncthreads();
     }
   }
+  __syncthreads();  // every block of (I + A)^{-1} is in LDS
   uint16_t* Th = reinterpret_cast<uint16_t*>(rec + kOffTh);
   uint16_t* Tl = reinterpret_cast<uint16_t*>(rec + kOffTl);
   // one 16-byte group (8 columns of a row) per thread and pass; blocks
