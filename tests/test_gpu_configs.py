@@ -163,6 +163,28 @@ def test_mixed_step_two_streams():
     assert head_errs_state(S_com[:, heads].cpu().numpy(), S_ref).max() <= STATE_TOL
 
 
+def test_mixed_steps_in_a_row_overlapped_equal_serial():
+    """Three overlapped steps back to back (the decode rows' states carried in
+    place, the prep's ordering event reused each step) against three steps on
+    one stream from the same initial states: bit-identical outputs."""
+    cu, pf, dec, ver, n_b = _mixed_inputs()
+    (tp, _), (td, _), (tv, _) = (to_torch(x, DEV) for x in (pf, dec, ver))
+    dec_state0 = td["state"].clone()
+    step, plans = _build_step(cu, tp, td, tv, n_b)
+    for _ in range(3):
+        step.launch_overlapped()
+    torch.cuda.synchronize()
+    two = [t.clone() for t in _outputs(plans)]
+    for t in _outputs(plans):
+        t.zero_()
+    td["state"].copy_(dec_state0)
+    for _ in range(3):
+        step.launch_serial()
+    torch.cuda.synchronize()
+    for a, b in zip(two, _outputs(plans)):
+        assert torch.equal(a, b)
+
+
 def test_verify_b32_full_heads():
     """B=32, T=4, Hv=32 with no state write: the MFMA verify kernel, all heads."""
     d = draw(1002, 32, 4, Hk, Hv, D, D)
@@ -177,8 +199,7 @@ def test_verify_b32_full_heads():
 def test_commit_verify_one_pass_b32_full_heads():
     """The bench's one-pass round at B=32: the previous round's 4 drafts with
     ragged acceptance n_b ~ U{1..4} committed and the next 4 drafts verified
-    in one launch (the streaming MFMA kernel walks 2048 units, several per
-    workgroup), all heads against the oracle."""
+    in one launch of the stepping tile kernel, all heads against the oracle."""
     d = draw(1012, 32, 8, Hk, Hv, D, D)
     t, r = to_torch(d, DEV)
     n_b = np.random.default_rng(1013).integers(1, 5, 32)
