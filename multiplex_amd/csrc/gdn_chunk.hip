@@ -924,18 +924,18 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(const ChunkParams p) {
     if constexpr (KT_LDS)
       o.e.x = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(c.rec, off_gq + (kOffE - kOffGam), 0, 0));
   };
-  // The per-token gates.  With several workgroups per CU (KT_LDS) the texture
-  // path bounds the scan: a lane loads one value of its quad's four tokens
-  // and quad broadcasts hand it the others.  With one workgroup per CU the
-  // broadcasts would lengthen the chain; there the gates go through LDS:
-  // each wave loads its 16 tokens' four values once (one dword a lane) and
-  // stores them at the end of the chunk before; every lane reads its values
-  // right after the chunk's first barrier (their latency then hides behind
-  // X_K; read at their stages they cost the chain more), so every read of
-  // the buffer is done before the chunk's second barrier, long before the
-  // next store.
-  // Loaded as 16-byte vectors per lane instead, every value would cross the
-  // texture path 16 times.
+  // The per-token gates (gamma, e, beta, the y gamma).  Loaded as 16-byte
+  // vectors per lane, every value would cross the texture path 16 times.
+  // With several workgroups per CU (KT_LDS), where the texture path bounds
+  // the scan, a lane loads one value of its quad's four tokens and quad
+  // broadcasts hand it the others.  With one workgroup per CU the broadcasts
+  // would lengthen the chain, so the gates go through LDS: each wave loads
+  // its 16 tokens' four values (one dword a lane) and stores them at the end
+  // of the chunk before; every lane reads its values right after the
+  // chunk's first barrier, where their latency hides behind X_K (read at the
+  // stages that use them, they cost the chain more).  So every read of the
+  // buffer is done before the chunk's second barrier, long before the next
+  // store.
   auto store_gates = [&]() {
     if constexpr (!KT_LDS) Gs[lq][16 * wave + lr] = o.gl;
   };
