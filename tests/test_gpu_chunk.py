@@ -149,6 +149,26 @@ def test_strong_decay_is_finite_and_exact():
     assert head_errs_state(S.cpu().numpy(), S_ref).max() <= STATE_TOL
 
 
+@pytest.mark.parametrize("B,Hk,Hv,T,heads", [(1, 2, 4, 300, [0, 1, 2, 3]), (2, 16, 32, 200, [0, 1, 17, 31])])
+def test_mixed_decays_within_chunks_match_oracle(B, Hk, Hv, T, heads):
+    """Tokens alternate between almost no decay (g near 1) and strong decay
+    (g near e^-60) and A_log spans its range over the heads, so inside one
+    chunk the factors e^(L_t - L_i) run from 1 down to underflow while |L|
+    grows large: the prep's fp64 prefix sums, its decays and the triangular
+    inverse, with one scan workgroup per CU (B=1) and several (B=2, Hv=32)."""
+    d = draw(315 + B, B, T, Hk, Hv, 128, 128)
+    d["a"][:, 0::2] = -6.0
+    d["a"][:, 1::2] = 4.0
+    d["a"][:, 5::7] = 1.0
+    d["A_log"][:] = np.linspace(0.0, np.log(15.0), Hv)
+    t, r = to_torch(d, DEV)
+    y, S = chunked(t, t["state"])
+    assert torch.isfinite(y.float()).all() and torch.isfinite(S).all()
+    y_ref, S_ref = oracle_heads(r, heads, Hv, Hk, r["state"])
+    assert row_errs_y(y[:, :, heads].float().cpu().numpy(), y_ref).max() <= Y_TOL
+    assert head_errs_state(S[:, heads].cpu().numpy(), S_ref).max() <= STATE_TOL
+
+
 def test_in_place_state():
     d = draw(307, 2, 100, 2, 4, 128, 128)
     t, _ = to_torch(d, DEV)
