@@ -778,15 +778,6 @@ __device__ __forceinline__ f32x4 buf_f32x4(BufRsrc r, uint32_t voff) {
   return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, 0, 0));
 }
 
-// Lane I of each group of four lanes, to all four (DPP quad_perm [I,I,I,I]).
-// The lanes of a quad need the same four per-token values: one 4-byte load
-// per lane (value lr % 4) and these moves replace a 16-byte load per lane,
-// which would fetch each value 16 times.
-template <int I>
-__device__ __forceinline__ float quad_bcast(float x) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), I * 0x55, 0xF, 0xF, false));
-}
-
 // One wave's operands of one chunk (all in MFMA operand layouts).
 struct WaveOps {
   bf16x8 k[4], q[4];     // K / Q rows 16w + lr, columns 32s + 8lq ..
@@ -794,9 +785,8 @@ struct WaveOps {
   bf16x8 ph[2], pl[2];   // P rows, same layout
   bf16x8 kt[2][2];       // K^T rows 32w + 16j + lr, columns 32s + 8lq ..
   uint16_t v[2][4];      // V[16w + 4lq + i][dv0 + 16t + lr] (bf16 bits) of tile t
-  f32x4 g, b, e;         // gamma / beta / e of tokens 16w + 4lq + i (KT_LDS: .x of token 16w + 4lq + lr % 4)
-  float gy;              // KT_LDS: gamma of token 16w + lr
-  float gl;              // otherwise: the next chunk's gate value of this lane, until it goes to LDS
+  f32x4 g, b, e;         // gamma / beta / e of tokens 16w + 4lq + i
+  float gl;              // the next chunk's gate value of this lane, until it goes to LDS
   float gC;              // gamma of the chunk's last token
 };
 
@@ -856,7 +846,7 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(const ChunkParams p) {
   __shared__ __align__(16) uint16_t Uh[NR][CP], Ul[NR][CP];  // U^T
   __shared__ __align__(16) uint16_t Eh[NR][CP], El[NR][CP];  // (diag(e) U)^T
   __shared__ __align__(16) uint16_t Kl[KT_LDS ? CH : 1][KP];   // K [token][dk] (KT_LDS)
-  __shared__ __align__(16) float Gs[4][KT_LDS ? 1 : CH];  // gamma, e, beta and the y gamma of the chunk
+  __shared__ __align__(16) float Gs[4][CH];  // gamma, e, beta and the y gamma of the chunk
 
   // Loop-invariant lane offsets (bytes) into the per-chunk descriptors:
   // fragment (rb, cb) of a record matrix is 1 KB at (rb * n_cb + cb) KB.
@@ -870,9 +860,7 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(const ChunkParams p) {
   const uint32_t rec_hv = static_cast<uint32_t>(hv) * kRecBytes;
   const uint32_t off_rows = rec_hv + (2 * wave * 64 + lane) * 16;        // T, P rows 16w + lr
   const uint32_t off_kt = rec_hk + kOffKT + (4 * wave * 64 + lane) * 16;  // K^T rows 32w + 16j + lr
-  const uint32_t off_gq = rec_hv + kOffGam + (16 * wave + 4 * lq + (lr & 3)) * 4;  // KT_LDS
-  const uint32_t off_g1 = rec_hv + kOffGy + (16 * wave + lr) * 4;                   // KT_LDS
-  // otherwise a lane loads array lq (gamma, e, beta, y gamma) of token 16w + lr
+  // a lane loads array lq (gamma, e, beta, y gamma) of token 16w + lr
   const uint32_t off_gl = rec_hv + (lq == 3 ? kOffGy : kOffGam + lq * CH * 4) + (16 * wave + lr) * 4;
 
   // Bases of the chunk whose descriptors come next, advanced by one chunk at
@@ -912,33 +900,18 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(const ChunkParams p) {
         o.v[t.value][i.value] = __builtin_amdgcn_raw_buffer_load_b16(c.v, off_v[i.value] + 32 * t.value, 0, 0);
       });
     });
-    if constexpr (KT_LDS) {
-      o.g.x = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(c.rec, off_gq, 0, 0));
-      o.b.x = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(c.rec, off_gq + (kOffBeta - kOffGam), 0, 0));
-      o.gy = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(c.rec, off_g1, 0, 0));
-    } else {
-      o.gl = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(c.rec, off_gl, 0, 0));
-    }
+    o.gl = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(c.rec, off_gl, 0, 0));
   };
-  auto load_e = [&](const ChunkBufs& c) {
-    if constexpr (KT_LDS)
-      o.e.x = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(c.rec, off_gq + (kOffE - kOffGam), 0, 0));
-  };
-  // The per-token gates (gamma, e, beta, the y gamma).  Loaded as 16-byte
-  // vectors per lane, every value would cross the texture path 16 times.
-  // With several workgroups per CU (KT_LDS), where the texture path bounds
-  // the scan, a lane loads one value of its quad's four tokens and quad
-  // broadcasts hand it the others.  With one workgroup per CU the broadcasts
-  // would lengthen the chain, so the gates go through LDS: each wave loads
-  // its 16 tokens' four values (one dword a lane) and stores them at the end
-  // of the chunk before; every lane reads its values right after the
-  // chunk's first barrier, where their latency hides behind X_K (read at the
-  // stages that use them, they cost the chain more).  So every read of the
-  // buffer is done before the chunk's second barrier, long before the next
-  // store.
-  auto store_gates = [&]() {
-    if constexpr (!KT_LDS) Gs[lq][16 * wave + lr] = o.gl;
-  };
+  // The per-token gates (gamma, e, beta, the y gamma) go through LDS.  Each
+  // wave loads its 16 tokens' four values (one dword a lane) and stores them
+  // at the end of the chunk before; every lane reads its values right after
+  // the chunk's first barrier, where their latency hides behind X_K (read at
+  // the stages that use them, they cost the chain more).  So every read of
+  // the buffer is done before the chunk's second barrier, long before the
+  // next store.  Loaded as 16-byte vectors per lane instead, every value
+  // would cross the texture path 16 times; one value a lane with quad
+  // broadcasts for the other three put DPP moves on the chain.
+  auto store_gates = [&]() { Gs[lq][16 * wave + lr] = o.gl; };
   auto gate4 = [&](int a) { return *reinterpret_cast<const f32x4*>(&Gs[a][16 * wave + 4 * lq]); };
   // T and P are lower triangular: the rows of waves 0 and 1 (tokens < 32)
   // have no entries in the second 32-column block, whose loads and products
@@ -953,10 +926,7 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(const ChunkParams p) {
       }
     });
   };
-  auto tok4 = [&](const f32x4& x, auto i) {
-    if constexpr (KT_LDS) return quad_bcast<decltype(i)::value>(x.x);
-    else return x[i.value];
-  };
+  auto tok4 = [&](const f32x4& x, auto i) { return x[i.value]; };
   auto load_kt = [&](const ChunkBufs& c) {
     if constexpr (!KT_LDS) {
       static_for<2>([&](auto j) {
@@ -1004,7 +974,6 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(const ChunkParams p) {
     load_kq(c0);
     load_vg(c0);
     load_t(c0);
-    load_e(c0);
     load_kt(c0);
     load_p(c0);
   }
@@ -1019,13 +988,10 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(const ChunkParams p) {
     if (ci + 1 < nch) advance();
     const ChunkBufs cn = bufs_here();
     __syncthreads();  // state hi/lo and gates of this chunk are in LDS
-    float gy_l = 0.0f;
-    if constexpr (!KT_LDS) {
-      o.g = gate4(0);
-      o.e = gate4(1);
-      o.b = gate4(2);
-      gy_l = Gs[3][16 * wave + lr];
-    }
+    o.g = gate4(0);
+    o.e = gate4(1);
+    o.b = gate4(2);
+    const float gy = Gs[3][16 * wave + lr];
 
     // ---- X_K = K S0^T (tokens x rows) and X_Q^T = S0 Q^T (rows x tokens)
     f32x4 xk0[TPW], xk1[TPW], xq0[TPW], xq1[TPW];
@@ -1060,10 +1026,8 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(const ChunkParams p) {
       });
       split4_store(r, &Rh[16 * t.value + lr][16 * wave + 4 * lq], &Rl[16 * t.value + lr][16 * wave + 4 * lq]);
     });
-    const float gy_k = KT_LDS ? o.gy : 0.0f;  // KT_LDS: this chunk's, before load_vg takes the next
     load_vg(cn);
     __syncthreads();  // R^T complete
-    const float gy = KT_LDS ? gy_k : gy_l;
 
     // K^T fragments of this wave's state columns (KT_LDS: from the K rows in
     // LDS since the barrier above, read here so their latency is off the update)
@@ -1102,7 +1066,6 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(const ChunkParams p) {
         split4_store(ev * uv, &Eh[16 * t.value + lr][16 * wave + 4 * lq], &El[16 * t.value + lr][16 * wave + 4 * lq]);
       });
     }
-    load_e(cn);
     __syncthreads();  // U^T, (eU)^T complete
 
     // ---- S^T = gamma_C S0^T + K^T (diag(e) U) on this wave's 32 columns
