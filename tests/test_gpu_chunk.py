@@ -336,6 +336,26 @@ def test_masked_rows_match_oracle(T, kind):
         assert row_errs_y(yn[on], y2.float().cpu().numpy()[on]).max() <= Y_TOL
 
 
+@pytest.mark.parametrize("kind", ["random", "left_pad"])
+def test_masked_rows_at_full_width_match_oracle(kind):
+    """Masks where the scan's tiles outnumber the CUs (B=2 at Hv=32: K^T
+    from LDS, two 16-row tiles a workgroup): four heads against the oracle,
+    masked tokens' y exactly 0."""
+    d = _masked(940, 2, 200, kind, Hk=16, Hv=32)
+    t, r = to_torch(d, DEV)
+    y, S = mx.gated_delta_update(t["q"], t["k"], t["v"], t["a"], t["b"], t["A_log"], t["dt_bias"], t["state"],
+                                 t["mask"], chunked=True)
+    heads = [0, 1, 17, 31]
+    hks = [h // 2 for h in heads]
+    g = gdn.compute_g(r["A_log"][heads], r["a"][:, :, heads], r["dt_bias"][heads])
+    y_ref, S_ref = gdn.recurrent(r["q"][:, :, hks], r["k"][:, :, hks], r["v"][:, :, heads], g,
+                                 gdn.compute_beta(r["b"][:, :, heads]), r["state"][:, heads], r["mask"])
+    yn = y[:, :, heads].float().cpu().numpy()
+    assert head_errs_state(S[:, heads].cpu().numpy(), S_ref).max() <= STATE_TOL
+    assert row_errs_y(yn, y_ref).max() <= Y_TOL
+    assert not y.float().cpu().numpy()[~r["mask"]].any(), "a masked token's y is not 0"
+
+
 def test_masked_packed_sequences_match_oracle():
     """Packed sequences with a token mask, and masked rows take the chunked
     kernel by default."""
