@@ -748,11 +748,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void c
 // that head's chunks.  Wave w produces the chunk's quantities for tokens
 // [16w, 16w+16) (X_K, X_Q, R, U, Y) and updates state columns
 // [32w, 32w+32).  Every MFMA operand that is specific to a wave -- its K, Q,
-// T and P rows, its K^T rows, its V values and gates -- is loaded from
-// global memory straight into registers in MFMA layout, and reloaded for the
-// next chunk right after its last use, so those loads overlap the rest of
-// the chunk.  LDS only carries what the waves exchange: the state (hi/lo
-// bf16) and R^T, U^T, (eU)^T; three barriers per chunk.
+// T and P rows, its K^T rows (or, with several workgroups per CU, K rows
+// read back transposed from LDS) and its V values -- is loaded from global
+// memory straight into registers in MFMA layout, and reloaded for the next
+// chunk right after its last use, so those loads overlap the rest of the
+// chunk.  Otherwise LDS carries what the waves exchange -- the state (hi/lo
+// bf16) and R^T, U^T, (eU)^T, three barriers per chunk -- and the chunk's
+// per-token gates, loaded once a chunk.
 //
 // The state update and Y are computed transposed (S^T += K^T (eU),
 // Y^T = gamma X_Q^T + U^T P^T): a lane then holds 4 consecutive state
