@@ -26,8 +26,8 @@ schedules give bit-identical results.
 
 ``launch()`` takes the schedule chosen at construction, overlapped by
 default (the step of 1024 + 2560 + 7168 prefill tokens, 48 decode rows and
-16 verify rows, with the verify and commit issued before the decode: 0.325 ms
-overlapped, 0.349 ms on one stream).
+16 verify rows, with the verify and commit issued before the decode: 0.324 ms
+overlapped, 0.339 ms on one stream).
 """
 
 from __future__ import annotations
