@@ -460,7 +460,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void c
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
   const int lr = lane & 15, lq = lane >> 4, lg8 = lq * 8;
 
-  __shared__ double Ld[CH];
+  __shared__ __align__(16) double Ld[CH];  // L_t log2(e) (the decays' exponents, base 2)
   __shared__ float Bs[CH];
   __shared__ float Ys[MASK ? CH : 1];  // 1, or 0 at a masked token (its row of P is zero)
   auto Ks = reinterpret_cast<uint16_t(*)[KP]>(buf0);
@@ -501,7 +501,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void c
     lg = on_lane ? fmaxf(lg, -1.0e30f) : 0.0f;
     bt = on_lane ? bt : 0.0f;
     L_lane = wave_scan_d(lg);
-    Ld[lane] = L_lane;
+    Ld[lane] = L_lane * kLog2e;
     Bs[lane] = bt;
     if constexpr (MASK) Ys[lane] = on_lane ? 1.0f : 0.0f;
     b_lane = bt;
@@ -606,18 +606,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void c
   // lane (r, q) takes row t = 16w + r, columns 16j + 4q .. +3.
   {
     const int t = 16 * wave + lr;
+    typedef double f64x2 __attribute__((ext_vector_type(2)));
     const double Lt = Ld[t];
     const float bt = Bs[t];
     const float yt = MASK ? Ys[t] : 1.0f;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int c0 = 16 * j + 4 * lq;
+      const f64x2 l01 = *reinterpret_cast<const f64x2*>(&Ld[c0]);  // two 16-byte reads for four columns
+      const f64x2 l23 = *reinterpret_cast<const f64x2*>(&Ld[c0 + 2]);
+      const double Lc[4] = {l01.x, l01.y, l23.x, l23.y};
       f32x4 av;
       float pv[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int col = c0 + i;
-        const float dec = col <= t ? __builtin_amdgcn_exp2f(static_cast<float>((Lt - Ld[col]) * kLog2e)) : 0.0f;
+        const float dec = col <= t ? __builtin_amdgcn_exp2f(static_cast<float>(Lt - Lc[i])) : 0.0f;
         av[i] = col < t ? bt * dec * kk[j][i] : 0.0f;
         pv[i] = MASK ? (dec * qk[j][i]) * yt : dec * qk[j][i];
       }
