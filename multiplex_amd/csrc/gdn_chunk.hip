@@ -144,12 +144,6 @@ __device__ __forceinline__ bf16x8 kt_frag(const uint16_t* p) {
 }
 
 
-// Component-wise "keep or zero" (a ternary on the u32x4 struct would be
-// lowered through memory).
-__device__ __forceinline__ u32x4 keep_if(bool c, const u32x4& a) {
-  return u32x4{c ? a.x : 0u, c ? a.y : 0u, c ? a.z : 0u, c ? a.w : 0u};
-}
-
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
@@ -284,13 +278,14 @@ constexpr int KTAP = 4;  // conv taps
 // The conv prologue (prologue_kernel in gdn_prologue.hip) for one lane's 8
 // channels c0 .. c0+7 over the R tokens [t0, t0 + R) of a chunk, with that
 // kernel's arithmetic and rounding, so q, k and v are bit-identical to its:
-// o = silu(w[3] x_t + w[0] x_{t-3} + w[1] x_{t-2} + w[2] x_{t-1}) (fused in
-// that order) and, with NORM, o * rsqrt(mean over the head of o^2 + eps) *
-// post, the mean over this lane's 16-lane row (the head's 16 lanes, in the
-// prologue's lane order).  x runs over X = the sequence's conv state (3
-// rows; zeros without one) followed by its qkv rows.  Tokens past the
-// chunk's end repeat its last row.  Every load is issued before the first
-// conversion.
+// with bf16 taps the conv on bf16 pairs (conv_pairs), with fp32 taps
+// w[3] x_t + w[0] x_{t-3} + w[1] x_{t-2} + w[2] x_{t-1} (fused in that
+// order); then o = silu(conv) and, with NORM, o * rsqrt(mean over the head of
+// o^2 + eps) * post, the mean over this lane's 16-lane row (the head's 16
+// lanes, in the prologue's lane order).  x runs over X = the sequence's conv
+// state (3 rows; zeros without one) followed by its qkv rows.  Tokens past
+// the chunk's end repeat its last row.  Every load is issued before the
+// first conversion.
 template <int WDT, int R, bool NORM>
 __device__ __forceinline__ void conv_run(const ChunkParams& p, const ChunkPos& cp, int c0, int t0, float post,
                                          u32x4 (&out)[R]) {
@@ -318,42 +313,8 @@ __device__ __forceinline__ void conv_run(const ChunkParams& p, const ChunkPos& c
 #pragma unroll
   for (int u = 0; u < R; ++u)
     xs[u] = load_raw8<GDN_DTYPE_BF16>(p.qkv, (cp.tok0 + min(t0 + u, cp.len - 1)) * p.qkv_ld + c0);
-  float w[KTAP][CPL];
-  {
-    float wv[CPL * KTAP];
-#pragma unroll
-    for (int i = 0; i < KTAP; ++i) unpack8<WDT>(wr[i], *reinterpret_cast<float(*)[CPL]>(&wv[8 * i]));
-#pragma unroll
-    for (int j = 0; j < CPL; ++j)
-#pragma unroll
-      for (int i = 0; i < KTAP; ++i) w[i][j] = wv[j * KTAP + i];
-  }
-  float win[KTAP - 1][CPL];
-#pragma unroll
-  for (int i = 0; i < KTAP - 1; ++i) {
-    unpack8<GDN_DTYPE_BF16>(xw[i], win[i]);
-#pragma unroll
-    for (int j = 0; j < CPL; ++j) win[i][j] *= wm[i];
-  }
-#pragma unroll
-  for (int u = 0; u < R; ++u) {
-    float x[CPL], o[CPL];
-    unpack8<GDN_DTYPE_BF16>(xs[u], x);
-    float ss = 0.0f;
-#pragma unroll
-    for (int j = 0; j < CPL; ++j) {
-      float acc = w[KTAP - 1][j] * x[j];
-#pragma unroll
-      for (int i = 0; i < KTAP - 1; ++i) acc = fmaf(w[i][j], win[i][j], acc);
-      o[j] = silu(acc);
-      ss = fmaf(o[j], o[j], ss);
-    }
-#pragma unroll
-    for (int i = 0; i < KTAP - 2; ++i)
-#pragma unroll
-      for (int j = 0; j < CPL; ++j) win[i][j] = win[i + 1][j];
-#pragma unroll
-    for (int j = 0; j < CPL; ++j) win[KTAP - 2][j] = x[j];
+  // token u's SiLU outputs o and their sum of squares ss -> out[u]
+  auto finish = [&](int u, float (&o)[CPL], float ss) {
     if constexpr (NORM) {
       ss = head_sum<16>(ss);
       const float sc = rsqrtf(ss / static_cast<float>(DK) + p.conv_eps) * post;
@@ -361,6 +322,78 @@ __device__ __forceinline__ void conv_run(const ChunkParams& p, const ChunkPos& c
       for (int j = 0; j < CPL; ++j) o[j] *= sc;
     }
     out[u] = u32x4{pk_bf16(o[0], o[1]), pk_bf16(o[2], o[3]), pk_bf16(o[4], o[5]), pk_bf16(o[6], o[7])};
+  };
+  if constexpr (WDT == GDN_DTYPE_BF16) {
+    uint32_t w01[CPL], w23[CPL];
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+      w01[j] = wr[j >> 1].v[2 * (j & 1)];
+      w23[j] = wr[j >> 1].v[2 * (j & 1) + 1];
+    }
+    u32x4 rw[KTAP - 1];  // X_{t-3}, X_{t-2}, X_{t-1} of the current token t
+#pragma unroll
+    for (int i = 0; i < KTAP - 1; ++i) rw[i] = row_or_zero(wm[i] != 0.0f, xw[i].v);
+    uint32_t pa[CPL], pb[CPL];  // p(t - 2), p(t - 1)
+    row_pairs(rw[0], rw[1], pa);
+    row_pairs(rw[1], rw[2], pb);
+#pragma unroll
+    for (int u = 0; u < R; ++u) {
+      uint32_t pc[CPL];  // p(t)
+      row_pairs(rw[KTAP - 2], xs[u].v, pc);
+      float o[CPL];
+      float ss = 0.0f;
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) {
+        o[j] = silu(conv_pairs(w01[j], w23[j], pa[j], pc[j]));
+        ss = fmaf(o[j], o[j], ss);
+      }
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) {
+        pa[j] = pb[j];
+        pb[j] = pc[j];
+      }
+      rw[KTAP - 2] = xs[u].v;
+      finish(u, o, ss);
+    }
+  } else {
+    float w[KTAP][CPL];
+    {
+      float wv[CPL * KTAP];
+#pragma unroll
+      for (int i = 0; i < KTAP; ++i) unpack8<WDT>(wr[i], *reinterpret_cast<float(*)[CPL]>(&wv[8 * i]));
+#pragma unroll
+      for (int j = 0; j < CPL; ++j)
+#pragma unroll
+        for (int i = 0; i < KTAP; ++i) w[i][j] = wv[j * KTAP + i];
+    }
+    float win[KTAP - 1][CPL];
+#pragma unroll
+    for (int i = 0; i < KTAP - 1; ++i) {
+      unpack8<GDN_DTYPE_BF16>(xw[i], win[i]);
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) win[i][j] *= wm[i];
+    }
+#pragma unroll
+    for (int u = 0; u < R; ++u) {
+      float x[CPL], o[CPL];
+      unpack8<GDN_DTYPE_BF16>(xs[u], x);
+      float ss = 0.0f;
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) {
+        float acc = w[KTAP - 1][j] * x[j];
+#pragma unroll
+        for (int i = 0; i < KTAP - 1; ++i) acc = fmaf(w[i][j], win[i][j], acc);
+        o[j] = silu(acc);
+        ss = fmaf(o[j], o[j], ss);
+      }
+#pragma unroll
+      for (int i = 0; i < KTAP - 2; ++i)
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) win[i][j] = win[i + 1][j];
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) win[KTAP - 2][j] = x[j];
+      finish(u, o, ss);
+    }
   }
 }
 
@@ -511,7 +544,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void c
     for (int j = 0; j < 4; ++j) {
       const int i = tid + 256 * j;
       const int r = i / (DK / 8), cc = (i % (DK / 8)) * 8;
-      const u32x4 kv = keep_if(r < len, kr[j]), qv = keep_if(r < len, qr[j]);
+      const u32x4 kv = row_or_zero(r < len, kr[j]), qv = row_or_zero(r < len, qr[j]);
       *reinterpret_cast<u32x4*>(&Ks[r][cc]) = kv;
       *reinterpret_cast<u32x4*>(&Qs[r][cc]) = qv;
       if (first_v) {
@@ -534,7 +567,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void c
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         const int r = t0 + u;
-        const u32x4 val = keep_if(r < len, o[u]);
+        const u32x4 val = row_or_zero(r < len, o[u]);
         *reinterpret_cast<u32x4*>(role == 0 ? &Qs[r][8 * g] : &Ks[r][8 * g]) = val;
         if (first_v)
           *reinterpret_cast<u32x4*>(reinterpret_cast<uint16_t*>(rec + (role == 0 ? kOffQf : kOffKf)) +

@@ -445,6 +445,43 @@ __device__ __forceinline__ float silu(float x) {
   return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(x * -1.4426950408889634f));
 }
 
+// ------------------------------------------- causal conv on bf16 pairs
+//
+// With bf16 inputs and bf16 taps the 4-tap causal conv runs on packed pairs:
+// for channel c at token t, p(t) = (x_{t-1}[c], x_t[c]) (earlier token in the
+// low half), and
+//   acc = dot(w23, p(t)) + dot(w01, p(t - 2)),   w01 = (w0, w1), w23 = (w2, w3)
+// on v_dot2c_f32_bf16 (exact bf16 products, fp32 accumulation).  One byte
+// permute forms a pair from two rows and serves two tokens' dots, the taps
+// are used as loaded, and nothing is unpacked to fp32 before the conv.
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+// A row slice (8 16-bit channels) or zeros: a masked or absent row.  Component
+// by component (a ternary on the whole vector would be lowered through memory).
+__device__ __forceinline__ u32x4 row_or_zero(bool keep, const u32x4& r) {
+  return u32x4{keep ? r.x : 0u, keep ? r.y : 0u, keep ? r.z : 0u, keep ? r.w : 0u};
+}
+
+// pr[c] = (prev[c], cur[c]) for the 8 channels of two consecutive rows.
+// v_perm_b32 selects bytes of {cur, prev} (prev = bytes 0-3, cur = 4-7).
+__device__ __forceinline__ void row_pairs(const u32x4& prev, const u32x4& cur, uint32_t (&pr)[CPL]) {
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    pr[2 * k] = __builtin_amdgcn_perm(cur[k], prev[k], 0x05040100u);      // low halves
+    pr[2 * k + 1] = __builtin_amdgcn_perm(cur[k], prev[k], 0x07060302u);  // high halves
+  }
+}
+
+// The conv of one channel from its taps (w01, w23 as loaded: 4 consecutive
+// bf16 taps per channel) and the pairs p(t - 2), p(t).
+__device__ __forceinline__ float conv_pairs(uint32_t w01, uint32_t w23, uint32_t p_m2, uint32_t p_0) {
+  const float a = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w23), __builtin_bit_cast(bf16x2_t, p_0),
+                                                  0.0f, false);
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w01), __builtin_bit_cast(bf16x2_t, p_m2), a,
+                                         false);
+}
+
 }  // namespace gdn
 
 // ----------------------------------------------------- host-side status

@@ -85,6 +85,7 @@ __global__ __launch_bounds__(256) void prologue_kernel(const ProParams p) {
   constexpr int LPH = D / CPL;   // lanes per head
   constexpr int HPW = 64 / LPH;  // heads per wavefront
   constexpr int WDT = W32 ? GDN_DTYPE_F32 : DT;
+  constexpr bool kPairs = DT == GDN_DTYPE_BF16 && !W32;  // the conv on bf16 pairs (conv_pairs)
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
   int seq, len, run;
@@ -172,24 +173,6 @@ __global__ __launch_bounds__(256) void prologue_kernel(const ProParams p) {
     xs[u] = load_raw8<DT>(p.qkv, tok * p.ld + c0);
     if constexpr (MASK) xm[u] = p.mask[tok] != 0 ? 1.0f : 0.0f;
   }
-  float w[KT][CPL];
-  {
-    float wv[CPL * KT];
-#pragma unroll
-    for (int i = 0; i < KT; ++i) unpack8<WDT>(wr[i], *reinterpret_cast<float(*)[CPL]>(&wv[8 * i]));
-#pragma unroll
-    for (int j = 0; j < CPL; ++j)
-#pragma unroll
-      for (int i = 0; i < KT; ++i) w[i][j] = wv[j * KT + i];
-  }
-  float win[KT - 1][CPL];
-#pragma unroll
-  for (int i = 0; i < KT - 1; ++i) {
-    unpack8<DT>(xw[i], win[i]);
-#pragma unroll
-    for (int j = 0; j < CPL; ++j) win[i][j] *= wm[i];
-  }
-
   // Head role: 0 = q, 1 = k, 2 = v (lanes of one head agree).
   const int role = hg < p.Hk ? 0 : (hg < 2 * p.Hk ? 1 : 2);
   const int head = role == 0 ? hg : (role == 1 ? hg - p.Hk : hg - 2 * p.Hk);
@@ -201,53 +184,129 @@ __global__ __launch_bounds__(256) void prologue_kernel(const ProParams p) {
   char* orow = static_cast<char*>(out) + ((start + t_begin) * H * D + static_cast<int64_t>(head) * D +
                                           (lane % LPH) * CPL) * ES;
   const int64_t ostep = static_cast<int64_t>(H) * D * ES;
+  const int64_t cs_row0 = static_cast<int64_t>(seq) * (KT - 1) * C + c0;  // the lane's slice of conv-state row 0
 
-  // Every token of the run is computed (tokens past the end repeat the last
-  // row, so no control flow splits the window); only real tokens are stored.
-#pragma unroll
-  for (int u = 0; u < R; ++u) {
-    float x[CPL], o[CPL];
-    unpack8<DT>(xs[u], x);
-    float ss = 0.0f;
-#pragma unroll
-    for (int j = 0; j < CPL; ++j) {
-      if constexpr (MASK) x[j] *= xm[u];
-      float acc = w[KT - 1][j] * x[j];
-#pragma unroll
-      for (int i = 0; i < KT - 1; ++i) acc = fmaf(w[i][j], win[i][j], acc);
-      o[j] = silu(acc);
-      ss = fmaf(o[j], o[j], ss);
-    }
-#pragma unroll
-    for (int i = 0; i < KT - 2; ++i)
-#pragma unroll
-      for (int j = 0; j < CPL; ++j) win[i][j] = win[i + 1][j];
-#pragma unroll
-    for (int j = 0; j < CPL; ++j) win[KT - 2][j] = x[j];
-    // every lane takes part in the reduction (DPP); v heads keep scale 1
+  // Token u's SiLU outputs o (and their sum of squares): the q/k norm over
+  // the head's lanes (every lane takes part in the DPP reduction; v heads
+  // keep scale 1), then the store of a real token.
+  auto finish = [&](int u, float (&o)[CPL], float ss) {
     ss = head_sum<LPH>(ss);
     const float sc = role == 2 ? 1.0f : rsqrtf(ss / static_cast<float>(D) + p.eps) * post;
 #pragma unroll
     for (int j = 0; j < CPL; ++j) o[j] *= sc;
     if (active && t_begin + u < t_end) store8<DT>(orow, 0, o);
     orow += ostep;
-  }
-
-  // new conv state = the last KT-1 rows of X (the wave holding the
+  };
+  // The new conv state is the last KT-1 rows of X (the wave holding the
   // sequence's last token writes it).  With one-token runs the window has
   // just shifted onto exactly those rows (masked, as load_x reads them);
   // longer runs have run past them and read them again.
-  if (t_end == len && p.cs_out != nullptr && active) {
+  const bool write_cs = t_end == len && p.cs_out != nullptr && active;
+
+  // Every token of the run is computed (tokens past the end repeat the last
+  // row, so no control flow splits the window); only real tokens are stored.
+  if constexpr (kPairs) {
+    // bf16 rows and taps: the conv on bf16 pairs (conv_pairs), with the
+    // taps as loaded and absent or masked rows as zeros
+    uint32_t w01[CPL], w23[CPL];
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+      w01[j] = wr[j >> 1].v[2 * (j & 1)];
+      w23[j] = wr[j >> 1].v[2 * (j & 1) + 1];
+    }
+    u32x4 rw[KT - 1];  // X_{t-3}, X_{t-2}, X_{t-1} of the current token t
+#pragma unroll
+    for (int i = 0; i < KT - 1; ++i) rw[i] = row_or_zero(wm[i] != 0.0f, xw[i].v);
+    uint32_t pa[CPL], pb[CPL];  // p(t - 2), p(t - 1)
+    row_pairs(rw[0], rw[1], pa);
+    row_pairs(rw[1], rw[2], pb);
+#pragma unroll
+    for (int u = 0; u < R; ++u) {
+      u32x4 xr = xs[u].v;
+      if constexpr (MASK) xr = row_or_zero(xm[u] != 0.0f, xr);
+      uint32_t pc[CPL];  // p(t)
+      row_pairs(rw[KT - 2], xr, pc);
+      float o[CPL];
+      float ss = 0.0f;
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) {
+        o[j] = silu(conv_pairs(w01[j], w23[j], pa[j], pc[j]));
+        ss = fmaf(o[j], o[j], ss);
+      }
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) {
+        pa[j] = pb[j];
+        pb[j] = pc[j];
+      }
+      rw[0] = rw[1];
+      rw[1] = rw[2];
+      rw[2] = xr;
+      finish(u, o, ss);
+    }
+    if (write_cs) {
+#pragma unroll
+      for (int i = 0; i < KT - 1; ++i) {
+        if constexpr (R == 1) {
+          *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(p.cs_out) + cs_row0 + i * C) = rw[i];
+        } else {
+          float r[CPL];
+          load_x(len + i, r);
+          store8<DT>(p.cs_out, cs_row0 + i * C, r);
+        }
+      }
+    }
+  } else {
+    float w[KT][CPL];
+    {
+      float wv[CPL * KT];
+#pragma unroll
+      for (int i = 0; i < KT; ++i) unpack8<WDT>(wr[i], *reinterpret_cast<float(*)[CPL]>(&wv[8 * i]));
+#pragma unroll
+      for (int j = 0; j < CPL; ++j)
+#pragma unroll
+        for (int i = 0; i < KT; ++i) w[i][j] = wv[j * KT + i];
+    }
+    float win[KT - 1][CPL];
 #pragma unroll
     for (int i = 0; i < KT - 1; ++i) {
-      float r[CPL];
-      if constexpr (R == 1) {
+      unpack8<DT>(xw[i], win[i]);
 #pragma unroll
-        for (int j = 0; j < CPL; ++j) r[j] = win[i][j];
-      } else {
-        load_x(len + i, r);
+      for (int j = 0; j < CPL; ++j) win[i][j] *= wm[i];
+    }
+#pragma unroll
+    for (int u = 0; u < R; ++u) {
+      float x[CPL], o[CPL];
+      unpack8<DT>(xs[u], x);
+      float ss = 0.0f;
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) {
+        if constexpr (MASK) x[j] *= xm[u];
+        float acc = w[KT - 1][j] * x[j];
+#pragma unroll
+        for (int i = 0; i < KT - 1; ++i) acc = fmaf(w[i][j], win[i][j], acc);
+        o[j] = silu(acc);
+        ss = fmaf(o[j], o[j], ss);
       }
-      store8<DT>(p.cs_out, (static_cast<int64_t>(seq) * (KT - 1) + i) * C + c0, r);
+#pragma unroll
+      for (int i = 0; i < KT - 2; ++i)
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) win[i][j] = win[i + 1][j];
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) win[KT - 2][j] = x[j];
+      finish(u, o, ss);
+    }
+    if (write_cs) {
+#pragma unroll
+      for (int i = 0; i < KT - 1; ++i) {
+        float r[CPL];
+        if constexpr (R == 1) {
+#pragma unroll
+          for (int j = 0; j < CPL; ++j) r[j] = win[i][j];
+        } else {
+          load_x(len + i, r);
+        }
+        store8<DT>(p.cs_out, cs_row0 + i * C, r);
+      }
     }
   }
 }
