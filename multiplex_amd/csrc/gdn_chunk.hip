@@ -300,7 +300,7 @@ __device__ __forceinline__ void conv_run(const ChunkParams& p, const ChunkPos& c
     const int xi = pos + i;
     const bool from_cs = xi < KTAP - 1;
     const bool cs_row = from_cs && p.cs_in != nullptr;
-    // without a conv state the row is the sequence's first qkv row times 0;
+    // without a conv state the row is the sequence's first qkv row, zeroed;
     // a run that starts past the chunk's end (outputs discarded) reads
     // within the chunk's valid rows
     const int tp = from_cs ? 0 : min(xi - (KTAP - 1), cp.ci * CH + cp.len - 1);

@@ -147,8 +147,8 @@ __global__ __launch_bounds__(256) void prologue_kernel(const ProParams p) {
   for (int i = 0; i < KT; ++i) wr[i] = load_raw8<WDT>(p.weight, static_cast<int64_t>(c0) * KT + 8 * i);
   // window row i = X[t + i] for the run's first token t: a conv-state row
   // for t + i < KT - 1, else a qkv row.  Without a conv state those rows are
-  // zeros: the sequence's first qkv row is read and multiplied by 0, so the
-  // load stays unconditional and in the global address space.
+  // zeros: the sequence's first qkv row is read and then zeroed (weight wm
+  // = 0), so the load stays unconditional and in the global address space.
   Raw8<DT> xw[KT - 1];
   float wm[KT - 1];
 #pragma unroll
