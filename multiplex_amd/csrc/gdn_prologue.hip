@@ -14,9 +14,10 @@ namespace {
 
 using namespace gdn;
 
-// Tokens per wavefront (prefill).  8 keeps the kernel at 109 VGPRs, four
-// waves per SIMD (16 took 142, three), and re-reads the 3-row window once
-// per 8 tokens (from L2).
+// Tokens per wavefront (prefill).  8 keeps the kernel at four waves per SIMD
+// (109 VGPRs with the conv in fp32 FMAs, 88 on bf16 pairs; 16 tokens took
+// 142, three waves), and re-reads the 3-row window once per 8 tokens (from
+// L2).
 constexpr int kRun = 8;
 constexpr int kWaves = 4;  // wavefronts per workgroup (consecutive runs)
 constexpr int KT = 4;      // conv taps
@@ -141,7 +142,8 @@ __global__ __launch_bounds__(256) void prologue_kernel(const ProParams p) {
   // the 3 inputs before the run, then the run's tokens (rows past the end
   // re-read the last row and are never stored).  All are raw loads, unpacked
   // only once every load is issued, so token u is computed as soon as its
-  // own row arrives.  A masked token reads as zero (mask byte as multiplier).
+  // own row arrives.  A masked token reads as zero (the mask byte as a
+  // multiplier in fp32, a row of zeros on bf16 pairs).
   Raw8<WDT> wr[KT];  // taps of the lane's 8 channels: weight[c][tap], 32 consecutive values
 #pragma unroll
   for (int i = 0; i < KT; ++i) wr[i] = load_raw8<WDT>(p.weight, static_cast<int64_t>(c0) * KT + 8 * i);
