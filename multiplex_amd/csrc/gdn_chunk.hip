@@ -371,7 +371,7 @@ __device__ __forceinline__ void conv_run(const ChunkParams& p, const ChunkPos& c
     for (int i = 0; i < KTAP - 1; ++i) {
       unpack8<GDN_DTYPE_BF16>(xw[i], win[i]);
 #pragma unroll
-      for (int j = 0; j < CPL; ++j) win[i][j] *= wm[i];
+      for (int j = 0; j < CPL; ++j) win[i][j] = wm[i] != 0.0f ? win[i][j] : 0.0f;
     }
 #pragma unroll
     for (int u = 0; u < R; ++u) {

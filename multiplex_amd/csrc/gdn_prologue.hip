@@ -105,7 +105,8 @@ __global__ __launch_bounds__(256) void prologue_kernel(const ProParams p) {
   const int c0 = hg * D + (lane % LPH) * CPL;
   const int64_t C = p.C;
 
-  // X = concat(conv_state (KT-1 rows), masked qkv): row xi of it.
+  // X = concat(conv_state (KT-1 rows), masked qkv): row xi of it (a masked
+  // row is zeros).
   auto load_x = [&](int xi, float (&dst)[CPL]) {
     if (xi < KT - 1) {
       if (p.cs_in != nullptr) {
@@ -118,9 +119,9 @@ __global__ __launch_bounds__(256) void prologue_kernel(const ProParams p) {
       const int64_t tok = start + xi - (KT - 1);
       unpack8<DT>(load_raw8<DT>(p.qkv, tok * p.ld + c0), dst);
       if constexpr (MASK) {
-        const float wm = p.mask[tok] != 0 ? 1.0f : 0.0f;
+        const bool keep = p.mask[tok] != 0;
 #pragma unroll
-        for (int j = 0; j < CPL; ++j) dst[j] *= wm;
+        for (int j = 0; j < CPL; ++j) dst[j] = keep ? dst[j] : 0.0f;
       }
     }
   };
@@ -142,15 +143,16 @@ __global__ __launch_bounds__(256) void prologue_kernel(const ProParams p) {
   // the 3 inputs before the run, then the run's tokens (rows past the end
   // re-read the last row and are never stored).  All are raw loads, unpacked
   // only once every load is issued, so token u is computed as soon as its
-  // own row arrives.  A masked token reads as zero (the mask byte as a
-  // multiplier in fp32, a row of zeros on bf16 pairs).
+  // own row arrives.  A masked token reads as zero: a select, as the
+  // reference's where(mask, qkv, 0), so a non-finite value in a masked row
+  // reaches no output.
   Raw8<WDT> wr[KT];  // taps of the lane's 8 channels: weight[c][tap], 32 consecutive values
 #pragma unroll
   for (int i = 0; i < KT; ++i) wr[i] = load_raw8<WDT>(p.weight, static_cast<int64_t>(c0) * KT + 8 * i);
   // window row i = X[t + i] for the run's first token t: a conv-state row
   // for t + i < KT - 1, else a qkv row.  Without a conv state those rows are
-  // zeros: the sequence's first qkv row is read and then zeroed (weight wm
-  // = 0), so the load stays unconditional and in the global address space.
+  // zeros: the sequence's first qkv row is read and then zeroed (wm = 0),
+  // so the load stays unconditional and in the global address space.
   Raw8<DT> xw[KT - 1];
   float wm[KT - 1];
 #pragma unroll
@@ -273,7 +275,7 @@ __global__ __launch_bounds__(256) void prologue_kernel(const ProParams p) {
     for (int i = 0; i < KT - 1; ++i) {
       unpack8<DT>(xw[i], win[i]);
 #pragma unroll
-      for (int j = 0; j < CPL; ++j) win[i][j] *= wm[i];
+      for (int j = 0; j < CPL; ++j) win[i][j] = wm[i] != 0.0f ? win[i][j] : 0.0f;
     }
 #pragma unroll
     for (int u = 0; u < R; ++u) {
@@ -282,7 +284,7 @@ __global__ __launch_bounds__(256) void prologue_kernel(const ProParams p) {
       float ss = 0.0f;
 #pragma unroll
       for (int j = 0; j < CPL; ++j) {
-        if constexpr (MASK) x[j] *= xm[u];
+        if constexpr (MASK) x[j] = xm[u] != 0.0f ? x[j] : 0.0f;
         float acc = w[KT - 1][j] * x[j];
 #pragma unroll
         for (int i = 0; i < KT - 1; ++i) acc = fmaf(w[i][j], win[i][j], acc);

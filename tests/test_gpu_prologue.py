@@ -74,6 +74,22 @@ def test_decode_prologue_full_layout():
     check(qkv, w, cs, mask, 16, 32, 128)
 
 
+@pytest.mark.parametrize("S", [1, 4, 77])
+@pytest.mark.parametrize("dtype,w32", [(torch.bfloat16, False), (torch.bfloat16, True), (torch.float32, True)])
+def test_masked_rows_holding_non_finite_values_read_as_zero(S, dtype, w32):
+    """The reference zeroes masked rows with a select (where(mask, qkv, 0),
+    dflash.py:352-353), so NaN and inf in a masked row reach neither q/k/v
+    nor the new conv state.  bf16 rows with bf16 taps take the conv on bf16
+    pairs, the other two the fp32 FMAs; runs of 1, 4 and 8 tokens, and at
+    S = 77 the conv state's rows are read again at the sequence's end."""
+    qkv, w, cs, mask = draw_prologue(90 + S, 2, S, 2, 4, 128, mask_p=0.3, dtype=dtype)
+    mask[0, -1] = False  # the last row of the new conv state is masked
+    n_bad = int((~mask).sum())
+    bad = torch.tensor([float("nan"), float("inf"), -float("inf")])[torch.arange(n_bad) % 3]
+    qkv[~mask] = bad[:, None].to(dtype)
+    check(qkv, w.float() if w32 else w, cs, mask, 2, 4, 128)
+
+
 def test_verify_prologue_with_mask_and_no_state():
     qkv, w, _, mask = draw_prologue(22, 4, 4, 2, 4, 128, with_state=False, mask_p=0.4)
     check(qkv, w, None, mask, 2, 4, 128)
