@@ -514,6 +514,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void c
   bool on_lane = false;  // wave 0: token `lane` is real and not masked
   asm volatile("" ::: "memory");  // keeps the gate loads issued ahead of the rows
   u32x4 kr[4], qr[4];
+  bool kq_on[4];  // the row is a real token (and, with MASK, not masked)
   if constexpr (CONV == 0) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -522,6 +523,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void c
       const int64_t off = ((tok0 + min(r, len - 1)) * p.Hk + hk) * DK + cc;
       kr[j] = *reinterpret_cast<const u32x4*>(p.k + off);
       qr[j] = *reinterpret_cast<const u32x4*>(p.q + off);
+      // a masked token's k and q rows are zeros, as the reference's where()
+      // keeps whatever they hold out of the state: they then add nothing to
+      // any other token's A, P, X or state update (beta = 0 alone would
+      // still let a non-finite value through as 0 * inf)
+      kq_on[j] = r < len && (!MASK || *(gbl_u8*)(p.mask + tok0 + min(r, len - 1)) != 0);
     }
   }
   unsigned char* rec = p.ws + (static_cast<size_t>(c) * p.Hv + hv) * kRecBytes;
@@ -544,7 +550,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void c
     for (int j = 0; j < 4; ++j) {
       const int i = tid + 256 * j;
       const int r = i / (DK / 8), cc = (i % (DK / 8)) * 8;
-      const u32x4 kv = row_or_zero(r < len, kr[j]), qv = row_or_zero(r < len, qr[j]);
+      const u32x4 kv = row_or_zero(kq_on[j], kr[j]), qv = row_or_zero(kq_on[j], qr[j]);
       *reinterpret_cast<u32x4*>(&Ks[r][cc]) = kv;
       *reinterpret_cast<u32x4*>(&Qs[r][cc]) = qv;
       if (first_v) {
@@ -850,7 +856,10 @@ constexpr int kCUs = 256;  // compute units of an MI355X (8 XCDs x 32)
 // bytes per row, for a longer chain per chunk (twice the MFMAs and LDS
 // exchanges per wave).  It pays when the tiles outnumber the CUs and the
 // operand traffic, not one long chain, bounds the scan.
-template <bool KT_LDS, int TPW>
+// MASK: a token mask was given.  A masked token has beta = 0, and its R is
+// then taken as 0 outright, so a non-finite v there stays out of U (the
+// prep zeroes its k and q rows likewise).
+template <bool KT_LDS, int TPW, bool MASK>
 __global__ __launch_bounds__(256) void chunk_scan_kernel(const ChunkParams p) {
   // Block b runs on XCD b % 8.  The v-heads of one k-head (a GQA group,
   // which share its K, Q and K^T) form a unit; units (over all sequences,
@@ -1062,6 +1071,7 @@ __global__ __launch_bounds__(256) void chunk_scan_kernel(const ChunkParams p) {
       static_for<4>([&](auto i) {
         r[i.value] = tok4(o.b, i) * (bf16_to_f32(o.v[t.value][i.value]) -
                                      tok4(o.g, i) * (xk0[t.value][i.value] + xk1[t.value][i.value]));
+        if constexpr (MASK) r[i.value] = tok4(o.b, i) != 0.0f ? r[i.value] : 0.0f;
       });
       split4_store(r, &Rh[16 * t.value + lr][16 * wave + 4 * lq], &Rl[16 * t.value + lr][16 * wave + 4 * lq]);
     });
@@ -1428,9 +1438,15 @@ int chunk_fwd(const void* q, const void* k, const void* v, int qkv_dtype, int ga
   const int64_t scan_blocks = (kTiles / tpw) * kXcds * unit * ((heads + kXcds * unit - 1) / (kXcds * unit));
   if (!(phases & kPhaseScan)) return GDN_OK;
   const dim3 sgrid(static_cast<unsigned>(scan_blocks));
-  if (tpw == 2) hipLaunchKernelGGL((chunk_scan_kernel<true, 2>), sgrid, dim3(256), 0, st, p);
-  else if (kt_lds) hipLaunchKernelGGL((chunk_scan_kernel<true, 1>), sgrid, dim3(256), 0, st, p);
-  else hipLaunchKernelGGL((chunk_scan_kernel<false, 1>), sgrid, dim3(256), 0, st, p);
+  if (mask != nullptr) {
+    if (tpw == 2) hipLaunchKernelGGL((chunk_scan_kernel<true, 2, true>), sgrid, dim3(256), 0, st, p);
+    else if (kt_lds) hipLaunchKernelGGL((chunk_scan_kernel<true, 1, true>), sgrid, dim3(256), 0, st, p);
+    else hipLaunchKernelGGL((chunk_scan_kernel<false, 1, true>), sgrid, dim3(256), 0, st, p);
+  } else {
+    if (tpw == 2) hipLaunchKernelGGL((chunk_scan_kernel<true, 2, false>), sgrid, dim3(256), 0, st, p);
+    else if (kt_lds) hipLaunchKernelGGL((chunk_scan_kernel<true, 1, false>), sgrid, dim3(256), 0, st, p);
+    else hipLaunchKernelGGL((chunk_scan_kernel<false, 1, false>), sgrid, dim3(256), 0, st, p);
+  }
   return gdn_host::check_launch("gdn_chunk_fwd/scan");
 }
 

@@ -519,6 +519,17 @@ __global__ __launch_bounds__(kTileThreads) void recurrent_tile_kernel(const RecP
 // masked token has g = 1, beta = 0 and y = 0.
 constexpr int kVerifyMaxT = 8;
 
+// Bit t set: token t of the row (t < T) is real and not masked, from a wave
+// whose lane l holds the mask byte of token min(l, T - 1).  The verify
+// kernels store a masked token's k, q and v as zeros: with g = 1 and
+// beta = 0 alone, a non-finite value there would still reach the other
+// tokens as 0 * inf in the coefficients, where the reference's where()
+// keeps the masked step out entirely.
+__device__ __forceinline__ uint32_t live_tokens(uint8_t lane_mask, int T) {
+  const int lane = threadIdx.x & 63;
+  return static_cast<uint32_t>(__builtin_amdgcn_ballot_w64(lane < T && lane_mask != 0));
+}
+
 // TM: tokens the kernel is built for (4 or kVerifyMaxT), T <= TM at run time.
 template <int DK, int DT, int GF, int TM>
 __global__ __launch_bounds__(kTileThreads) void verify_wy_kernel(const RecParams p) {
@@ -570,19 +581,28 @@ __global__ __launch_bounds__(kTileThreads) void verify_wy_kernel(const RecParams
   {
     const int64_t tok = c.tok0 + min(tid, T - 1);
     gate_load<GF, DT>(p.ga, tok * p.ga.ld + c.hv, gx, gy);
-    const uint8_t* mp = p.mask != nullptr ? p.mask + tok : &kActive;
+    // the mask byte of token lane (the same token as tid in wave 0, the one
+    // that uses mm), so that every wave can form the live-token bits
+    const int64_t mtok = c.tok0 + min(static_cast<int>(tid & 63), T - 1);
+    const uint8_t* mp = p.mask != nullptr ? p.mask + mtok : &kActive;
     mm = *(gbl_u8*)mp;
   }
+  const uint32_t live = live_tokens(mm, T);
 
   static_for<KV4>([&](auto it) {
     const int i = tid + kTileThreads * it.value;
     if (i < NK4) {
       const int j = i / (DK / 4), e = (i % (DK / 4)) * 4;
-      *reinterpret_cast<f32x4*>(&Ks[j][e]) = IO<DT>::cvt4(kr[it.value]);
-      *reinterpret_cast<f32x4*>(&Qs[j][e]) = IO<DT>::cvt4(qr[it.value]);
+      const bool on = (live >> j) & 1u;
+      const f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
+      *reinterpret_cast<f32x4*>(&Ks[j][e]) = on ? IO<DT>::cvt4(kr[it.value]) : z;
+      *reinterpret_cast<f32x4*>(&Qs[j][e]) = on ? IO<DT>::cvt4(qr[it.value]) : z;
     }
   });
-  if (tid < TM * kTileRows) Vs[tid / kTileRows][tid % kTileRows] = IO<DT>::cvt1(vr);
+  if (tid < TM * kTileRows) {
+    const int j = tid / kTileRows;
+    Vs[j][tid % kTileRows] = (live >> j) & 1u ? IO<DT>::cvt1(vr) : 0.0f;
+  }
   if (tid < TM) {
     const float ea = GF == GF_ANY && p.ga.mode == GDN_GATES_PRE ? 0.0f : exp_fast(al);
     float g, beta;
@@ -785,12 +805,17 @@ __global__ __launch_bounds__(256) void verify_mfma_kernel(const RecParams p) {
   {
     const int64_t tok = tok0 + min(tid, T - 1);
     gate_load<GF, DT>(p.ga, tok * p.ga.ld + hv, gx, gy);
-    const uint8_t* mp = p.mask != nullptr ? p.mask + tok : &kActive;
+    // the mask byte of token lane (the same token as tid in wave 0, whose
+    // first TM threads use mm), so that every wave can form the live bits
+    const int64_t mtok = tok0 + min(static_cast<int>(tid & 63), T - 1);
+    const uint8_t* mp = p.mask != nullptr ? p.mask + mtok : &kActive;
     mm = *(gbl_u8*)mp;
   }
+  const uint32_t live = live_tokens(mm, T);
 
   {
-    const bool keep = kq_m < 2 * TM && kq_t < T;  // zero rows past the k and q rows
+    // zero rows past the k and q rows, and a masked token's rows
+    const bool keep = kq_m < 2 * TM && kq_t < T && ((live >> kq_t) & 1u);
     *reinterpret_cast<u32x4*>(&KQ[kq_m][kq_e]) =
         u32x4{keep ? kq.x : 0u, keep ? kq.y : 0u, keep ? kq.z : 0u, keep ? kq.w : 0u};
   }
@@ -799,7 +824,7 @@ __global__ __launch_bounds__(256) void verify_mfma_kernel(const RecParams p) {
 #pragma unroll
   for (int j = 0; j < NVS; ++j) {
     const int i = tid + 256 * j;
-    Vs[i / kVmRows][i % kVmRows] = IO<DT>::cvt1(vr[j]);
+    Vs[i / kVmRows][i % kVmRows] = (live >> (i / kVmRows)) & 1u ? IO<DT>::cvt1(vr[j]) : 0.0f;
   }
   {
     // every thread transforms and stores (a use under a branch would have
